@@ -1,0 +1,338 @@
+#!/usr/bin/env python3
+"""Benchmark: the INT4-G32 quantized-linear path on one MI355X.
+
+Step (the headline workload): one batch-1 decoder MLP pass, INT4 group-32 weights --
+RMSNorm(4096, eps 1e-6) -> fused gate||up GEMV K=4096 -> N=2x12288 with the SiLU*mul
+epilogue -> down GEMV K=12288 -> N=4096.  ``value`` is algorithmic HBM bytes per step
+(87,359,488 B: packed codes + bf16 scales + 4-bit zeros + activations in/out) divided by
+the measured time per step, in GB/s.  Inputs are resident in HBM; the steps rotate over
+``--copies`` distinct weight copies (>= 512 MiB in total) so the 256 MiB Infinity Cache
+cannot serve them, and are replayed from one HIP graph.
+
+The JSON line also carries:
+  roofline      the dominant kernel (fused gate||up GEMV) timed alone with HIP events on its
+                launch stream: achieved GB/s on its algorithmic bytes vs the 8 TB/s HBM peak;
+                ``traffic`` comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in
+                profiles/ when present
+  cpu_baseline  the oracle's torch-CPU dequant-then-matmul of the same MLP step on this host
+  extra         the K=4096 N=12288 GEMV alone (GB/s, us/call, fraction of peak)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "moss-tts-optimized_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "INT4-G32 GEMV HBM GB/s (% of peak) + 36-layer decode-step ms at bs=1"
+HBM_PEAK_GBS = 8000.0
+HIDDEN, INTER = 4096, 12288
+
+
+def gemv_bytes(k: int, n: int, m: int = 1) -> int:
+    """Algorithmic bytes of one INT4-G32 projection: codes + bf16 scales + 4-bit zeros +
+    bf16 activations in and out."""
+    return n * k // 2 + (k // 32) * n * 2 + (k // 32) * n // 2 + 2 * m * k + 2 * m * n
+
+
+GATEUP_BYTES = gemv_bytes(HIDDEN, 2 * INTER) - 2 * 2 * INTER + 2 * INTER   # output is the SiLU*mul half
+DOWN_BYTES = gemv_bytes(INTER, HIDDEN)
+MLP_BYTES = GATEUP_BYTES + DOWN_BYTES                                      # 87,359,488
+NORM_BYTES = 3 * 2 * HIDDEN                                                # x, weight, y
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _quantized(torch, w4g32, n, k, gen, dev):
+    w = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32).mul_(0.02)
+    pw = w4g32.quantize_minmax(w)
+    del w
+    return pw
+
+
+def _time_graph(torch, graph, replays: int) -> float:
+    """Seconds per replay, HIP events on the capture/replay stream."""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / replays
+
+
+def _capture(torch, fn):
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def _traffic():
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data.get("gateup_silu_k4096_n24576", {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(torch, budget_s: float):
+    """The oracle's torch-CPU dequant+matmul of one MLP step (dequantizing every call)."""
+    from oracle import pointwise as op
+    from oracle import w4g32 as ow
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(7)
+
+    def rand_gptq(n, k):
+        qweight = torch.randint(-2**31, 2**31 - 1, (k // 8, n), generator=g, dtype=torch.int32)
+        scales = (torch.rand((k // 32, n), generator=g) * 0.005 + 0.001).bfloat16()
+        qzeros = torch.randint(-2**31, 2**31 - 1, (k // 32, n // 8), generator=g, dtype=torch.int32)
+        return qweight, scales, qzeros
+
+    gu = rand_gptq(2 * INTER, HIDDEN)
+    dn = rand_gptq(HIDDEN, INTER)
+    h = torch.randn((1, HIDDEN), generator=g).bfloat16()
+    nw = (1 + torch.randn(HIDDEN, generator=g) * 0.01).bfloat16()
+
+    def step():
+        x = op.rmsnorm(h, nw, 1e-6)
+        y = ow.gptq_dequant_linear_cpu(x, *gu)
+        a = ow.silu_mul_rounded(y[:, :INTER], y[:, INTER:])
+        return ow.gptq_dequant_linear_cpu(a, *dn).bfloat16()
+
+    t0 = time.perf_counter()
+    step()
+    first = time.perf_counter() - t0
+    warm = 1 if first > budget_s / 6 else 3
+    for _ in range(warm - 1):
+        step()
+    reps = max(3, min(10, int(budget_s / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(MLP_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full MLP steps (RMSNorm + gate||up K=4096 N=24576 + SiLU*mul + down K=12288 "
+                      f"N=4096), dequantizing every call; median {med * 1e3:.1f} ms/step after {warm} warm-up",
+            "ms_per_step": round(med * 1e3, 3)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=800)
+    ap.add_argument("--warmup", type=int, default=80)
+    ap.add_argument("--copies", type=int, default=8, help="distinct MLP weight copies rotated over")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="eager launches only (for rocprofv3 --pmc): a 512 MiB copy of known size, then "
+                         "one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures the single-GPU path only: every box in this build has one MI355X, "
+              "and the INT4-G32 decode path runs on one GPU (sharding is described, not run). "
+              "Use --gpus 1.", file=sys.stderr)
+        return 2
+    if args.steps <= 0 or args.warmup < 0 or args.copies <= 0:
+        print("steps must be positive, warmup non-negative", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from moss_tts._runtime import native, pointwise, w4g32
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    arch = native.device_arch(0)
+    _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); building {args.copies} weight copies")
+
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    copies = []
+    for c in range(args.copies):
+        copies.append((_quantized(torch, w4g32, 2 * INTER, HIDDEN, gen, dev),
+                       _quantized(torch, w4g32, HIDDEN, INTER, gen, dev)))
+    h = torch.randn((1, HIDDEN), generator=gen, device=dev).bfloat16()
+    norm_w = (1 + 0.01 * torch.randn(HIDDEN, generator=gen, device=dev)).bfloat16()
+    resident = sum(gu.nbytes + dn.nbytes for gu, dn in copies)
+    _log(f"[bench] {resident / 2**20:.0f} MiB of packed MLP weights resident")
+
+    if args.pmc_pass:
+        src = torch.empty(512 * 2**20 // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        xs = pointwise.rmsnorm(h, norm_w, 1e-6)
+        for gu, _ in copies:
+            w4g32.gateup_silu(xs, gu)
+        torch.cuda.synchronize()
+        for gu, _ in copies:
+            w4g32.gemv(xs, gu.rows(0, INTER))
+        torch.cuda.synchronize()
+        _log(f"[bench] pmc pass done: copy {src.numel() * 4} B; {len(copies)} gate||up launches "
+             f"({GATEUP_BYTES} algorithmic B each); {len(copies)} GEMV K=4096 N=12288 launches "
+             f"({gemv_bytes(HIDDEN, INTER)} B each)")
+        return 0
+
+    def steps(count: int, offset: int = 0, dequant: int = w4g32.EXACT):
+        def run():
+            for i in range(count):
+                gu, dn = copies[(offset + i) % len(copies)]
+                x = pointwise.rmsnorm(h, norm_w, 1e-6)
+                a = w4g32.gateup_silu(x, gu, dequant=dequant)
+                w4g32.gemv(a, dn, dequant=dequant)
+        return run
+
+    cycle = len(copies)
+    g_cycle = _capture(torch, steps(cycle))
+    rem = args.steps % cycle
+    g_rem = _capture(torch, steps(rem)) if rem else None
+
+    for _ in range(max(1, -(-args.warmup // cycle))):
+        g_cycle.replay()
+    torch.cuda.synchronize()
+    _log(f"[bench] warm-up done; timing {args.steps} steps")
+
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps // cycle):
+        g_cycle.replay()
+    if g_rem is not None:
+        g_rem.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    sec = start.elapsed_time(end) / 1e3
+    ms_per_step = sec / args.steps * 1e3
+    value = MLP_BYTES / (sec / args.steps) / 1e9
+    _log(f"[bench] {ms_per_step * 1e3:.2f} us/step ({value:.0f} GB/s), wall {wall:.3f}s")
+
+    # the unrounded-dequant MLP step, reported beside the default (exact) one
+    g_unr = _capture(torch, steps(cycle, dequant=w4g32.UNROUNDED))
+    g_unr.replay()
+    unr_s = _time_graph(torch, g_unr, max(1, args.steps // cycle)) / cycle
+
+    # dominant kernel alone: fused gate||up GEMV over the rotating copies
+    xs = pointwise.rmsnorm(h, norm_w, 1e-6)
+
+    def per_launch(fn, launches):
+        graph = _capture(torch, fn)
+        return _time_graph(torch, graph, 50) / launches
+
+    gu_s = per_launch(lambda: [w4g32.gateup_silu(xs, gu) for gu, _ in copies], len(copies))
+    gu_gbs = GATEUP_BYTES / gu_s / 1e9
+    gu_unr_s = per_launch(lambda: [w4g32.gateup_silu(xs, gu, dequant=w4g32.UNROUNDED) for gu, _ in copies],
+                          len(copies))
+    _log(f"[bench] gate||up GEMV: {gu_s * 1e6:.2f} us/launch, {gu_gbs:.0f} GB/s "
+         f"(unrounded {gu_unr_s * 1e6:.2f} us)")
+
+    # the K=4096, N=12288 GEMV alone, over >= 512 MiB of distinct weights
+    gemv_copies = [gu.rows(0, INTER) for gu, _ in copies] + [gu.rows(INTER, 2 * INTER) for gu, _ in copies]
+    ns_s = per_launch(lambda: [w4g32.gemv(xs, w) for w in gemv_copies], len(gemv_copies))
+    ns_unr_s = per_launch(lambda: [w4g32.gemv(xs, w, dequant=w4g32.UNROUNDED) for w in gemv_copies],
+                          len(gemv_copies))
+    ns_bytes = gemv_bytes(HIDDEN, INTER)
+    ns_gbs = ns_bytes / ns_s / 1e9
+    a = w4g32.gateup_silu(xs, copies[0][0])
+    dn_s = per_launch(lambda: [w4g32.gemv(a, dn) for _, dn in copies], len(copies))
+    _log(f"[bench] GEMV K=4096 N=12288: {ns_s * 1e6:.2f} us, {ns_gbs:.0f} GB/s (unrounded {ns_unr_s * 1e6:.2f} us); "
+         f"down K=12288 N=4096: {dn_s * 1e6:.2f} us, {DOWN_BYTES / dn_s / 1e9:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("[bench] CPU baseline (oracle, torch CPU) ...")
+        cpu = cpu_baseline(torch, args.cpu_budget)
+        _log(f"[bench] CPU baseline: {cpu['ms_per_step']} ms/step on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decoder MLP, batch 1, INT4-G32 weights: RMSNorm(4096) + gate||up GEMV K=4096 "
+                        "N=2x12288 with SiLU*mul epilogue + down GEMV K=12288 N=4096",
+            "bytes_per_step": MLP_BYTES + NORM_BYTES,
+            "algorithmic_bytes_counted": MLP_BYTES,
+            "weight_copies": len(copies),
+            "resident_weight_mib": round(resident / 2**20, 1),
+            "weights": "N(0,0.02) fp32, min-max quantized per 32-input group on the GPU (seeded)",
+            "activations": "bf16 N(0,1) through RMSNorm with weight 1+N(0,0.01)",
+            "timing": "one HIP graph of weight-copy-rotating steps, HIP events on its stream",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "w4g32_gemv_kernel<KG=2,R=2,PAIRED> (fused gate||up + SiLU*mul)",
+            "bound": "hbm",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": _traffic(),
+            "algorithmic_bytes_per_launch": GATEUP_BYTES,
+            "us_per_launch": round(gu_s * 1e6, 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": {
+            "gemv_k4096_n12288": {"us_per_call": round(ns_s * 1e6, 3), "GB/s": round(ns_gbs, 1),
+                                  "frac_of_peak": round(ns_gbs / HBM_PEAK_GBS, 4), "bytes": ns_bytes,
+                                  "dequant": "exact"},
+            "gemv_k4096_n12288_unrounded": {"us_per_call": round(ns_unr_s * 1e6, 3),
+                                            "GB/s": round(ns_bytes / ns_unr_s / 1e9, 1),
+                                            "frac_of_peak": round(ns_bytes / ns_unr_s / 1e9 / HBM_PEAK_GBS, 4)},
+            "gateup_unrounded": {"us_per_call": round(gu_unr_s * 1e6, 3),
+                                 "GB/s": round(GATEUP_BYTES / gu_unr_s / 1e9, 1)},
+            "mlp_step_unrounded": {"us_per_step": round(unr_s * 1e6, 3), "GB/s": round(MLP_BYTES / unr_s / 1e9, 1)},
+            "gemv_down_k12288_n4096": {"us_per_call": round(dn_s * 1e6, 3),
+                                       "GB/s": round(DOWN_BYTES / dn_s / 1e9, 1)},
+            "wall_s_timed_region": round(wall, 4),
+        },
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,109 @@
+/*
+ * libmoss_hip.so -- C-ABI of the MI355X (gfx950) INT4-G32 quantized-linear path.
+ *
+ * Conventions (mirroring the reference's native launch convention,
+ * src/moss_tts/_runtime/attention_native.cu:91-97 and attention_native.py:26-44):
+ *   - every pointer is a device pointer owned by the caller; nothing is allocated inside;
+ *   - bf16 tensors are passed as raw 16-bit patterns, row-major and contiguous;
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream); launches are
+ *     asynchronous on it and graph-capturable (no host sync, no allocation);
+ *   - the return value is a hipError_t (0 = success); argument errors return
+ *     hipErrorInvalidValue (1) before anything is launched.
+ *
+ * Row-packed INT4-G32 weight ("rowpack", per output row n, G = K/32 groups):
+ *   qw  uint32 [N, K/8]  group g = words 4g..4g+3; word j covers k = 32g+8j+t, the code of
+ *                        t = 2i at bits [4i,4i+4), of t = 2i+1 at bits [16+4i,20+4i)
+ *   sc  bf16   [N, G]
+ *   zp  uint8  [N, G/2]  byte b = z[b] | z[b+G/2] << 4
+ *   w[n,k] = bf16_rne(float(q - z) * float(s))
+ */
+#ifndef MOSS_HIP_H
+#define MOSS_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- library */
+int moss_abi_version(void);
+const char *moss_error_string(int code);
+/* 0 if the current device is gfx950; writes its gcnArchName into arch_out.
+ * Replaces the SM90 capability check of src/moss_tts/api.py:79-80. */
+int moss_check_device(char *arch_out, int arch_len);
+
+/* ------------------------------------------------------- INT4-G32 weights */
+/* AutoGPTQ-style qweight int32 [K/8,N], scales bf16 [K/32,N], qzeros int32 [K/32,N/8]
+ * (zero points stored literally) -> rowpack.  Replaces the install-time repack of
+ * src/moss_tts/_runtime/dp4a_packing.py:128-160 (pack_interleaved :15-19). */
+int moss_w4g32_repack_gptq(const void *qweight, const void *scales, const void *qzeros, void *qw, void *sc,
+                           void *zp, int K, int N, void *stream);
+
+/* The reference's calibrated export (packed u8 [N,K/2], two's-complement nibbles, byte j =
+ * codes 2j | 2j+1 << 4) -> rowpack codes q = u ^ 8 and zeros z = 8 (the caller copies the
+ * bf16-exact scales).  Replaces install_calibrated's buffers,
+ * src/moss_tts/_runtime/calibrated_backend.py:30-56 (format: src/moss_tts/calibration.py:190-203). */
+int moss_w4g32_import_signed(const void *packed, void *qw, void *zp, int K, int N, void *stream);
+
+/* rowpack -> unsigned codes u8 [N,K].  Counterpart of unpack_signed,
+ * src/moss_tts/_runtime/calibrated_backend.py:8-13. */
+int moss_w4g32_unpack_codes(const void *qw, void *codes, int K, int N, void *stream);
+
+/* rowpack -> bf16 [N,K], bit-exact dequant.  Counterpart of dequantize,
+ * src/moss_tts/_runtime/calibrated_quant.py:41-42. */
+int moss_w4g32_dequant_bf16(const void *qw, const void *sc, const void *zp, void *w, int K, int N, void *stream);
+
+/* fp32 [N,K] -> rowpack with the asymmetric min-max RTN quantizer per (row, 32-group).
+ * The synthetic-weight recipe; role of static_scales + quantization,
+ * src/moss_tts/_runtime/calibrated_quant.py:36-38. */
+int moss_w4g32_quantize_minmax(const void *w, void *qw, void *sc, void *zp, int K, int N, void *stream);
+
+/* ------------------------------------------------------------ decode GEMV */
+/* dequant_mode of the decode GEMVs:
+ *   MOSS_DEQUANT_EXACT (0)      every weight is the bit-exact bf16 dequant bf16_rne((q-z)*s)
+ *                               (calibrated_quant.py:41-42) before it multiplies x; the
+ *                               result is an fp32 dot of exactly the reference's dequantized
+ *                               weights (default);
+ *   MOSS_DEQUANT_UNROUNDED (1)  sum_g s * sum (q-z) x without the per-weight bf16 rounding
+ *                               (about half the VALU work; error vs. the exact form bounded
+ *                               by 2^-9 * sum |w x|). */
+#define MOSS_DEQUANT_EXACT 0
+#define MOSS_DEQUANT_UNROUNDED 1
+
+/* y bf16 [N] = x bf16 [K] . dequant(W)^T, M must be 1, K % 64 == 0, K <= 16384.
+ * rows_per_wave in {0 (auto), 1, 2, 4}.  Replaces the W4A8 projection
+ * linear() of src/moss_tts/_runtime/dp4a_scaled.py:81-95 (and int4_dp4a.py:335-353). */
+int moss_w4g32_gemv(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
+                    int rows_per_wave, int dequant_mode, void *stream);
+
+/* Fused gate||up GEMV + SiLU*mul: W has 2*N_half rows (gate rows first, up rows second,
+ * src/moss_tts/_runtime/llm.py:144); y bf16 [N_half] = bf16(bf16(silu(bf16(g))) * bf16(u)).
+ * Replaces linear(..., paired=True) of src/moss_tts/_runtime/dp4a_scaled.py:64-68,81-95. */
+int moss_w4g32_gateup_silu(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K,
+                           int N_half, int rows_per_wave, int dequant_mode, void *stream);
+
+/* --------------------------------------------------- norms, RoPE, SiLU*mul */
+/* Row RMSNorm over n (n % 8 == 0, n <= 8192), bf16 in/out, rounding points of Qwen3RMSNorm.
+ * res == NULL: y = rmsnorm(x) (src/moss_tts/_runtime/kernels.py:50-66).
+ * res != NULL: sum_out = bf16(x + res); y = rmsnorm(sum_out) (kernels.py:69-90). */
+int moss_rmsnorm(const void *x, const void *res, const void *w, void *sum_out, void *y, int rows, int n, float eps,
+                 void *stream);
+
+/* Qwen3-8B q/k head RMSNorm + RoPE + KV-cache write for ntok tokens.
+ * qkv bf16 [ntok, 6144] (q 32x128 | k 8x128 | v 8x128), q/k norm weights bf16 [128],
+ * cos/sin bf16 [ntok, 128], positions int64 [ntok] (unique, in [0, L)), q_out bf16
+ * [ntok, 32, 128], caches bf16 [8, L, 128] written at rows positions[t].
+ * Replaces _qk_rope_cache (src/moss_tts/_runtime/kernels.py:142-170) and _prefill_qkv
+ * (src/moss_tts/_runtime/prefill_qkv.py:7-28, project :61-83). */
+int moss_qk_norm_rope_kv(const void *qkv, const void *q_weight, const void *k_weight, const void *cos,
+                         const void *sin, void *q_out, void *k_cache, void *v_cache, const void *positions, int L,
+                         int ntok, float eps, void *stream);
+
+/* x bf16 [rows, 2n] = (gate | up) halves of width n (n even) -> y bf16 [rows, n],
+ * y = bf16(bf16(silu(g)) * u).  Replaces _silu mode 0 of
+ * src/moss_tts/_runtime/prefill_pointwise.py:18-31 and _silu_mul, kernels.py:123-139. */
+int moss_silu_mul(const void *x, void *y, int rows, int n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOSS_HIP_H */

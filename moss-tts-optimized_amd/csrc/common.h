@@ -1,0 +1,104 @@
+// Shared device helpers for the gfx950 kernels behind libmoss_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MOSS_API extern "C" __attribute__((visibility("default")))
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Dequant modes of the decode GEMVs (see include/moss_hip.h).
+#define MOSS_DEQUANT_EXACT 0
+#define MOSS_DEQUANT_UNROUNDED 1
+
+namespace moss {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 bit helpers
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_bits(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// float -> bf16 bits, round to nearest even; NaN -> quiet NaN with the sign kept.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Round a float through bf16 and back (the "x.to(bf16).to(f32)" step).
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------- cross-lane sums
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x141>(v);  // row_half_mirror: lane i <- lane 7-i within 8
+    v += dpp_move<0x140>(v);  // row_mirror: lane i <- lane 15-i within 16
+    return v;
+}
+
+// Full 64-lane sum, wave-uniform result.  Fixed order, so results are deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Exact bf16 dequant of one code pair: d = (128+qa | 128+qb) in bf16, s_lo = (s | 0),
+// s_hi = (0 | s), bias = -(128+z) s (exact in fp32).  Each v_dot2_f32_bf16 then yields the
+// exact fp32 (q - z) s (every addend's bits lie inside the adder's window) and
+// v_cvt_pk_bf16_f32 rounds the pair to nearest even.  The block is one asm statement
+// because a v_dot2 result is not interlocked on gfx950: a non-dot VALU may read it only
+// after 3 wait states (the s_nop 2), which the compiler cannot see inside inline asm.
+__device__ __forceinline__ uint32_t dequant_pair_exact(uint32_t d, uint32_t s_lo, uint32_t s_hi, float bias) {
+    uint32_t w;
+    float t;
+    asm("v_dot2_f32_bf16 %0, %2, %3, %5\n\t"
+        "v_dot2_f32_bf16 %1, %2, %4, %5\n\t"
+        "s_nop 2\n\t"
+        "v_cvt_pk_bf16_f32 %0, %0, %1"
+        : "=&v"(w), "=&v"(t)
+        : "v"(d), "v"(s_lo), "v"(s_hi), "v"(bias));
+    return w;
+}
+
+}  // namespace moss
+
+// ---------------------------------------------------------------- host-side plumbing
+#define MOSS_CHECK_ARG(cond)                                   \
+    do {                                                       \
+        if (!(cond)) return (int)hipErrorInvalidValue;         \
+    } while (0)
+
+#define MOSS_ALIGNED(p, a) ((((uintptr_t)(p)) % (a)) == 0)
+
+static inline int moss_launch_status() { return (int)hipGetLastError(); }

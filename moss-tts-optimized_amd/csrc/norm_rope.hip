@@ -1,0 +1,198 @@
+// RMSNorm / add-RMSNorm, q/k head-norm + RoPE + KV-cache write, and the standalone SiLU*mul.
+//
+// Rounding points follow the reference kernels:
+//   rmsnorm       y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)        src/moss_tts/_runtime/kernels.py:50-59
+//   add_rmsnorm   s = bf16(x + r); y = rmsnorm(s)                        src/moss_tts/_runtime/kernels.py:69-82
+//   qk-norm+RoPE  xn = bf16(bf16(x*r) * w[d]); out = bf16(bf16(xn*cos) + bf16(+-xs*sin))
+//                 with xs the value at (d+64)%128 and float negation for d < 64
+//                 src/moss_tts/_runtime/kernels.py:142-170, prefill_qkv.py:7-28
+//   silu_mul      y = bf16(bf16(g / (1 + exp(-g))) * u)                  src/moss_tts/_runtime/prefill_pointwise.py:18-31
+#include "common.h"
+
+namespace moss {
+namespace {
+
+constexpr int kNormThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) lds[w] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / kWave; ++i) s += lds[i];
+    return s;
+}
+
+// One workgroup per row; each thread owns 8-value chunks c = tid, tid + 256, ...
+// (n % 8 == 0, n <= 8 * 256 * kMaxChunks).
+constexpr int kMaxChunks = 4;
+
+template <bool RESIDUAL>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ res,
+                                                             const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ sum_out,
+                                                             uint16_t* __restrict__ y, int n, float eps) {
+    __shared__ float lds[kNormThreads / kWave];
+    const size_t row = blockIdx.x;
+    const int chunks = n / 8;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * n);
+    const uint4* rr = reinterpret_cast<const uint4*>(res + row * n);
+    float v[kMaxChunks][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        const int ci = threadIdx.x + c * kNormThreads;
+        if (ci < chunks) {
+            const uint4 a = xr[ci];
+            const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+            uint32_t sw[4];
+            if constexpr (RESIDUAL) {
+                const uint4 b = rr[ci];
+                const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const uint32_t lo = f32_to_bf16(bf16_lo(aw[p]) + bf16_lo(bw[p]));
+                    const uint32_t hi = f32_to_bf16(bf16_hi(aw[p]) + bf16_hi(bw[p]));
+                    sw[p] = lo | (hi << 16);
+                }
+                reinterpret_cast<uint4*>(sum_out + row * n)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+            } else {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) sw[p] = aw[p];
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                v[c][2 * p] = bf16_lo(sw[p]);
+                v[c][2 * p + 1] = bf16_hi(sw[p]);
+                ss = fmaf(v[c][2 * p], v[c][2 * p], ss);
+                ss = fmaf(v[c][2 * p + 1], v[c][2 * p + 1], ss);
+            }
+        }
+    }
+    const float inv = rsqrtf(block_sum(ss, lds) / (float)n + eps);
+    const uint4* wr = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        const int ci = threadIdx.x + c * kNormThreads;
+        if (ci < chunks) {
+            const uint4 ww = wr[ci];
+            const uint32_t wv[4] = {ww.x, ww.y, ww.z, ww.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
+                const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
+                o[p] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+            }
+            reinterpret_cast<uint4*>(y + row * n)[ci] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
+// One wave per (token, head); lane l owns dims l and l + 64, which are each other's RoPE
+// partners, so only the sum of squares crosses lanes.  Heads 0..31 are queries, 32..39 keys.
+__global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restrict__ qkv,
+                                                       const uint16_t* __restrict__ qw,
+                                                       const uint16_t* __restrict__ kw,
+                                                       const uint16_t* __restrict__ cos_t,
+                                                       const uint16_t* __restrict__ sin_t,
+                                                       uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+                                                       uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
+                                                       int L, int ntok, float eps) {
+    constexpr int QH = 32, KH = 8, D = 128, ROW = (QH + 2 * KH) * D;  // 6144
+    const int wave = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (wave >= ntok * (QH + KH)) return;
+    const int t = wave / (QH + KH), h = wave % (QH + KH);
+    const int l = threadIdx.x & (kWave - 1);
+    const bool is_q = h < QH;
+    const size_t base = (size_t)t * ROW + (is_q ? h * D : QH * D + (h - QH) * D);
+    const uint16_t* wt = is_q ? qw : kw;
+    const float a = bf16_bits(qkv[base + l]);       // dim l
+    const float b = bf16_bits(qkv[base + l + 64]);  // dim l + 64
+    const float r = rsqrtf(wave_sum(a * a + b * b) / (float)D + eps);
+    const float an = round_bf16(round_bf16(a * r) * bf16_bits(wt[l]));
+    const float bn = round_bf16(round_bf16(b * r) * bf16_bits(wt[l + 64]));
+    const float c0 = bf16_bits(cos_t[(size_t)t * D + l]), c1 = bf16_bits(cos_t[(size_t)t * D + l + 64]);
+    const float s0 = bf16_bits(sin_t[(size_t)t * D + l]), s1 = bf16_bits(sin_t[(size_t)t * D + l + 64]);
+    // d = l < 64: partner is bn, negated;  d = l + 64: partner is an
+    const uint16_t o0 = f32_to_bf16(round_bf16(an * c0) + round_bf16((-bn) * s0));
+    const uint16_t o1 = f32_to_bf16(round_bf16(bn * c1) + round_bf16(an * s1));
+    if (is_q) {
+        uint16_t* dst = q_out + ((size_t)t * QH + h) * D;
+        dst[l] = o0;
+        dst[l + 64] = o1;
+    } else {
+        const int kh = h - QH;
+        const int64_t p = pos[t];
+        uint16_t* kd = kc + ((size_t)kh * L + p) * D;
+        uint16_t* vd = vc + ((size_t)kh * L + p) * D;
+        kd[l] = o0;
+        kd[l + 64] = o1;
+        const size_t vb = (size_t)t * ROW + (QH + KH) * D + kh * D;
+        vd[l] = qkv[vb + l];
+        vd[l + 64] = qkv[vb + l + 64];
+    }
+}
+
+// x [rows, 2n] (gate | up) -> y [rows, n]; n % 2 == 0.
+__global__ __launch_bounds__(256) void silu_mul_rows(const uint32_t* __restrict__ x, uint32_t* __restrict__ y,
+                                                     int n, size_t pairs) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= pairs) return;
+    const size_t half = (size_t)n / 2;
+    const size_t row = i / half, c = i % half;
+    const uint32_t g = x[row * n + c];         // gate pair (row, 2c..2c+1)
+    const uint32_t u = x[row * n + half + c];  // up pair
+    float r[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const float gv = p ? bf16_hi(g) : bf16_lo(g);
+        const float uv = p ? bf16_hi(u) : bf16_lo(u);
+        r[p] = round_bf16(gv / (1.0f + expf(-gv))) * uv;
+    }
+    y[row * half + c] = (uint32_t)f32_to_bf16(r[0]) | ((uint32_t)f32_to_bf16(r[1]) << 16);
+}
+
+}  // namespace
+}  // namespace moss
+
+using namespace moss;
+
+MOSS_API int moss_rmsnorm(const void* x, const void* res, const void* w, void* sum_out, void* y, int rows, int n,
+                          float eps, void* stream) {
+    MOSS_CHECK_ARG(x && w && y && rows > 0 && n > 0 && n % 8 == 0 && n <= 8 * kNormThreads * kMaxChunks);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(w, 16) && MOSS_ALIGNED(y, 16));
+    MOSS_CHECK_ARG(!res || (sum_out && MOSS_ALIGNED(res, 16) && MOSS_ALIGNED(sum_out, 16)));
+    hipStream_t st = (hipStream_t)stream;
+    if (res)
+        hipLaunchKernelGGL(rmsnorm_rows<true>, dim3(rows), dim3(kNormThreads), 0, st, (const uint16_t*)x,
+                           (const uint16_t*)res, (const uint16_t*)w, (uint16_t*)sum_out, (uint16_t*)y, n, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_rows<false>, dim3(rows), dim3(kNormThreads), 0, st, (const uint16_t*)x,
+                           (const uint16_t*)nullptr, (const uint16_t*)w, (uint16_t*)nullptr, (uint16_t*)y, n, eps);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_qk_norm_rope_kv(const void* qkv, const void* q_weight, const void* k_weight, const void* cos,
+                                  const void* sin, void* q_out, void* k_cache, void* v_cache, const void* positions,
+                                  int L, int ntok, float eps, void* stream) {
+    MOSS_CHECK_ARG(qkv && q_weight && k_weight && cos && sin && q_out && k_cache && v_cache && positions);
+    MOSS_CHECK_ARG(L > 0 && ntok > 0);
+    const int waves = ntok * 40;
+    hipLaunchKernelGGL(qk_norm_rope_kv, dim3((waves + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)qkv, (const uint16_t*)q_weight, (const uint16_t*)k_weight,
+                       (const uint16_t*)cos, (const uint16_t*)sin, (uint16_t*)q_out, (uint16_t*)k_cache,
+                       (uint16_t*)v_cache, (const int64_t*)positions, L, ntok, eps);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_silu_mul(const void* x, void* y, int rows, int n, void* stream) {
+    MOSS_CHECK_ARG(x && y && rows > 0 && n > 0 && n % 2 == 0 && MOSS_ALIGNED(x, 4) && MOSS_ALIGNED(y, 4));
+    const size_t pairs = (size_t)rows * (n / 2);
+    hipLaunchKernelGGL(silu_mul_rows, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint32_t*)x, (uint32_t*)y, n, pairs);
+    return moss_launch_status();
+}

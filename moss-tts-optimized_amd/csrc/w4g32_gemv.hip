@@ -1,0 +1,290 @@
+// Batch-1 INT4 group-32 GEMV (W4A16) and the fused gate||up SiLU*mul variant.
+//
+// y[n] = sum_g s[n,g] * sum_{k in g} (q[n,k] - z[n,g]) * x[k]     (fp32 accumulate, bf16 out)
+//
+// Mapping (gfx950, wave64): one wave owns R output rows; its 64 lanes split K, lane l
+// owning groups l, l+64, l+128, ... (16 bytes of codes per group, so each global_load_dwordx4
+// of a wave reads 1 KiB contiguous).  The lane's slice of x stays in VGPRs for all R rows.
+// Codes become bf16 lanes with one and-or: (w >> 4i) & 0x000F000F | 0x43004300 is the pair
+// (128 + q_2i, 128 + q_2i+1), exact in bf16, fed to v_dot2_f32_bf16 against the matching
+// x pair.  Per group: sum (q - z) x = acc - (128 + z) * sum_g x, then * s.  Rows are reduced
+// with DPP (no LDS, no atomics, no workspace): every output element is written once.
+//
+// Reference semantics: dequant-then-matmul of src/moss_tts/calibration.py:185-188 with
+// src/moss_tts/_runtime/calibrated_quant.py:41-42; paired epilogue rounding points of
+// src/moss_tts/_runtime/dp4a_scaled.py:65-68 (gate, up, SiLU and product rounded to bf16).
+#include "common.h"
+
+namespace moss {
+namespace {
+
+template <int KG>
+struct XSlice {
+    uint32_t v[KG][16];  // 32 bf16 of group (lane + 64 j), as 16 packed pairs
+    float sum[KG];       // fp32 sum of those 32 values
+};
+
+template <int KG, bool SUMS>
+__device__ __forceinline__ void load_x(XSlice<KG>& xs, const uint16_t* __restrict__ x, int lane, int G) {
+    uint32_t ones = 0x3F803F80u;  // bf16 pair (1.0, 1.0): group sums through the same dot2 path
+    asm volatile("" : "+v"(ones));
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        const int g = lane + kWave * j;
+        float s = 0.f;
+        if (g < G) {
+            const uint4* p = reinterpret_cast<const uint4*>(x + 32 * g);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint4 t = p[c];
+                xs.v[j][4 * c + 0] = t.x;
+                xs.v[j][4 * c + 1] = t.y;
+                xs.v[j][4 * c + 2] = t.z;
+                xs.v[j][4 * c + 3] = t.w;
+            }
+            if constexpr (SUMS) {
+#pragma unroll
+                for (int m = 0; m < 16; ++m) s = dot2_bf16(xs.v[j][m], ones, s);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 16; ++m) xs.v[j][m] = 0u;
+        }
+        xs.sum[j] = s;
+    }
+}
+
+template <int KG>
+struct RowLoad {
+    uint4 w[KG];
+    uint32_t s[KG];  // bf16 scale bits
+    uint32_t z[KG];  // zero point
+};
+
+// FULL: G == 64 * KG with KG even, so lane l's zero for group l + 64 j (j < KG/2) is the low
+// nibble of byte l + 64 j and the zero for group l + 64 (j + KG/2) its high nibble.
+template <int KG, bool FULL>
+__device__ __forceinline__ void load_row(RowLoad<KG>& r, const uint4* __restrict__ qw,
+                                         const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                         int n, int lane, int G) {
+    const int h = G >> 1;
+    if constexpr (FULL) {
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            r.w[j] = qw[(size_t)n * G + lane + kWave * j];
+            r.s[j] = sc[(size_t)n * G + lane + kWave * j];
+        }
+#pragma unroll
+        for (int j = 0; j < KG / 2; ++j) {
+            const uint32_t b = zp[(size_t)n * h + lane + kWave * j];
+            r.z[j] = b & 15u;
+            r.z[j + KG / 2] = b >> 4;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const int g = lane + kWave * j;
+            if (g < G) {
+                r.w[j] = qw[(size_t)n * G + g];
+                r.s[j] = sc[(size_t)n * G + g];
+                const uint32_t b = zp[(size_t)n * h + (g < h ? g : g - h)];
+                r.z[j] = g < h ? (b & 15u) : (b >> 4);
+            } else {
+                r.w[j] = make_uint4(0u, 0u, 0u, 0u);
+                r.s[j] = 0u;
+                r.z[j] = 0u;
+            }
+        }
+    }
+}
+
+// Constants pinned in VGPRs so each code pair costs one v_and_or_b32 (a VOP3 form, which
+// on gfx9 takes no literal operand) after its shift.
+struct Magic {
+    uint32_t mask, bias;
+};
+
+__device__ __forceinline__ Magic make_magic() {
+    Magic m{0x000F000Fu, 0x43004300u};
+    asm volatile("" : "+v"(m.mask), "+v"(m.bias));
+    return m;
+}
+
+__device__ __forceinline__ float word_dot(uint32_t w, const uint32_t* xv, float acc, Magic m) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = dot2_bf16(((w >> (4 * i)) & m.mask) | m.bias, xv[i], acc);
+    return acc;
+}
+
+// Unrounded form: sum_g s * (sum (128+q) x - (128+z) sum x); weights are never rounded.
+template <int KG>
+__device__ __forceinline__ float row_partial_unrounded(const XSlice<KG>& xs, const RowLoad<KG>& r, Magic m) {
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        float acc = 0.f;
+        acc = word_dot(r.w[j].x, &xs.v[j][0], acc, m);
+        acc = word_dot(r.w[j].y, &xs.v[j][4], acc, m);
+        acc = word_dot(r.w[j].z, &xs.v[j][8], acc, m);
+        acc = word_dot(r.w[j].w, &xs.v[j][12], acc, m);
+        const float centred = fmaf(-(128.0f + (float)r.z[j]), xs.sum[j], acc);
+        part = fmaf(bf16_bits((uint16_t)r.s[j]), centred, part);
+    }
+    return part;
+}
+
+// Exact form: every weight is the bit-exact bf16 dequant bf16_rne((q - z) * s) before it
+// meets x (dequant_pair_exact), then a dot2 with the matching x pair accumulates in fp32.
+__device__ __forceinline__ float word_dot_exact(uint32_t w, const uint32_t* xv, float acc, Magic m, uint32_t s_lo,
+                                                uint32_t s_hi, float bias) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = ((w >> (4 * i)) & m.mask) | m.bias;
+        acc = dot2_bf16(dequant_pair_exact(d, s_lo, s_hi, bias), xv[i], acc);
+    }
+    return acc;
+}
+
+template <int KG>
+__device__ __forceinline__ float row_partial_exact(const XSlice<KG>& xs, const RowLoad<KG>& r, Magic m) {
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        const uint32_t s_lo = r.s[j] & 0xffffu;
+        const uint32_t s_hi = s_lo << 16;
+        const float bias = -(128.0f + (float)r.z[j]) * bf16_bits((uint16_t)s_lo);  // exact: 16 bits
+        float acc = 0.f;
+        acc = word_dot_exact(r.w[j].x, &xs.v[j][0], acc, m, s_lo, s_hi, bias);
+        acc = word_dot_exact(r.w[j].y, &xs.v[j][4], acc, m, s_lo, s_hi, bias);
+        acc = word_dot_exact(r.w[j].z, &xs.v[j][8], acc, m, s_lo, s_hi, bias);
+        acc = word_dot_exact(r.w[j].w, &xs.v[j][12], acc, m, s_lo, s_hi, bias);
+        part += acc;
+    }
+    return part;
+}
+
+__device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
+    const float g = round_bf16(gate);
+    const float u = round_bf16(up);
+    const float a = round_bf16(g / (1.0f + expf(-g)));
+    return f32_to_bf16(a * u);
+}
+
+// n_out output rows; PAIRED reads gate row n and up row n + n_out.
+template <int KG, int R, bool PAIRED, bool FULL, bool EXACT>
+__global__ __launch_bounds__(256) void w4g32_gemv_kernel(const uint16_t* __restrict__ x,
+                                                         const uint4* __restrict__ qw,
+                                                         const uint16_t* __restrict__ sc,
+                                                         const uint8_t* __restrict__ zp,
+                                                         uint16_t* __restrict__ y, int G, int n_out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+    const int row0 = wave * R;
+    if (row0 >= n_out) return;  // wave-uniform
+
+    constexpr int NR = PAIRED ? 2 * R : R;
+    RowLoad<KG> rows[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int local = PAIRED ? (r % R) : r;
+        const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
+        load_row<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
+    }
+    XSlice<KG> xs;
+    load_x<KG, !EXACT>(xs, x, lane, G);
+
+    const Magic m = make_magic();
+    float out[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+        out[r] = wave_sum(EXACT ? row_partial_exact(xs, rows[r], m) : row_partial_unrounded(xs, rows[r], m));
+
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            if (n < n_out) y[n] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
+        }
+    }
+}
+
+template <bool PAIRED, int R, bool EXACT>
+int launch_rows(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
+                hipStream_t st) {
+    const int KG = (G + kWave - 1) / kWave;
+    const int waves = (n_out + R - 1) / R;
+    const dim3 grid((waves + 3) / 4), block(256);
+    const auto* xp = (const uint16_t*)x;
+    const auto* qp = (const uint4*)qw;
+    const auto* sp = (const uint16_t*)sc;
+    const auto* zpp = (const uint8_t*)zp;
+    auto* yp = (uint16_t*)y;
+    const bool full = (G == kWave * KG) && (KG % 2 == 0);
+    switch (KG) {
+#define MOSS_KG_CASE(KGV)                                                                                          \
+    case KGV:                                                                                                      \
+        if (full)                                                                                                  \
+            hipLaunchKernelGGL((w4g32_gemv_kernel<KGV, R, PAIRED, (KGV % 2 == 0), EXACT>), grid, block, 0, st, xp, qp, sp, \
+                               zpp, yp, G, n_out);                                                                 \
+        else                                                                                                       \
+            hipLaunchKernelGGL((w4g32_gemv_kernel<KGV, R, PAIRED, false, EXACT>), grid, block, 0, st, xp, qp, sp, zpp, yp, \
+                               G, n_out);                                                                          \
+        break;
+        MOSS_KG_CASE(1)
+        MOSS_KG_CASE(2)
+        MOSS_KG_CASE(3)
+        MOSS_KG_CASE(4)
+        MOSS_KG_CASE(5)
+        MOSS_KG_CASE(6)
+        MOSS_KG_CASE(7)
+        MOSS_KG_CASE(8)
+#undef MOSS_KG_CASE
+        default: return (int)hipErrorInvalidValue;
+    }
+    return moss_launch_status();
+}
+
+template <bool PAIRED, bool EXACT>
+int launch_gemv_mode(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
+                     int rows, hipStream_t st) {
+    switch (rows) {
+        case 1: return launch_rows<PAIRED, 1, EXACT>(x, qw, sc, zp, y, G, n_out, st);
+        case 2: return launch_rows<PAIRED, 2, EXACT>(x, qw, sc, zp, y, G, n_out, st);
+        case 4: return launch_rows<PAIRED, 4, EXACT>(x, qw, sc, zp, y, G, n_out, st);
+        default: return (int)hipErrorInvalidValue;
+    }
+}
+
+template <bool PAIRED>
+int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
+                int rows, int mode, hipStream_t st) {
+    const int G = K / 32;
+    if (rows <= 0) rows = (G <= 128) ? (PAIRED ? 2 : 4) : (G <= 256 ? 2 : 1);
+    if (mode == MOSS_DEQUANT_EXACT) return launch_gemv_mode<PAIRED, true>(x, qw, sc, zp, y, G, n_out, rows, st);
+    if (mode == MOSS_DEQUANT_UNROUNDED) return launch_gemv_mode<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
+    return (int)hipErrorInvalidValue;
+}
+
+}  // namespace
+}  // namespace moss
+
+using namespace moss;
+
+// Largest K the register-resident x slice supports: 8 groups per lane.
+static constexpr int kMaxGemvK = 8 * 64 * 32;
+
+MOSS_API int moss_w4g32_gemv(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
+                             int N, int rows_per_wave, int dequant_mode, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && y);
+    MOSS_CHECK_ARG(M == 1 && K > 0 && N > 0 && K % 64 == 0 && K <= kMaxGemvK);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
+    return launch_gemv<false>(x, qw, sc, zp, y, K, N, rows_per_wave, dequant_mode, (hipStream_t)stream);
+}
+
+MOSS_API int moss_w4g32_gateup_silu(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M,
+                                    int K, int N_half, int rows_per_wave, int dequant_mode, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && y);
+    MOSS_CHECK_ARG(M == 1 && K > 0 && N_half > 0 && K % 64 == 0 && K <= kMaxGemvK);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
+    return launch_gemv<true>(x, qw, sc, zp, y, K, N_half, rows_per_wave, dequant_mode, (hipStream_t)stream);
+}

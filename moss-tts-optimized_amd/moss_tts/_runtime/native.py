@@ -1,0 +1,93 @@
+"""ctypes binding of ``libmoss_hip.so`` (the gfx950 C-ABI declared in ``include/moss_hip.h``).
+
+Mirrors the reference's native convention (``src/moss_tts/_runtime/attention_native.py:11-44``):
+the library is loaded once (``functools.lru_cache``), ``argtypes``/``restype`` are declared,
+and a nonzero ``hipError_t`` raises ``RuntimeError``.  There is no fallback: a missing or
+unloadable library is an error.
+
+``torch`` is imported before the library so that its ``libamdhip64.so.7`` (same SONAME) is
+the HIP runtime the library binds to; streams and pointers are then shared with torch.
+"""
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+
+import torch  # noqa: F401  (must load torch's HIP runtime first)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib", "libmoss_hip.so")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes; every function returns int (hipError_t) unless listed in _RESTYPES.
+SIGNATURES: dict[str, list] = {
+    "moss_abi_version": [],
+    "moss_error_string": [_I],
+    "moss_check_device": [ctypes.c_char_p, _I],
+    "moss_w4g32_repack_gptq": [_P, _P, _P, _P, _P, _P, _I, _I, _P],
+    "moss_w4g32_import_signed": [_P, _P, _P, _I, _I, _P],
+    "moss_w4g32_unpack_codes": [_P, _P, _I, _I, _P],
+    "moss_w4g32_dequant_bf16": [_P, _P, _P, _P, _I, _I, _P],
+    "moss_w4g32_quantize_minmax": [_P, _P, _P, _P, _I, _I, _P],
+    "moss_w4g32_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "moss_w4g32_gateup_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "moss_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "moss_qk_norm_rope_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "moss_silu_mul": [_P, _P, _I, _I, _P],
+}
+_RESTYPES = {"moss_error_string": ctypes.c_char_p}
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+@functools.lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise NativeLibraryMissing(
+            f"{LIB_PATH} is not built; build it with moss_tts._build.build() (hipcc, gfx950)")
+    so = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+    for name, args in SIGNATURES.items():
+        fn = getattr(so, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, _I)
+    return so
+
+
+def error_string(code: int) -> str:
+    s = lib().moss_error_string(int(code))
+    return s.decode() if s else f"hipError {code}"
+
+
+def check(code: int, what: str) -> None:
+    if code:
+        raise RuntimeError(f"{what} failed: {error_string(code)} (hipError {code})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def stream_of(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+@functools.lru_cache(maxsize=None)
+def device_arch(index: int) -> str:
+    """gcnArchName of a device; raises unless it is gfx950."""
+    with torch.cuda.device(index):
+        buf = ctypes.create_string_buffer(64)
+        rc = lib().moss_check_device(buf, 64)
+    arch = buf.value.decode()
+    if rc:
+        raise RuntimeError(f"libmoss_hip.so targets gfx950 (MI350/MI355); device {index} is {arch or 'unknown'}"
+                           f" ({error_string(rc)})")
+    return arch

@@ -1,0 +1,219 @@
+"""INT4 group-32 operators on the gfx950 library: weight formats, dequant, decode GEMV.
+
+Operator conventions follow the reference's projection functions
+(``src/moss_tts/_runtime/dp4a_scaled.py:81-95``, ``dp4a_layout.py:75-84``): caller mistakes
+(dtype, contiguity, device, shapes) raise ``ValueError`` before any launch; outputs are
+allocated with ``torch.empty`` on the input's device; launches go to the current stream and
+are graph-capturable; a failed launch raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import native
+
+GROUP = 32
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _cuda_contig(name: str, t: torch.Tensor, dtype: torch.dtype, device=None) -> None:
+    _require(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _require(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _require(t.is_cuda, f"{name} must be a CUDA (HIP) tensor")
+    _require(t.is_contiguous(), f"{name} must be contiguous")
+    if device is not None:
+        _require(t.device == device, f"{name} must be on {device}, got {t.device}")
+
+
+def _aligned(t: torch.Tensor, a: int) -> bool:
+    return t.data_ptr() % a == 0
+
+
+@dataclass(frozen=True)
+class PackedW4G32:
+    """One INT4-G32 weight in the row-packed layout (see ``include/moss_hip.h``).
+
+    ``qw int32 [N, K/8]``, ``scales bf16 [N, K/32]``, ``zeros uint8 [N, K/64]``.
+    """
+
+    qw: torch.Tensor
+    scales: torch.Tensor
+    zeros: torch.Tensor
+
+    def __post_init__(self):
+        qw, sc, zp = self.qw, self.scales, self.zeros
+        _cuda_contig("qw", qw, torch.int32)
+        _cuda_contig("scales", sc, torch.bfloat16, qw.device)
+        _cuda_contig("zeros", zp, torch.uint8, qw.device)
+        _require(qw.ndim == 2 and sc.ndim == 2 and zp.ndim == 2, "packed tensors must be 2-D")
+        n, k8 = qw.shape
+        k = 8 * k8
+        _require(k % 64 == 0, "K must be a multiple of 64")
+        _require(tuple(sc.shape) == (n, k // GROUP), f"scales must be [{n}, {k // GROUP}], got {tuple(sc.shape)}")
+        _require(tuple(zp.shape) == (n, k // 64), f"zeros must be [{n}, {k // 64}], got {tuple(zp.shape)}")
+        _require(_aligned(qw, 16), "qw must be 16-byte aligned")
+
+    @property
+    def N(self) -> int:
+        return self.qw.shape[0]
+
+    @property
+    def K(self) -> int:
+        return self.qw.shape[1] * 8
+
+    @property
+    def device(self) -> torch.device:
+        return self.qw.device
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.qw, self.scales, self.zeros))
+
+    def rows(self, start: int, stop: int) -> "PackedW4G32":
+        """Row slice (output channels ``[start, stop)``) as a view."""
+        return PackedW4G32(self.qw[start:stop], self.scales[start:stop], self.zeros[start:stop])
+
+    @staticmethod
+    def cat(parts: list["PackedW4G32"]) -> "PackedW4G32":
+        """Concatenate along output rows (the fused q||k||v and gate||up weights)."""
+        return PackedW4G32(torch.cat([p.qw for p in parts]), torch.cat([p.scales for p in parts]),
+                           torch.cat([p.zeros for p in parts]))
+
+    @staticmethod
+    def empty(N: int, K: int, device) -> "PackedW4G32":
+        _require(K % 64 == 0 and K > 0 and N > 0, "K must be a positive multiple of 64")
+        return PackedW4G32(torch.empty((N, K // 8), dtype=torch.int32, device=device),
+                           torch.empty((N, K // GROUP), dtype=torch.bfloat16, device=device),
+                           torch.empty((N, K // 64), dtype=torch.uint8, device=device))
+
+
+# ------------------------------------------------------------------------ formats
+def repack_gptq(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor) -> PackedW4G32:
+    """AutoGPTQ-style ``qweight int32 [K/8,N]``, ``scales bf16 [K/32,N]``, ``qzeros int32
+    [K/32,N/8]`` (zeros stored literally, no act-order) -> :class:`PackedW4G32`."""
+    _cuda_contig("qweight", qweight, torch.int32)
+    dev = qweight.device
+    _cuda_contig("scales", scales, torch.bfloat16, dev)
+    _cuda_contig("qzeros", qzeros, torch.int32, dev)
+    _require(qweight.ndim == 2, "qweight must be [K/8, N]")
+    k8, n = qweight.shape
+    k = 8 * k8
+    _require(k % 64 == 0 and n % 8 == 0, "K must be a multiple of 64 and N of 8")
+    _require(tuple(scales.shape) == (k // GROUP, n), f"scales must be [{k // GROUP}, {n}]")
+    _require(tuple(qzeros.shape) == (k // GROUP, n // 8), f"qzeros must be [{k // GROUP}, {n // 8}]")
+    out = PackedW4G32.empty(n, k, dev)
+    native.call("moss_w4g32_repack_gptq", native.ptr(qweight), native.ptr(scales), native.ptr(qzeros),
+                native.ptr(out.qw), native.ptr(out.scales), native.ptr(out.zeros), k, n, native.stream_of(qweight))
+    return out
+
+
+def import_signed(packed: torch.Tensor, scales: torch.Tensor) -> PackedW4G32:
+    """The reference's export record ``packed u8 [N,K/2]`` + ``scales [N,K/32]`` (bf16, or
+    fp32 that is exactly representable in bf16) -> :class:`PackedW4G32` with ``q = u ^ 8``,
+    ``z = 8`` (``src/moss_tts/calibration.py:190-203``, ``_runtime/calibrated_backend.py:46-51``)."""
+    _cuda_contig("packed", packed, torch.uint8)
+    dev = packed.device
+    _require(scales.is_cuda and scales.device == dev, "scales must be on the packed tensor's device")
+    _require(scales.dtype in (torch.bfloat16, torch.float32), "scales must be bf16 or fp32")
+    _require(packed.ndim == 2, "packed must be [N, K/2]")
+    n, k2 = packed.shape
+    k = 2 * k2
+    _require(k % 64 == 0, "K must be a multiple of 64")
+    _require(tuple(scales.shape) == (n, k // GROUP), f"scales must be [{n}, {k // GROUP}]")
+    sc = scales.to(torch.bfloat16).contiguous()
+    if scales.dtype != torch.bfloat16:
+        # the reference's own exactness rule before narrowing scale storage
+        # (src/moss_tts/_runtime/dp4a_packing.py:149-152, short_scales.py:37-40)
+        _require(torch.equal(sc.float(), scales), "scales are not exactly representable as bf16")
+    _require(_aligned(packed, 4), "packed must be 4-byte aligned")
+    qw = torch.empty((n, k // 8), dtype=torch.int32, device=dev)
+    zp = torch.empty((n, k // 64), dtype=torch.uint8, device=dev)
+    native.call("moss_w4g32_import_signed", native.ptr(packed), native.ptr(qw), native.ptr(zp), k, n,
+                native.stream_of(packed))
+    return PackedW4G32(qw, sc, zp)
+
+
+def quantize_minmax(w: torch.Tensor) -> PackedW4G32:
+    """fp32 ``[N, K]`` -> :class:`PackedW4G32` (asymmetric min-max RTN per (row, 32-group))."""
+    _cuda_contig("w", w, torch.float32)
+    _require(w.ndim == 2 and w.shape[1] % 64 == 0, "w must be [N, K] with K % 64 == 0")
+    _require(_aligned(w, 16), "w must be 16-byte aligned")
+    n, k = w.shape
+    out = PackedW4G32.empty(n, k, w.device)
+    native.call("moss_w4g32_quantize_minmax", native.ptr(w), native.ptr(out.qw), native.ptr(out.scales),
+                native.ptr(out.zeros), k, n, native.stream_of(w))
+    return out
+
+
+def unpack_codes(w: PackedW4G32) -> torch.Tensor:
+    """Unsigned 4-bit codes ``uint8 [N, K]``."""
+    codes = torch.empty((w.N, w.K), dtype=torch.uint8, device=w.device)
+    native.call("moss_w4g32_unpack_codes", native.ptr(w.qw), native.ptr(codes), w.K, w.N, native.stream_of(w.qw))
+    return codes
+
+
+def dequantize(w: PackedW4G32) -> torch.Tensor:
+    """Bit-exact ``bf16 [N, K]``: ``bf16_rne(float(q - z) * float(s))``
+    (``src/moss_tts/_runtime/calibrated_quant.py:41-42``)."""
+    out = torch.empty((w.N, w.K), dtype=torch.bfloat16, device=w.device)
+    native.call("moss_w4g32_dequant_bf16", native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
+                native.ptr(out), w.K, w.N, native.stream_of(w.qw))
+    return out
+
+
+# --------------------------------------------------------------------- projections
+_MAX_GEMV_K = 8 * 64 * 32
+
+
+def _check_row(x: torch.Tensor, w: PackedW4G32) -> None:
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.numel() == w.K, f"one contiguous bf16 row of {w.K} values required, got shape {tuple(x.shape)}")
+    _require(w.K <= _MAX_GEMV_K, f"decode GEMV supports K <= {_MAX_GEMV_K}")
+    _require(_aligned(x, 16), "x must be 16-byte aligned")
+
+
+def _rows_arg(rows_per_wave: int) -> int:
+    _require(rows_per_wave in (0, 1, 2, 4), "rows_per_wave must be 0 (auto), 1, 2 or 4")
+    return rows_per_wave
+
+
+#: every weight is the bit-exact bf16 dequant before it meets x (default)
+EXACT = 0
+#: sum_g s * sum (q - z) x, without rounding each weight to bf16
+UNROUNDED = 1
+
+
+def _mode_arg(dequant: int) -> int:
+    _require(dequant in (EXACT, UNROUNDED), "dequant must be EXACT (0) or UNROUNDED (1)")
+    return dequant
+
+
+def gemv(x: torch.Tensor, w: PackedW4G32, *, rows_per_wave: int = 0, dequant: int = EXACT) -> torch.Tensor:
+    """Batch-1 decode projection: bf16 ``[..., K]`` (one row) -> bf16 ``[..., N]``."""
+    _check_row(x, w)
+    rows = _rows_arg(rows_per_wave)
+    mode = _mode_arg(dequant)
+    y = torch.empty((*x.shape[:-1], w.N), dtype=torch.bfloat16, device=x.device)
+    native.call("moss_w4g32_gemv", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
+                native.ptr(y), 1, w.K, w.N, rows, mode, native.stream_of(x))
+    return y
+
+
+def gateup_silu(x: torch.Tensor, w: PackedW4G32, *, rows_per_wave: int = 0, dequant: int = EXACT) -> torch.Tensor:
+    """Fused gate||up decode projection with the SiLU*mul epilogue: ``[..., K]`` ->
+    ``[..., N/2]`` (gate rows ``[0, N/2)``, up rows ``[N/2, N)``)."""
+    _check_row(x, w)
+    _require(w.N % 2 == 0, "gate||up weight needs an even number of rows")
+    rows = _rows_arg(rows_per_wave)
+    mode = _mode_arg(dequant)
+    half = w.N // 2
+    y = torch.empty((*x.shape[:-1], half), dtype=torch.bfloat16, device=x.device)
+    native.call("moss_w4g32_gateup_silu", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales),
+                native.ptr(w.zeros), native.ptr(y), 1, w.K, half, rows, mode, native.stream_of(x))
+    return y
