@@ -14,7 +14,8 @@
  *   qw  uint32 [N, K/8]  group g = words 4g..4g+3; word j covers k = 32g+8j+t, the code of
  *                        t = 2i at bits [4i,4i+4), of t = 2i+1 at bits [16+4i,20+4i)
  *   sc  bf16   [N, G]
- *   zp  uint8  [N, G/2]  byte b = z[b] | z[b+G/2] << 4
+ *   zp  uint8  [N, G/2]  blocks of 128 groups: for block c (r = min(128, G-128c) groups)
+ *                        byte 64c+b = z[128c+b] | z[128c+r/2+b] << 4
  *   w[n,k] = bf16_rne(float(q - z) * float(s))
  */
 #ifndef MOSS_HIP_H

@@ -31,6 +31,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 // Round a float through bf16 and back (the "x.to(bf16).to(f32)" step).
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits(f32_to_bf16(f)); }
 
+// Zero point of group g in a row-packed zp row (blocks of 128 groups: for block c with
+// r = min(128, G - 128c) groups, byte 64c + b holds z[128c + b] low and z[128c + r/2 + b] high).
+__device__ __forceinline__ uint32_t zero_of_group(const uint8_t* __restrict__ zrow, int g, int G) {
+    const int c0 = g & ~127, r = min(128, G - c0), off = g - c0, hr = r >> 1;
+    return off < hr ? (uint32_t)(zrow[(c0 >> 1) + off] & 15u) : (uint32_t)(zrow[(c0 >> 1) + off - hr] >> 4);
+}
+
 // ---------------------------------------------------------------- cross-lane sums
 template <int CTRL>
 __device__ __forceinline__ float dpp_move(float v) {

@@ -7,8 +7,9 @@
 //                        [16+4i, 20+4i), so one mask+or per pair of codes yields two bf16
 //                        lanes for v_dot2_f32_bf16.
 //   sc  bf16   [N, G]
-//   zp  uint8  [N, G/2]  byte b = z[b] | z[b + G/2] << 4 (lane l of a GEMV wave reads one
-//                        byte for its groups l and l + 64 when G = 128).
+//   zp  uint8  [N, G/2]  blocks of 128 groups: for block c (r = min(128, G - 128c) groups)
+//                        byte 64c + b = z[128c + b] | z[128c + r/2 + b] << 4, so a GEMV lane
+//                        owning groups l and l + 64 of a 128-group slice reads one byte.
 // w[n, k] = bf16_rne(float(q - z) * float(s))  -- src/moss_tts/_runtime/calibrated_quant.py:41-42.
 #include "common.h"
 
@@ -33,9 +34,11 @@ __device__ __forceinline__ uint32_t rowpack_code(uint32_t w, int t) {
     return (t & 1) ? (w >> (16 + 4 * (t >> 1))) & 15u : (w >> (4 * (t >> 1))) & 15u;
 }
 
-__device__ __forceinline__ uint32_t rowpack_zero(const uint8_t* __restrict__ zrow, int g, int G) {
-    const int h = G >> 1;
-    return g < h ? (uint32_t)(zrow[g] & 15u) : (uint32_t)(zrow[g - h] >> 4);
+// (byte index, group of its low nibble, group of its high nibble) for zero byte i of a row
+__device__ __forceinline__ void zero_byte_groups(int i, int G, int& lo, int& hi) {
+    const int c0 = (i >> 6) << 7, r = min(128, G - c0), b = i - (c0 >> 1);
+    lo = c0 + b;
+    hi = c0 + (r >> 1) + b;
 }
 
 constexpr int kTile = 64;
@@ -81,9 +84,11 @@ __global__ __launch_bounds__(256) void repack_gptq_zeros(const uint32_t* __restr
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)N * h) return;
     const int n = (int)(i / h), b = (int)(i % h);
+    int glo, ghi;
+    zero_byte_groups(b, G, glo, ghi);
     const int sh = 4 * (n & 7);
-    const uint32_t lo = (qz[(size_t)b * (N / 8) + n / 8] >> sh) & 15u;
-    const uint32_t hi = (qz[(size_t)(b + h) * (N / 8) + n / 8] >> sh) & 15u;
+    const uint32_t lo = (qz[(size_t)glo * (N / 8) + n / 8] >> sh) & 15u;
+    const uint32_t hi = (qz[(size_t)ghi * (N / 8) + n / 8] >> sh) & 15u;
     zp[i] = (uint8_t)(lo | (hi << 4));
 }
 
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(256) void dequant_bf16(const uint32_t* __restrict__
     const int n = (int)(i / K8), w = (int)(i % K8), g = w >> 2;
     const uint32_t word = qw[i];
     const float s = bf16_bits(sc[(size_t)n * G + g]);
-    const int z = (int)rowpack_zero(zp + (size_t)n * (G >> 1), g, G);
+    const int z = (int)zero_of_group(zp + (size_t)n * (G >> 1), g, G);
     uint32_t o[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(256) void dequant_bf16(const uint32_t* __restrict__
 }
 
 // Min-max RTN quantizer (fp32 weights [N, K]) straight into the row-packed layout.
-// One thread per zero byte: groups b and b + G/2 of one row, so no two threads share a byte.
+// One thread per zero byte (its two groups), so no two threads share a byte.
 __device__ __forceinline__ void quantize_group(const float* __restrict__ wg, uint32_t* __restrict__ qwg,
                                                uint16_t* __restrict__ s_out, uint32_t* z_out) {
     float v[32];
@@ -174,10 +179,11 @@ __global__ __launch_bounds__(256) void quantize_minmax(const float* __restrict__
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)N * h) return;
     const int n = (int)(i / h), b = (int)(i % h);
+    int glo, ghi;
+    zero_byte_groups(b, G, glo, ghi);
     uint32_t z0, z1;
-    quantize_group(w + (size_t)n * K + 32 * b, qw + (size_t)n * (K >> 3) + 4 * b, sc + (size_t)n * G + b, &z0);
-    quantize_group(w + (size_t)n * K + 32 * (b + h), qw + (size_t)n * (K >> 3) + 4 * (b + h),
-                   sc + (size_t)n * G + b + h, &z1);
+    quantize_group(w + (size_t)n * K + 32 * glo, qw + (size_t)n * (K >> 3) + 4 * glo, sc + (size_t)n * G + glo, &z0);
+    quantize_group(w + (size_t)n * K + 32 * ghi, qw + (size_t)n * (K >> 3) + 4 * ghi, sc + (size_t)n * G + ghi, &z1);
     zp[i] = (uint8_t)(z0 | (z1 << 4));
 }
 

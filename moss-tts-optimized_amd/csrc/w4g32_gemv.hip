@@ -24,7 +24,7 @@ struct XSlice {
     float sum[KG];       // fp32 sum of those 32 values
 };
 
-template <int KG, bool SUMS>
+template <int KG, bool SUMS, bool FULL>
 __device__ __forceinline__ void load_x(XSlice<KG>& xs, const uint16_t* __restrict__ x, int lane, int G) {
     uint32_t ones = 0x3F803F80u;  // bf16 pair (1.0, 1.0): group sums through the same dot2 path
     asm volatile("" : "+v"(ones));
@@ -32,7 +32,7 @@ __device__ __forceinline__ void load_x(XSlice<KG>& xs, const uint16_t* __restric
     for (int j = 0; j < KG; ++j) {
         const int g = lane + kWave * j;
         float s = 0.f;
-        if (g < G) {
+        if (FULL || g < G) {
             const uint4* p = reinterpret_cast<const uint4*>(x + 32 * g);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -61,8 +61,8 @@ struct RowLoad {
     uint32_t z[KG];  // zero point
 };
 
-// FULL: G == 64 * KG with KG even, so lane l's zero for group l + 64 j (j < KG/2) is the low
-// nibble of byte l + 64 j and the zero for group l + 64 (j + KG/2) its high nibble.
+// FULL: G == 64 * KG with KG even: every 128-group block is complete, so byte 64 jj + l of
+// the zp row holds lane l's zeros for groups l + 128 jj (low) and l + 128 jj + 64 (high).
 template <int KG, bool FULL>
 __device__ __forceinline__ void load_row(RowLoad<KG>& r, const uint4* __restrict__ qw,
                                          const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
@@ -75,10 +75,10 @@ __device__ __forceinline__ void load_row(RowLoad<KG>& r, const uint4* __restrict
             r.s[j] = sc[(size_t)n * G + lane + kWave * j];
         }
 #pragma unroll
-        for (int j = 0; j < KG / 2; ++j) {
-            const uint32_t b = zp[(size_t)n * h + lane + kWave * j];
-            r.z[j] = b & 15u;
-            r.z[j + KG / 2] = b >> 4;
+        for (int jj = 0; jj < KG / 2; ++jj) {
+            const uint32_t b = zp[(size_t)n * h + lane + kWave * jj];
+            r.z[2 * jj] = b & 15u;
+            r.z[2 * jj + 1] = b >> 4;
         }
     } else {
 #pragma unroll
@@ -87,8 +87,7 @@ __device__ __forceinline__ void load_row(RowLoad<KG>& r, const uint4* __restrict
             if (g < G) {
                 r.w[j] = qw[(size_t)n * G + g];
                 r.s[j] = sc[(size_t)n * G + g];
-                const uint32_t b = zp[(size_t)n * h + (g < h ? g : g - h)];
-                r.z[j] = g < h ? (b & 15u) : (b >> 4);
+                r.z[j] = zero_of_group(zp + (size_t)n * h, g, G);
             } else {
                 r.w[j] = make_uint4(0u, 0u, 0u, 0u);
                 r.s[j] = 0u;
@@ -122,13 +121,13 @@ __device__ __forceinline__ float row_partial_unrounded(const XSlice<KG>& xs, con
     float part = 0.f;
 #pragma unroll
     for (int j = 0; j < KG; ++j) {
-        float acc = 0.f;
+        // the chain starts at -(128 + z) * sum(x): it ends at sum (q - z) x directly
+        float acc = -(128.0f + (float)r.z[j]) * xs.sum[j];
         acc = word_dot(r.w[j].x, &xs.v[j][0], acc, m);
         acc = word_dot(r.w[j].y, &xs.v[j][4], acc, m);
         acc = word_dot(r.w[j].z, &xs.v[j][8], acc, m);
         acc = word_dot(r.w[j].w, &xs.v[j][12], acc, m);
-        const float centred = fmaf(-(128.0f + (float)r.z[j]), xs.sum[j], acc);
-        part = fmaf(bf16_bits((uint16_t)r.s[j]), centred, part);
+        part = fmaf(bf16_bits((uint16_t)r.s[j]), acc, part);
     }
     return part;
 }
@@ -147,20 +146,18 @@ __device__ __forceinline__ float word_dot_exact(uint32_t w, const uint32_t* xv, 
 
 template <int KG>
 __device__ __forceinline__ float row_partial_exact(const XSlice<KG>& xs, const RowLoad<KG>& r, Magic m) {
-    float part = 0.f;
+    float acc = 0.f;  // one dot2 chain over the whole row: the weights already carry their scale
 #pragma unroll
     for (int j = 0; j < KG; ++j) {
         const uint32_t s_lo = r.s[j] & 0xffffu;
         const uint32_t s_hi = s_lo << 16;
         const float bias = -(128.0f + (float)r.z[j]) * bf16_bits((uint16_t)s_lo);  // exact: 16 bits
-        float acc = 0.f;
         acc = word_dot_exact(r.w[j].x, &xs.v[j][0], acc, m, s_lo, s_hi, bias);
         acc = word_dot_exact(r.w[j].y, &xs.v[j][4], acc, m, s_lo, s_hi, bias);
         acc = word_dot_exact(r.w[j].z, &xs.v[j][8], acc, m, s_lo, s_hi, bias);
         acc = word_dot_exact(r.w[j].w, &xs.v[j][12], acc, m, s_lo, s_hi, bias);
-        part += acc;
     }
-    return part;
+    return acc;
 }
 
 __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
@@ -170,6 +167,13 @@ __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
     return f32_to_bf16(a * u);
 }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int KG, bool FULL>
+__device__ __forceinline__ void load_row_nt(RowLoad<KG>& r, const uint4* __restrict__ qw,
+                                            const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                            int n, int lane, int G);
+
 // n_out output rows; PAIRED reads gate row n and up row n + n_out.
 template <int KG, int R, bool PAIRED, bool FULL, bool EXACT>
 __global__ __launch_bounds__(256) void w4g32_gemv_kernel(const uint16_t* __restrict__ x,
@@ -178,7 +182,8 @@ __global__ __launch_bounds__(256) void w4g32_gemv_kernel(const uint16_t* __restr
                                                          const uint8_t* __restrict__ zp,
                                                          uint16_t* __restrict__ y, int G, int n_out) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+    // wave-uniform: lets row addressing run on the scalar unit
+    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
     const int row0 = wave * R;
     if (row0 >= n_out) return;  // wave-uniform
 
@@ -188,10 +193,10 @@ __global__ __launch_bounds__(256) void w4g32_gemv_kernel(const uint16_t* __restr
     for (int r = 0; r < NR; ++r) {
         const int local = PAIRED ? (r % R) : r;
         const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
-        load_row<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
+        load_row_nt<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
     }
     XSlice<KG> xs;
-    load_x<KG, !EXACT>(xs, x, lane, G);
+    load_x<KG, !EXACT, FULL>(xs, x, lane, G);
 
     const Magic m = make_magic();
     float out[NR];
@@ -206,6 +211,231 @@ __global__ __launch_bounds__(256) void w4g32_gemv_kernel(const uint16_t* __restr
             if (n < n_out) y[n] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
         }
     }
+}
+
+// ---------------------------------------------------------------------------------------
+// Streaming variant: a fixed grid of waves, each walking rows n = wave, wave + stride, ...
+// with the next row's codes/scales/zeros loaded (non-temporally: read once, never reused)
+// while the current row is computed, so VALU work overlaps the HBM stream instead of
+// bunching up after it.
+
+template <int KG, bool FULL>
+__device__ __forceinline__ void load_row_nt(RowLoad<KG>& r, const uint4* __restrict__ qw,
+                                            const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                            int n, int lane, int G) {
+    const int h = G >> 1;
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        const int g = lane + kWave * j;
+        if (FULL || g < G) {
+            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(qw + (size_t)n * G + g));
+            r.w[j] = make_uint4(v.x, v.y, v.z, v.w);
+            r.s[j] = __builtin_nontemporal_load(sc + (size_t)n * G + g);
+        } else {
+            r.w[j] = make_uint4(0u, 0u, 0u, 0u);
+            r.s[j] = 0u;
+        }
+    }
+    if constexpr (FULL) {
+#pragma unroll
+        for (int jj = 0; jj < KG / 2; ++jj) {
+            const uint32_t b = __builtin_nontemporal_load(zp + (size_t)n * h + lane + kWave * jj);
+            r.z[2 * jj] = b & 15u;
+            r.z[2 * jj + 1] = b >> 4;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const int g = lane + kWave * j;
+            if (g < G) {
+                r.z[j] = zero_of_group(zp + (size_t)n * h, g, G);
+            } else {
+                r.z[j] = 0u;
+            }
+        }
+    }
+}
+
+template <int KG, bool PAIRED, bool FULL, bool EXACT>
+__device__ __forceinline__ void stream_row(const XSlice<KG>& xs, const RowLoad<KG>* rows, Magic m, int n, int lane,
+                                           uint16_t* __restrict__ y) {
+    const float a = wave_sum(EXACT ? row_partial_exact(xs, rows[0], m) : row_partial_unrounded(xs, rows[0], m));
+    if constexpr (PAIRED) {
+        const float b = wave_sum(EXACT ? row_partial_exact(xs, rows[1], m) : row_partial_unrounded(xs, rows[1], m));
+        if (lane == 0) y[n] = silu_mul_bf16(a, b);
+    } else {
+        if (lane == 0) y[n] = f32_to_bf16(a);
+    }
+}
+
+template <int KG, bool PAIRED, bool FULL, bool EXACT>
+__global__ __launch_bounds__(256) void w4g32_gemv_stream(const uint16_t* __restrict__ x,
+                                                         const uint4* __restrict__ qw,
+                                                         const uint16_t* __restrict__ sc,
+                                                         const uint8_t* __restrict__ zp,
+                                                         uint16_t* __restrict__ y, int G, int n_out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int stride = gridDim.x * (blockDim.x / kWave);
+    int n = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
+    if (n >= n_out) return;  // wave-uniform
+    constexpr int NR = PAIRED ? 2 : 1;
+    RowLoad<KG> buf0[NR], buf1[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) load_row_nt<KG, FULL>(buf0[r], qw, sc, zp, n + r * n_out, lane, G);
+    XSlice<KG> xs;
+    load_x<KG, !EXACT, FULL>(xs, x, lane, G);
+    const Magic m = make_magic();
+    // ping-pong between two register buffers so no copy is needed between iterations
+    while (true) {
+        const int n1 = n + stride;
+        if (n1 < n_out) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) load_row_nt<KG, FULL>(buf1[r], qw, sc, zp, n1 + r * n_out, lane, G);
+        }
+        stream_row<KG, PAIRED, FULL, EXACT>(xs, buf0, m, n, lane, y);
+        if (n1 >= n_out) break;
+        const int n2 = n1 + stride;
+        if (n2 < n_out) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) load_row_nt<KG, FULL>(buf0[r], qw, sc, zp, n2 + r * n_out, lane, G);
+        }
+        stream_row<KG, PAIRED, FULL, EXACT>(xs, buf1, m, n1, lane, y);
+        if (n2 >= n_out) break;
+        n = n2;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Large K (K = 4096 W): the W waves of a workgroup each own one 4096-wide slice of K (128
+// groups, lane l holding groups 128 s + l and 128 s + l + 64), so every wave keeps the
+// 32-VGPR x slice of the K = 4096 case; the per-slice row sums meet in LDS and are added in
+// slice order by wave 0.
+template <bool NT>
+__device__ __forceinline__ void load_row_slice(RowLoad<2>& r, const uint4* __restrict__ qw,
+                                               const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                               int n, int lane, int G, int g0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const size_t gi = (size_t)n * G + g0 + lane + kWave * j;
+        if constexpr (NT) {
+            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(qw + gi));
+            r.w[j] = make_uint4(v.x, v.y, v.z, v.w);
+            r.s[j] = __builtin_nontemporal_load(sc + gi);
+        } else {
+            r.w[j] = qw[gi];
+            r.s[j] = sc[gi];
+        }
+    }
+    // block g0 / 128 is complete: byte g0 / 2 + lane holds this lane's two zero points
+    const size_t zi = (size_t)n * (G >> 1) + (g0 >> 1) + lane;
+    const uint32_t b = NT ? (uint32_t)__builtin_nontemporal_load(zp + zi) : (uint32_t)zp[zi];
+    r.z[0] = b & 15u;
+    r.z[1] = b >> 4;
+}
+
+template <int W, int R, bool PAIRED, bool EXACT>
+__global__ __launch_bounds__(64 * W) void w4g32_gemv_ksplit(const uint16_t* __restrict__ x,
+                                                            const uint4* __restrict__ qw,
+                                                            const uint16_t* __restrict__ sc,
+                                                            const uint8_t* __restrict__ zp,
+                                                            uint16_t* __restrict__ y, int G, int n_out) {
+    constexpr int NR = PAIRED ? 2 * R : R;
+    __shared__ float part[W][NR];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int slice = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int row0 = blockIdx.x * R;
+    if (row0 >= n_out) return;  // uniform across the workgroup
+    const int g0 = 128 * slice;
+
+    RowLoad<2> rows[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int local = PAIRED ? (r % R) : r;
+        const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
+        load_row_slice<true>(rows[r], qw, sc, zp, n, lane, G, g0);
+    }
+    XSlice<2> xs;
+    load_x<2, !EXACT, true>(xs, x + 32 * g0, lane, 128);
+    const Magic m = make_magic();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const float v = wave_sum(EXACT ? row_partial_exact(xs, rows[r], m) : row_partial_unrounded(xs, rows[r], m));
+        if (lane == 0) part[slice][r] = v;
+    }
+    __syncthreads();
+    if (slice == 0 && lane < R) {
+        const int n = row0 + lane;
+        if (n < n_out) {
+            float a = 0.f, b = 0.f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                a += part[w][lane];
+                if constexpr (PAIRED) b += part[w][R + lane];
+            }
+            y[n] = PAIRED ? silu_mul_bf16(a, b) : f32_to_bf16(a);
+        }
+    }
+}
+
+template <bool PAIRED, bool EXACT>
+int launch_ksplit(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
+                  int rows, hipStream_t st) {
+    const int W = G / 128;
+    if (rows <= 0) rows = EXACT ? 2 : 4;
+    const dim3 grid((n_out + rows - 1) / rows);
+    const auto* xp = (const uint16_t*)x;
+    const auto* qp = (const uint4*)qw;
+    const auto* sp = (const uint16_t*)sc;
+    const auto* zpp = (const uint8_t*)zp;
+    auto* yp = (uint16_t*)y;
+#define MOSS_KS(WV, RV)                                                                                      \
+    if (W == WV && rows == RV) {                                                                             \
+        hipLaunchKernelGGL((w4g32_gemv_ksplit<WV, RV, PAIRED, EXACT>), grid, dim3(64 * WV), 0, st, xp, qp, sp, \
+                           zpp, yp, G, n_out);                                                               \
+        return moss_launch_status();                                                                         \
+    }
+    MOSS_KS(2, 1) MOSS_KS(2, 2) MOSS_KS(2, 4)
+    MOSS_KS(3, 1) MOSS_KS(3, 2) MOSS_KS(3, 4)
+    MOSS_KS(4, 1) MOSS_KS(4, 2) MOSS_KS(4, 4)
+#undef MOSS_KS
+    return (int)hipErrorInvalidValue;
+}
+
+template <bool PAIRED, bool EXACT>
+int launch_stream(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
+                  int waves, hipStream_t st) {
+    const int KG = (G + kWave - 1) / kWave;
+    if (waves <= 0) waves = 2048;
+    waves = min(waves, n_out);
+    const dim3 grid((waves + 3) / 4), block(256);
+    const auto* xp = (const uint16_t*)x;
+    const auto* qp = (const uint4*)qw;
+    const auto* sp = (const uint16_t*)sc;
+    const auto* zpp = (const uint8_t*)zp;
+    auto* yp = (uint16_t*)y;
+    const bool full = (G == kWave * KG) && (KG % 2 == 0);
+    switch (KG) {
+#define MOSS_KG_CASE(KGV)                                                                                        \
+    case KGV:                                                                                                    \
+        if (full)                                                                                                \
+            hipLaunchKernelGGL((w4g32_gemv_stream<KGV, PAIRED, (KGV % 2 == 0), EXACT>), grid, block, 0, st, xp, \
+                               qp, sp, zpp, yp, G, n_out);                                                       \
+        else                                                                                                     \
+            hipLaunchKernelGGL((w4g32_gemv_stream<KGV, PAIRED, false, EXACT>), grid, block, 0, st, xp, qp, sp,   \
+                               zpp, yp, G, n_out);                                                               \
+        break;
+        MOSS_KG_CASE(1)
+        MOSS_KG_CASE(2)
+        MOSS_KG_CASE(3)
+        MOSS_KG_CASE(4)
+        MOSS_KG_CASE(5)
+        MOSS_KG_CASE(6)
+        MOSS_KG_CASE(7)
+        MOSS_KG_CASE(8)
+#undef MOSS_KG_CASE
+        default: return (int)hipErrorInvalidValue;
+    }
+    return moss_launch_status();
 }
 
 template <bool PAIRED, int R, bool EXACT>
@@ -259,7 +489,18 @@ template <bool PAIRED>
 int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
                 int rows, int mode, hipStream_t st) {
     const int G = K / 32;
-    if (rows <= 0) rows = (G <= 128) ? (PAIRED ? 2 : 4) : (G <= 256 ? 2 : 1);
+    if (rows < 0) {
+        if (mode == MOSS_DEQUANT_EXACT) return launch_stream<PAIRED, true>(x, qw, sc, zp, y, G, n_out, -rows * 256, st);
+        if (mode == MOSS_DEQUANT_UNROUNDED)
+            return launch_stream<PAIRED, false>(x, qw, sc, zp, y, G, n_out, -rows * 256, st);
+        return (int)hipErrorInvalidValue;
+    }
+    if (G % 128 == 0 && G >= 256 && G <= 512 && rows >= 0 && rows <= 4 && rows != 3) {
+        if (mode == MOSS_DEQUANT_EXACT) return launch_ksplit<PAIRED, true>(x, qw, sc, zp, y, G, n_out, rows, st);
+        if (mode == MOSS_DEQUANT_UNROUNDED) return launch_ksplit<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
+        return (int)hipErrorInvalidValue;
+    }
+    if (rows == 0) rows = (G <= 128) ? (PAIRED ? 2 : 4) : (G <= 256 ? 2 : 1);
     if (mode == MOSS_DEQUANT_EXACT) return launch_gemv_mode<PAIRED, true>(x, qw, sc, zp, y, G, n_out, rows, st);
     if (mode == MOSS_DEQUANT_UNROUNDED) return launch_gemv_mode<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
     return (int)hipErrorInvalidValue;

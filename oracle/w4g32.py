@@ -231,7 +231,10 @@ def rowpack(q: torch.Tensor, z: torch.Tensor, s: torch.Tensor):
       ``k = 32g + 8j + t``; the code for ``t = 2i`` sits at bits ``[4i, 4i+4)`` and for
       ``t = 2i+1`` at bits ``[16+4i, 20+4i)``.
     * ``sc bf16 [N, G]`` (unchanged order).
-    * ``zp uint8 [N, G/2]``: byte b holds ``z[b]`` (low nibble) and ``z[b + G/2]`` (high).
+    * ``zp uint8 [N, G/2]`` in blocks of 128 groups: for block c with ``r = min(128, G - 128c)``
+      groups, byte ``64c + b`` (``b < r/2``) holds ``z[128c + b]`` (low nibble) and
+      ``z[128c + r/2 + b]`` (high nibble).  A GEMV lane owning groups ``l`` and ``l + 64`` of
+      a 128-group slice finds both zero points in one byte.
     """
     qn = _np(q).astype(np.uint32)
     zn = _np(z).astype(np.uint8)
@@ -243,9 +246,11 @@ def rowpack(q: torch.Tensor, z: torch.Tensor, s: torch.Tensor):
     for i in range(4):
         w |= (t[:, :, 2 * i] & 15) << (4 * i)
         w |= (t[:, :, 2 * i + 1] & 15) << (16 + 4 * i)
-    g = zn.shape[1]
-    zp = (zn[:, : g // 2] & 15) | ((zn[:, g // 2:] & 15) << 4)
-    return (torch.from_numpy(w.view(np.int32)), s.contiguous(), torch.from_numpy(zp.astype(np.uint8)))
+    zp = np.zeros((n, zn.shape[1] // 2), dtype=np.uint8)
+    for c0 in range(0, zn.shape[1], 128):
+        r = min(128, zn.shape[1] - c0)
+        zp[:, c0 // 2: c0 // 2 + r // 2] = (zn[:, c0: c0 + r // 2] & 15) | ((zn[:, c0 + r // 2: c0 + r] & 15) << 4)
+    return (torch.from_numpy(w.view(np.int32)), s.contiguous(), torch.from_numpy(zp))
 
 
 def rowunpack(qw: torch.Tensor, zp: torch.Tensor):
@@ -257,7 +262,13 @@ def rowunpack(qw: torch.Tensor, zp: torch.Tensor):
         out[:, :, 2 * i] = (w >> (4 * i)) & 15
         out[:, :, 2 * i + 1] = (w >> (16 + 4 * i)) & 15
     zb = _np(zp).astype(np.uint8)
-    z = np.concatenate([zb & 15, zb >> 4], axis=1)
+    g = 2 * zb.shape[1]
+    z = np.zeros((n, g), dtype=np.uint8)
+    for c0 in range(0, g, 128):
+        r = min(128, g - c0)
+        blk = zb[:, c0 // 2: c0 // 2 + r // 2]
+        z[:, c0: c0 + r // 2] = blk & 15
+        z[:, c0 + r // 2: c0 + r] = blk >> 4
     return torch.from_numpy(out.reshape(n, k8 * 8)), torch.from_numpy(z)
 
 

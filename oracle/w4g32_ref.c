@@ -91,9 +91,13 @@ void oracle_rowpack(const uint8_t *q, const uint8_t *z, int N, int K, uint32_t *
             }
             qw[(size_t)n * (K / 8) + w] = word;
         }
-        for (int b = 0; b < G / 2; ++b)
-            zp[(size_t)n * (G / 2) + b] =
-                (uint8_t)((z[(size_t)n * G + b] & 15u) | ((z[(size_t)n * G + b + G / 2] & 15u) << 4));
+        /* zero points in blocks of 128 groups: byte 64c + b = z[128c + b] | z[128c + r/2 + b] << 4 */
+        for (int c0 = 0; c0 < G; c0 += 128) {
+            int r = G - c0 < 128 ? G - c0 : 128;
+            for (int b = 0; b < r / 2; ++b)
+                zp[(size_t)n * (G / 2) + c0 / 2 + b] = (uint8_t)((z[(size_t)n * G + c0 + b] & 15u) |
+                                                                ((z[(size_t)n * G + c0 + r / 2 + b] & 15u) << 4));
+        }
     }
 }
 
