@@ -144,6 +144,35 @@ def cpu_baseline(torch, budget_s: float):
             "ms_per_step": round(med * 1e3, 3)}
 
 
+def decode_step_bench(torch, n_layers: int, steps: int, dev):
+    """The full batch-1 decode step (embedding -> n_layers -> 32 INT4 heads, KV cache of 2048
+    rows filled with N(0,1), current position 2047) captured as one graph; ms per step."""
+    from moss_tts._runtime.decode import DecodeStepG32
+
+    _log(f"[bench] building the {n_layers}-layer decode step (random INT4-G32 weights, KV 2048)")
+    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
+    eng.capture()
+    ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
+    eng.step(ids, 2047)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        eng.graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    nbytes = eng.step_bytes(2047)
+    _log(f"[bench] decode step ({n_layers} layers): {ms:.3f} ms, {nbytes / ms / 1e6:.0f} GB/s")
+    out = {"layers": n_layers, "ms_per_step": round(ms, 4), "bytes_per_step": nbytes,
+           "GB/s": round(nbytes / ms / 1e6, 1), "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+           "kv_rows": 2048, "position": 2047, "dequant": "exact", "target_ms": 4.0}
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,6 +181,9 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=8, help="distinct MLP weight copies rotated over")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=30,
+                    help="timed replays of the 36-layer decode step (0 skips it)")
+    ap.add_argument("--decode-layers", type=int, default=36)
     ap.add_argument("--pmc-pass", action="store_true",
                     help="eager launches only (for rocprofv3 --pmc): a 512 MiB copy of known size, then "
                          "one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy")
@@ -272,6 +304,13 @@ def main() -> int:
     _log(f"[bench] GEMV K=4096 N=12288: {ns_s * 1e6:.2f} us, {ns_gbs:.0f} GB/s (unrounded {ns_unr_s * 1e6:.2f} us); "
          f"down K=12288 N=4096: {dn_s * 1e6:.2f} us, {DOWN_BYTES / dn_s / 1e9:.0f} GB/s")
 
+    n_copies = len(copies)
+    decode = None
+    if args.decode_steps > 0 and not args.pmc_pass:
+        del copies, gemv_copies, g_cycle, g_unr
+        torch.cuda.empty_cache()
+        decode = decode_step_bench(torch, args.decode_layers, args.decode_steps, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         _log("[bench] CPU baseline (oracle, torch CPU) ...")
@@ -296,7 +335,7 @@ def main() -> int:
                         "N=2x12288 with SiLU*mul epilogue + down GEMV K=12288 N=4096",
             "bytes_per_step": MLP_BYTES + NORM_BYTES,
             "algorithmic_bytes_counted": MLP_BYTES,
-            "weight_copies": len(copies),
+            "weight_copies": n_copies,
             "resident_weight_mib": round(resident / 2**20, 1),
             "weights": "N(0,0.02) fp32, min-max quantized per 32-input group on the GPU (seeded)",
             "activations": "bf16 N(0,1) through RMSNorm with weight 1+N(0,0.01)",
@@ -328,6 +367,7 @@ def main() -> int:
             "gemv_down_k12288_n4096": {"us_per_call": round(dn_s * 1e6, 3),
                                        "GB/s": round(DOWN_BYTES / dn_s / 1e9, 1)},
             "wall_s_timed_region": round(wall, 4),
+            "decode_step": decode,
         },
     }
     print(json.dumps(line), flush=True)

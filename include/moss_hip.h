@@ -91,18 +91,40 @@ int moss_rmsnorm(const void *x, const void *res, const void *w, void *sum_out, v
 
 /* Qwen3-8B q/k head RMSNorm + RoPE + KV-cache write for ntok tokens.
  * qkv bf16 [ntok, 6144] (q 32x128 | k 8x128 | v 8x128), q/k norm weights bf16 [128],
- * cos/sin bf16 [ntok, 128], positions int64 [ntok] (unique, in [0, L)), q_out bf16
- * [ntok, 32, 128], caches bf16 [8, L, 128] written at rows positions[t].
+ * cos/sin bf16 rows of 128: row t of [ntok, 128] (cos_by_position = 0) or row positions[t]
+ * of a [L, 128] table (cos_by_position = 1, so a captured decode graph stays valid for any
+ * position), positions int64 [ntok] (unique, in [0, L); clamped), q_out bf16 [ntok, 32, 128],
+ * caches bf16 [8, L, 128] written at rows positions[t].
  * Replaces _qk_rope_cache (src/moss_tts/_runtime/kernels.py:142-170) and _prefill_qkv
  * (src/moss_tts/_runtime/prefill_qkv.py:7-28, project :61-83). */
 int moss_qk_norm_rope_kv(const void *qkv, const void *q_weight, const void *k_weight, const void *cos,
                          const void *sin, void *q_out, void *k_cache, void *v_cache, const void *positions, int L,
-                         int ntok, float eps, void *stream);
+                         int ntok, float eps, int cos_by_position, void *stream);
 
 /* x bf16 [rows, 2n] = (gate | up) halves of width n (n even) -> y bf16 [rows, n],
  * y = bf16(bf16(silu(g)) * u).  Replaces _silu mode 0 of
  * src/moss_tts/_runtime/prefill_pointwise.py:18-31 and _silu_mul, kernels.py:123-139. */
 int moss_silu_mul(const void *x, void *y, int rows, int n, void *stream);
+
+/* ------------------------------------------------------- decode attention */
+/* Number of 64-row splits for a cache of L rows (sizes partial [32, S, 128] fp32, lse [32, S]). */
+int moss_decode_attention_splits(int L);
+
+/* One query token, Qwen3-8B GQA (32 query / 8 KV heads, head_dim 128): q bf16 [32,128],
+ * caches bf16 [8, L, 128] (one layer of the [1, 8, L, 128] static cache), position int64 [1]
+ * on the device (rows 0..position are attended; clamped to L-1), caller-owned workspaces
+ * partial fp32 [32, S, 128] and lse fp32 [32, S], out bf16 [32 * 128].  Split + LSE merge.
+ * Replaces _decode_attn/_decode_attn_reduce (src/moss_tts/_runtime/kernels.py:173-208,
+ * driven from qk_rope_decode :211-251) and launch_attention_ordered
+ * (src/moss_tts/_runtime/attention_native.cu:91-97). */
+int moss_decode_attention(const void *q, const void *k_cache, const void *v_cache, const void *position,
+                          void *partial, void *lse, void *out, int L, void *stream);
+
+/* ids int64 [T, Q+1] (text token then Q codebook codes), text bf16 [Vt, H], audio bf16
+ * [Q, V, H] -> out bf16 [T, H] with a bf16 rounding after each addition; ids are clamped
+ * into their tables.  Replaces embedding_sum (src/moss_tts/_runtime/kernels.py:7-26). */
+int moss_embedding_sum(const void *ids, const void *text, const void *audio, void *out, int T, int H, int Vt, int V,
+                       int Q, void *stream);
 
 #ifdef __cplusplus
 }

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
                                                        const uint16_t* __restrict__ sin_t,
                                                        uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
                                                        uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
-                                                       int L, int ntok, float eps) {
+                                                       int L, int ntok, float eps, int cos_by_position) {
     constexpr int QH = 32, KH = 8, D = 128, ROW = (QH + 2 * KH) * D;  // 6144
     const int wave = blockIdx.x * 4 + threadIdx.x / kWave;
     if (wave >= ntok * (QH + KH)) return;
@@ -115,8 +115,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
     const float r = rsqrtf(wave_sum(a * a + b * b) / (float)D + eps);
     const float an = round_bf16(round_bf16(a * r) * bf16_bits(wt[l]));
     const float bn = round_bf16(round_bf16(b * r) * bf16_bits(wt[l + 64]));
-    const float c0 = bf16_bits(cos_t[(size_t)t * D + l]), c1 = bf16_bits(cos_t[(size_t)t * D + l + 64]);
-    const float s0 = bf16_bits(sin_t[(size_t)t * D + l]), s1 = bf16_bits(sin_t[(size_t)t * D + l + 64]);
+    // positions are validated on the host; the clamp keeps every cache/table access in range
+    const int64_t p = min(max(pos[t], (int64_t)0), (int64_t)(L - 1));
+    const size_t crow = cos_by_position ? (size_t)p : (size_t)t;  // table row: by position or token
+    const float c0 = bf16_bits(cos_t[crow * D + l]), c1 = bf16_bits(cos_t[crow * D + l + 64]);
+    const float s0 = bf16_bits(sin_t[crow * D + l]), s1 = bf16_bits(sin_t[crow * D + l + 64]);
     // d = l < 64: partner is bn, negated;  d = l + 64: partner is an
     const uint16_t o0 = f32_to_bf16(round_bf16(an * c0) + round_bf16((-bn) * s0));
     const uint16_t o1 = f32_to_bf16(round_bf16(bn * c1) + round_bf16(an * s1));
@@ -126,7 +129,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
         dst[l + 64] = o1;
     } else {
         const int kh = h - QH;
-        const int64_t p = pos[t];
         uint16_t* kd = kc + ((size_t)kh * L + p) * D;
         uint16_t* vd = vc + ((size_t)kh * L + p) * D;
         kd[l] = o0;
@@ -178,14 +180,14 @@ MOSS_API int moss_rmsnorm(const void* x, const void* res, const void* w, void* s
 
 MOSS_API int moss_qk_norm_rope_kv(const void* qkv, const void* q_weight, const void* k_weight, const void* cos,
                                   const void* sin, void* q_out, void* k_cache, void* v_cache, const void* positions,
-                                  int L, int ntok, float eps, void* stream) {
+                                  int L, int ntok, float eps, int cos_by_position, void* stream) {
     MOSS_CHECK_ARG(qkv && q_weight && k_weight && cos && sin && q_out && k_cache && v_cache && positions);
     MOSS_CHECK_ARG(L > 0 && ntok > 0);
     const int waves = ntok * 40;
     hipLaunchKernelGGL(qk_norm_rope_kv, dim3((waves + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t*)qkv, (const uint16_t*)q_weight, (const uint16_t*)k_weight,
                        (const uint16_t*)cos, (const uint16_t*)sin, (uint16_t*)q_out, (uint16_t*)k_cache,
-                       (uint16_t*)v_cache, (const int64_t*)positions, L, ntok, eps);
+                       (uint16_t*)v_cache, (const int64_t*)positions, L, ntok, eps, cos_by_position);
     return moss_launch_status();
 }
 

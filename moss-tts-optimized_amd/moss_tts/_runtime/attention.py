@@ -1,0 +1,73 @@
+"""Decode attention over the static bf16 KV cache and the decode-step embedding sum.
+
+``decode_attention`` mirrors the reference's decode path after q/k-norm + RoPE
+(``src/moss_tts/_runtime/kernels.py:211-251``, native launcher
+``src/moss_tts/_runtime/attention_native.py:31-44``): validation raises ``ValueError``,
+the split workspaces are caller-owned or allocated with ``torch.empty``, launches go to the
+current stream.  ``embedding_sum`` mirrors ``src/moss_tts/_runtime/kernels.py:21-26``.
+"""
+from __future__ import annotations
+
+import functools
+
+import torch
+
+from . import native
+from .w4g32 import _aligned, _cuda_contig, _require
+
+QH, KH, HD = 32, 8, 128
+
+
+@functools.lru_cache(maxsize=None)
+def splits(L: int) -> int:
+    return int(native.lib().moss_decode_attention_splits(int(L)))
+
+
+def workspace(L: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(partial fp32 [32, S, 128], lse fp32 [32, S]) for a cache of ``L`` rows."""
+    s = splits(L)
+    return (torch.empty((QH, s, HD), device=device, dtype=torch.float32),
+            torch.empty((QH, s), device=device, dtype=torch.float32))
+
+
+def decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, position: torch.Tensor,
+                     *, out: torch.Tensor | None = None, ws=None) -> torch.Tensor:
+    """One decode token: ``q`` bf16 (32*128 values), ``keys``/``values`` bf16 ``[1, 8, L, 128]``
+    (one layer), ``position`` int64 ``[1]`` on the device.  Returns bf16 ``[1, 1, 4096]``."""
+    _cuda_contig("q", q, torch.bfloat16)
+    dev = q.device
+    _require(q.numel() == QH * HD, f"q must hold {QH}x{HD} values")
+    for name, t in (("keys", keys), ("values", values)):
+        _cuda_contig(name, t, torch.bfloat16, dev)
+    _require(keys.shape == values.shape and keys.ndim == 4 and tuple(keys.shape[:2]) == (1, KH)
+             and keys.shape[3] == HD, "matching [1, 8, L, 128] KV buffers required")
+    _cuda_contig("position", position, torch.int64, dev)
+    _require(position.numel() == 1, "one int64 position required")
+    _require(_aligned(keys, 16) and _aligned(values, 16), "KV buffers must be 16-byte aligned")
+    L = keys.shape[2]
+    partial, lse = ws if ws is not None else workspace(L, dev)
+    _require(partial.numel() >= QH * splits(L) * HD and lse.numel() >= QH * splits(L), "workspace too small")
+    if out is None:
+        out = torch.empty((1, 1, QH * HD), device=dev, dtype=torch.bfloat16)
+    native.call("moss_decode_attention", native.ptr(q), native.ptr(keys), native.ptr(values), native.ptr(position),
+                native.ptr(partial), native.ptr(lse), native.ptr(out), L, native.stream_of(q))
+    return out
+
+
+def embedding_sum(ids: torch.Tensor, text_weight: torch.Tensor, audio_weight: torch.Tensor) -> torch.Tensor:
+    """``ids`` int64 ``[..., Q+1]`` -> bf16 ``[..., H]``: text row plus the Q codebook rows,
+    rounded to bf16 after every addition."""
+    _cuda_contig("ids", ids, torch.int64)
+    dev = ids.device
+    _cuda_contig("text_weight", text_weight, torch.bfloat16, dev)
+    _cuda_contig("audio_weight", audio_weight, torch.bfloat16, dev)
+    _require(text_weight.ndim == 2 and audio_weight.ndim == 3, "text [V, H] and audio [Q, V, H] tables required")
+    q = audio_weight.shape[0]
+    _require(ids.shape[-1] == q + 1, f"ids must end in a dimension of {q + 1}")
+    h = text_weight.shape[1]
+    _require(audio_weight.shape[2] == h, "text and audio widths differ")
+    t = ids.numel() // (q + 1)
+    out = torch.empty((*ids.shape[:-1], h), device=dev, dtype=torch.bfloat16)
+    native.call("moss_embedding_sum", native.ptr(ids), native.ptr(text_weight), native.ptr(audio_weight),
+                native.ptr(out), t, h, text_weight.shape[0], audio_weight.shape[1], q, native.stream_of(ids))
+    return out

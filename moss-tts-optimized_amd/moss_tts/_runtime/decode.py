@@ -1,0 +1,168 @@
+"""Batch-1 decode step of the Qwen3-8B backbone on the gfx950 kernels, captured as one graph.
+
+Per layer (the order of ``src/moss_tts/_runtime/llm.py:227-260`` with fused residuals):
+add-RMSNorm -> q||k||v GEMV -> q/k head-norm + RoPE + KV write -> split-K GQA attention ->
+O GEMV -> add-RMSNorm -> gate||up GEMV with SiLU*mul -> down GEMV.  The step starts with the
+33-row embedding sum (``src/moss_tts/_runtime/kernels.py:7-26``) and ends with the final norm
+and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``),
+here INT4-G32 as well.  Static input buffers (ids, position) make the step graph-capturable;
+``step()`` copies new inputs into them and replays the graph, as ``FastLLM.step`` does
+(``src/moss_tts/_runtime/llm.py:327-338``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import attention, pointwise, w4g32
+from .modules import QuantGateUpG32, QuantLinearG32
+from .w4g32 import _require
+
+HIDDEN, INTER, QH, KH, HD = 4096, 12288, 32, 8, 128
+CODEBOOKS, AUDIO_VOCAB = 32, 1025
+
+
+@dataclass
+class DecoderLayerG32:
+    qkv: QuantLinearG32
+    o: QuantLinearG32
+    gate_up: QuantGateUpG32
+    down: QuantLinearG32
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+
+    @property
+    def nbytes(self) -> int:
+        return sum(m.packed.nbytes for m in (self.qkv, self.o, self.gate_up, self.down))
+
+
+def rope_tables(length: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin ``[length, 128]`` bf16, as Qwen3RotaryEmbedding forms them: fp32
+    ``inv_freq = 1/theta^(2i/128)``, ``freqs = position * inv_freq``, ``emb = cat(freqs,
+    freqs)``, cos/sin in fp32, then bf16 (transformers ``modeling_qwen3.py:106-138``)."""
+    inv = 1.0 / (theta ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))
+    freqs = torch.arange(length, dtype=torch.float32)[:, None] @ inv[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().bfloat16().to(device), emb.sin().bfloat16().to(device)
+
+
+class DecodeStepG32:
+    """The INT4-G32 decode step.  ``max_length`` is the static KV capacity; the KV caches
+    are ``[1, 8, max_length, 128]`` bf16 per layer and kind, like the reference's StaticCache
+    (``src/moss_tts/_runtime/llm.py:192-193``)."""
+
+    def __init__(self, layers: list[DecoderLayerG32], final_norm: torch.Tensor, heads: QuantLinearG32,
+                 text_embedding: torch.Tensor, audio_embedding: torch.Tensor, *, max_length: int,
+                 eps: float = 1e-6, theta: float = 1e6):
+        _require(len(layers) > 0, "at least one layer")
+        dev = final_norm.device
+        _require(dev.type == "cuda", "the decode step runs on a HIP device")
+        _require(max_length > 0 and max_length % 64 == 0, "max_length must be a positive multiple of 64")
+        _require(heads.in_features == HIDDEN, "heads must read the 4096-wide hidden state")
+        self.layers = layers
+        self.final_norm = final_norm
+        self.heads = heads
+        self.text_embedding = text_embedding
+        self.audio_embedding = audio_embedding
+        self.max_length = max_length
+        self.eps = eps
+        self.device = dev
+        self.keys = [torch.zeros((1, KH, max_length, HD), device=dev, dtype=torch.bfloat16) for _ in layers]
+        self.values = [torch.zeros((1, KH, max_length, HD), device=dev, dtype=torch.bfloat16) for _ in layers]
+        self.cos, self.sin = rope_tables(max_length, theta, dev)
+        self.ids = torch.zeros((1, CODEBOOKS + 1), device=dev, dtype=torch.int64)
+        self.position = torch.zeros(1, device=dev, dtype=torch.int64)
+        self.ws = attention.workspace(max_length, dev)
+        self.graph = None
+        self.logits = None
+
+    # ------------------------------------------------------------------ forward
+    def forward(self) -> torch.Tensor:
+        """One step from the static ``ids``/``position`` buffers -> logits bf16 ``[N_heads]``."""
+        x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
+        residual = x
+        h = pointwise.rmsnorm(x, self.layers[0].input_norm, self.eps)
+        mlp = None
+        for i, layer in enumerate(self.layers):
+            if i > 0:
+                residual, h = pointwise.add_rmsnorm(mlp, residual, layer.input_norm, self.eps)
+            qkv = layer.qkv(h)
+            q = pointwise.qk_rope(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
+                                  self.values[i], self.position, self.eps, cos_by_position=True)
+            attn = attention.decode_attention(q, self.keys[i], self.values[i], self.position, ws=self.ws)
+            o = layer.o(attn.view(1, HIDDEN))
+            residual, h = pointwise.add_rmsnorm(o, residual, layer.post_norm, self.eps)
+            mlp = layer.down(layer.gate_up(h))
+        _, h = pointwise.add_rmsnorm(mlp, residual, self.final_norm, self.eps)
+        return self.heads(h).view(-1)
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        """Warm up on a side stream, then capture one step as a graph (``llm.py:289-301``)."""
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self.forward()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self.forward()
+        torch.cuda.synchronize(self.device)
+
+    @torch.inference_mode()
+    def step(self, ids: torch.Tensor, position: int) -> torch.Tensor:
+        """``ids`` int64 ``[1, 33]`` (host or device), ``0 <= position < max_length``."""
+        if not 0 <= position < self.max_length:
+            raise ValueError("KV capacity exceeded")
+        self.ids.copy_(ids.reshape(1, CODEBOOKS + 1))
+        self.position.fill_(position)
+        if self.graph is None:
+            return self.forward()
+        self.graph.replay()
+        return self.logits
+
+    @property
+    def weight_bytes(self) -> int:
+        return sum(layer.nbytes for layer in self.layers) + self.heads.packed.nbytes
+
+    def step_bytes(self, position: int) -> int:
+        """Algorithmic HBM bytes of one step at ``position``: packed weights and heads, the
+        K/V rows ``0..position`` of every layer, the 33 embedding rows."""
+        kv = len(self.layers) * 2 * KH * (position + 1) * HD * 2
+        return self.weight_bytes + kv + (CODEBOOKS + 1) * HIDDEN * 2
+
+    # -------------------------------------------------------------- synthetic model
+    @classmethod
+    @torch.inference_mode()
+    def random(cls, n_layers: int, *, max_length: int, device, seed: int = 0, text_vocab: int = 151936,
+               kv_fill: bool = True, dequant: int = w4g32.EXACT) -> "DecodeStepG32":
+        """Random-init Qwen3-8B-shaped weights (N(0, 0.02), min-max INT4-G32 quantized on the
+        device), norm weights 1 + N(0, 0.01), embeddings N(0, 1), KV caches N(0, 1)."""
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+
+        def q(n, k, mod=QuantLinearG32):
+            w = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32).mul_(0.02)
+            m = mod(w4g32.quantize_minmax(w), dequant=dequant)
+            del w
+            return m
+
+        def norm(n):
+            return (1 + 0.01 * torch.randn(n, generator=gen, device=dev)).bfloat16()
+
+        layers = [DecoderLayerG32(q((QH + 2 * KH) * HD, HIDDEN), q(HIDDEN, QH * HD),
+                                  q(2 * INTER, HIDDEN, QuantGateUpG32), q(HIDDEN, INTER),
+                                  norm(HIDDEN), norm(HIDDEN), norm(HD), norm(HD)) for _ in range(n_layers)]
+        heads = q(CODEBOOKS * AUDIO_VOCAB, HIDDEN)
+        text = torch.randn((text_vocab, HIDDEN), generator=gen, device=dev).bfloat16()
+        audio = torch.randn((CODEBOOKS, AUDIO_VOCAB, HIDDEN), generator=gen, device=dev).bfloat16()
+        eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length)
+        if kv_fill:
+            for t in eng.keys + eng.values:
+                t.copy_(torch.randn(t.shape, generator=gen, device=dev))
+        return eng

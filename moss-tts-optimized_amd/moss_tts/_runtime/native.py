@@ -35,8 +35,11 @@ SIGNATURES: dict[str, list] = {
     "moss_w4g32_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_w4g32_gateup_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
-    "moss_qk_norm_rope_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "moss_qk_norm_rope_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _P],
     "moss_silu_mul": [_P, _P, _I, _I, _P],
+    "moss_decode_attention_splits": [_I],
+    "moss_decode_attention": [_P, _P, _P, _P, _P, _P, _P, _I, _P],
+    "moss_embedding_sum": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
 }
 _RESTYPES = {"moss_error_string": ctypes.c_char_p}
 

@@ -57,16 +57,21 @@ QKV = (QH + 2 * KH) * HD
 
 def qk_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, cos: torch.Tensor,
             sin: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, positions: torch.Tensor,
-            eps: float) -> torch.Tensor:
+            eps: float, *, cos_by_position: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
     """q/k head RMSNorm + RoPE for ``n`` tokens; writes K/V rows ``positions`` of the cache
-    in place and returns ``q`` as ``[1, 32, n, 128]`` (a transposed view, like the reference)."""
+    in place and returns ``q`` as ``[1, 32, n, 128]`` (a transposed view, like the reference).
+
+    ``cos``/``sin`` hold one row per token, or with ``cos_by_position`` a whole ``[L, 128]``
+    table indexed by each token's (device-side) position."""
     _cuda_contig("qkv", qkv, torch.bfloat16)
     dev = qkv.device
     _require(qkv.shape[-1] == QKV, f"Qwen3-8B QKV rows of {QKV} required")
     n = qkv.numel() // QKV
+    L = keys.shape[2] if keys.ndim == 4 else 0
     for name, t in (("cos", cos), ("sin", sin)):
         _cuda_contig(name, t, torch.bfloat16, dev)
-        _require(t.numel() == n * HD, f"{name} must hold {n} rows of {HD}")
+        rows = L if cos_by_position else n
+        _require(t.numel() == rows * HD, f"{name} must hold {rows} rows of {HD}")
     for name, t in (("q_weight", q_weight), ("k_weight", k_weight)):
         _cuda_contig(name, t, torch.bfloat16, dev)
         _require(t.numel() == HD, f"{name} must hold {HD} values")
@@ -76,12 +81,11 @@ def qk_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, c
              and keys.shape[3] == HD, "matching [1, 8, L, 128] KV buffers required")
     _cuda_contig("positions", positions, torch.int64, dev)
     _require(positions.numel() == n, "one int64 position per token required")
-    L = keys.shape[2]
     _require(n <= L, "more tokens than KV rows")
-    q = torch.empty((1, n, QH, HD), device=dev, dtype=torch.bfloat16)
+    q = out if out is not None else torch.empty((1, n, QH, HD), device=dev, dtype=torch.bfloat16)
     native.call("moss_qk_norm_rope_kv", native.ptr(qkv), native.ptr(q_weight), native.ptr(k_weight),
                 native.ptr(cos), native.ptr(sin), native.ptr(q), native.ptr(keys), native.ptr(values),
-                native.ptr(positions), L, n, float(eps), native.stream_of(qkv))
+                native.ptr(positions), L, n, float(eps), int(bool(cos_by_position)), native.stream_of(qkv))
     return q.transpose(1, 2)
 
 

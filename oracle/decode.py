@@ -1,0 +1,40 @@
+"""CPU oracle: one batch-1 decode step composed from the per-operation oracles.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  Order of operations:
+``src/moss_tts/_runtime/llm.py:227-260`` (fused residual path) with the projections as
+dequant-then-matmul (``src/moss_tts/calibration.py:185-188``) rounded to bf16 at each
+projection output, heads ``src/moss_tts/_runtime/llm.py:271-279``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import attention as oa
+from . import pointwise as op
+from . import w4g32 as ow
+
+
+def decode_step(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):
+    """``layers``: dicts with bf16 dequantized ``qkv``, ``o``, ``gate_up``, ``down`` weights and
+    ``input_norm``, ``post_norm``, ``q_norm``, ``k_norm``; ``keys``/``values`` lists of
+    ``[1, 8, L, 128]`` caches (updated in place).  Returns bf16 logits."""
+    p = int(position)
+    x = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
+    residual = x
+    h = op.rmsnorm(x, layers[0]["input_norm"], eps)
+    mlp = None
+    for i, L in enumerate(layers):
+        if i > 0:
+            residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
+        qkv = ow.linear(h, L["qkv"]).bfloat16()
+        q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],
+                               torch.tensor([p]), eps)
+        attn = oa.decode_attention(q, keys[i], values[i], p).bfloat16().view(1, -1)
+        o = ow.linear(attn, L["o"]).bfloat16()
+        residual, h = op.add_rmsnorm(o, residual, L["post_norm"], eps)
+        y = ow.linear(h, L["gate_up"])
+        n = y.shape[1] // 2
+        a = ow.silu_mul_rounded(y[:, :n], y[:, n:])
+        mlp = ow.linear(a, L["down"]).bfloat16()
+    _, h = op.add_rmsnorm(mlp, residual, final_norm, eps)
+    return ow.linear(h, heads_w).bfloat16().view(-1)

@@ -85,3 +85,48 @@ def test_silu_mul(dev, rows, n):
     g = torch.Generator().manual_seed(rows + n)
     x = (torch.randn((rows, 2 * n), generator=g) * 3).bfloat16()
     _close(pointwise.silu_mul(x.to(dev)), p.silu_mul(x), f"silu_mul {rows}x{n}")
+
+
+@pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (96, 95)])
+def test_decode_attention(dev, L, position):
+    """Split-softmax GQA decode attention vs the oracle's exact fp32 softmax; bf16 output."""
+    from moss_tts._runtime import attention
+    from oracle import attention as oa
+
+    print(f"decode_attention L={L} p={position}", flush=True)
+    g = torch.Generator().manual_seed(L + position)
+    q = torch.randn((32, 128), generator=g).bfloat16()
+    kc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
+    vc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
+    pos = torch.tensor([position], dtype=torch.int64)
+    out = attention.decode_attention(q.to(dev), kc.to(dev), vc.to(dev), pos.to(dev))
+    ref = oa.decode_attention(q, kc, vc, position).reshape(1, 1, 4096)
+    _close(out, ref.bfloat16(), f"attention L={L} p={position}", exact_frac=0.95)
+
+
+def test_decode_attention_ignores_rows_after_position(dev):
+    from moss_tts._runtime import attention
+
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((32, 128), generator=g).bfloat16().to(dev)
+    kc = torch.randn((1, 8, 256, 128), generator=g).bfloat16().to(dev)
+    vc = torch.randn((1, 8, 256, 128), generator=g).bfloat16().to(dev)
+    pos = torch.tensor([100], dtype=torch.int64, device=dev)
+    a = attention.decode_attention(q, kc, vc, pos)
+    kc[:, :, 101:] = 1e4
+    vc[:, :, 101:] = float("nan")
+    b = attention.decode_attention(q, kc, vc, pos)
+    assert torch.equal(a, b)
+
+
+def test_embedding_sum(dev):
+    from moss_tts._runtime import attention
+    from oracle import attention as oa
+
+    g = torch.Generator().manual_seed(3)
+    text = torch.randn((300, 4096), generator=g).bfloat16()
+    audio = torch.randn((32, 1025, 4096), generator=g).bfloat16()
+    ids = torch.cat([torch.tensor([[17]]), torch.randint(0, 1025, (1, 32), generator=g)], 1)
+    out = attention.embedding_sum(ids.to(dev), text.to(dev), audio.to(dev))
+    ref = oa.embedding_sum(ids[0], text, audio)
+    assert torch.equal(out.cpu()[0].view(torch.int16), ref.view(torch.int16))
