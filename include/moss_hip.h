@@ -82,6 +82,15 @@ int moss_w4g32_gemv(const void *x, const void *qw, const void *sc, const void *z
 int moss_w4g32_gateup_silu(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K,
                            int N_half, int rows_per_wave, int dequant_mode, void *stream);
 
+/* ------------------------------------------------------------- prefill GEMM */
+/* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);
+ * weights are dequantized bit-exactly (bf16_rne((q-z)*s)) into LDS and multiplied with
+ * v_mfma_f32_32x32x16_bf16, fp32 accumulate.  The reference runs bf16 F.linear here
+ * (src/moss_tts/_runtime/llm.py:29,84,130); its INT4 contract is dequant + F.linear
+ * (src/moss_tts/calibration.py:185-188). */
+int moss_w4g32_gemm(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
+                    void *stream);
+
 /* --------------------------------------------------- norms, RoPE, SiLU*mul */
 /* Row RMSNorm over n (n % 8 == 0, n <= 8192), bf16 in/out, rounding points of Qwen3RMSNorm.
  * res == NULL: y = rmsnorm(x) (src/moss_tts/_runtime/kernels.py:50-66).

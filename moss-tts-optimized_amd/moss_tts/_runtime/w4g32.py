@@ -217,3 +217,17 @@ def gateup_silu(x: torch.Tensor, w: PackedW4G32, *, rows_per_wave: int = 0, dequ
     native.call("moss_w4g32_gateup_silu", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales),
                 native.ptr(w.zeros), native.ptr(y), 1, w.K, half, rows, mode, native.stream_of(x))
     return y
+
+
+def gemm(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
+    """Prefill projection: bf16 ``[..., M, K]`` -> bf16 ``[..., M, N]`` on the matrix cores, with
+    bit-exact bf16 dequantized weights and fp32 accumulation."""
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.shape[-1] == w.K, f"x must end in a dimension of {w.K}")
+    _require(_aligned(x, 16), "x must be 16-byte aligned")
+    m = x.numel() // w.K
+    _require(m > 0, "empty input")
+    y = torch.empty((*x.shape[:-1], w.N), dtype=torch.bfloat16, device=x.device)
+    native.call("moss_w4g32_gemm", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
+                native.ptr(y), m, w.K, w.N, native.stream_of(x))
+    return y

@@ -238,3 +238,35 @@ def test_gemv_rejects_bad_inputs(dev):
         w4g32.gemv(torch.randn((1, 128), device=dev).bfloat16(), pw, rows_per_wave=3)
     with pytest.raises(ValueError):
         w4g32.gemv(torch.randn((1, 128), device=dev).bfloat16(), pw, dequant=2)
+
+
+# ------------------------------------------------------------------- prefill GEMM
+@pytest.mark.parametrize("m,k,n", [(2, 64, 8), (16, 128, 64), (100, 512, 200), (128, 4096, 128), (512, 1024, 4096),
+                                   (37, 4096, 32800), (512, 4096, 6144), (512, 12288, 4096)])
+def test_gemm_parity(dev, m, k, n):
+    """MFMA GEMM with bit-exact bf16 dequantized weights: fp32 summation order is the only
+    difference from the oracle's dequant-then-matmul."""
+    from moss_tts._runtime import w4g32
+
+    print(f"gemm M={m} K={k} N={n}", flush=True)
+    q, z, s = _case(n, k, 300 + m + k + n)
+    x = torch.randn((m, k), generator=torch.Generator().manual_seed(4)).bfloat16()
+    y = w4g32.gemm(x.to(dev), _packed(q, z, s, dev))
+    torch.cuda.synchronize()
+    dq = o.dequantize(q, z, s)
+    ref = o.linear(x, dq)
+    _assert_close(y, ref, f"gemm M={m} K={k} N={n}")
+    abs_sum = o.linear(x.float().abs(), dq.float().abs())
+    _assert_rne_or_adjacent(y, ref, abs_sum, k, f"gemm M={m} K={k} N={n}")
+
+
+def test_gemm_rows_match_gemv(dev):
+    """Row r of the GEMM equals the exact-dequant GEMV of x[r] up to fp32 summation order."""
+    from moss_tts._runtime import w4g32
+
+    pw = w4g32.quantize_minmax((torch.randn((4096, 4096), device=dev) * 0.02).contiguous())
+    x = torch.randn((64, 4096), device=dev).bfloat16()
+    y = w4g32.gemm(x, pw).float()
+    for r in (0, 17, 63):
+        g = w4g32.gemv(x[r:r + 1].contiguous(), pw).float()
+        assert torch.allclose(y[r], g[0], atol=2e-2, rtol=1e-2)
