@@ -91,6 +91,25 @@ int moss_w4g32_gateup_silu(const void *x, const void *qw, const void *sc, const 
 int moss_w4g32_gemm(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
                     void *stream);
 
+/* --------------------------------------------------- FP8 E4M3 weight-only */
+/* W e4m3 (OCP) [N, K] row-major bytes (16-byte aligned), scale fp32 [N] or NULL (= 1):
+ * y bf16 [M, N] = bf16(scale[n] * sum_k f32(W[n,k]) * x[m,k]), fp32 accumulate.
+ * M == 1: decode GEMV (K % 16 == 0, K <= 16384, rows_per_wave in {0 (auto), 1, 2, 4});
+ * M > 1: MFMA GEMM with exact e4m3 -> bf16 weights (K % 64 == 0).  Arithmetic of
+ * _fp8_silu_gemv, src/moss_tts/_runtime/fused_mlp.py:7-23, without the SiLU epilogue. */
+int moss_fp8_linear(const void *x, const void *w, const void *scale, void *y, int M, int K, int N,
+                    int rows_per_wave, void *stream);
+
+/* Fused gate||up FP8 decode GEMV: W e4m3 [2*N_half, K] (gate rows first), scale fp32
+ * [2*N_half] or NULL, M must be 1; y bf16 [N_half] = bf16(bf16(silu(bf16(g*sg))) *
+ * bf16(u*su)).  Replaces fp8_silu_decode, src/moss_tts/_runtime/fused_mlp.py:26-30. */
+int moss_fp8_gateup_silu(const void *x, const void *w, const void *scale, void *y, int M, int K, int N_half,
+                         int rows_per_wave, void *stream);
+
+/* e4m3 [count] -> bf16 [count] (count % 4 == 0), exact.  The weight conversion the FP8
+ * kernels apply, exposed for checking (torch's float8_e4m3fn -> bfloat16 cast). */
+int moss_fp8_to_bf16(const void *w, void *out, long long count, void *stream);
+
 /* --------------------------------------------------- norms, RoPE, SiLU*mul */
 /* Row RMSNorm over n (n % 8 == 0, n <= 8192), bf16 in/out, rounding points of Qwen3RMSNorm.
  * res == NULL: y = rmsnorm(x) (src/moss_tts/_runtime/kernels.py:50-66).

@@ -41,6 +41,9 @@ SIGNATURES: dict[str, list] = {
     "moss_decode_attention_splits": [_I],
     "moss_decode_attention": [_P, _P, _P, _P, _P, _P, _P, _I, _P],
     "moss_embedding_sum": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "moss_fp8_linear": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "moss_fp8_gateup_silu": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "moss_fp8_to_bf16": [_P, _P, ctypes.c_longlong, _P],
 }
 _RESTYPES = {"moss_error_string": ctypes.c_char_p}
 

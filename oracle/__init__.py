@@ -19,8 +19,9 @@ Modules
                ``src/moss_tts/_runtime/dp4a_scaled.py:65-68``)
 ``fp8``        OCP e4m3 weight-only linear (``src/moss_tts/_runtime/fused_mlp.py:7-23``)
 ``attention``  split-K GQA decode attention (``src/moss_tts/_runtime/kernels.py:173-208``)
-``w4a8``       grouped int8 activation quantizer and W4A8 GEMV
-               (``src/moss_tts/_runtime/int4_dp4a.py:21-30``, ``dp4a_scaled.py:22-57``)
+               and the 33-row embedding sum (``src/moss_tts/_runtime/kernels.py:7-26``)
+``decode``     one batch-1 decode step composed from the above
+               (``src/moss_tts/_runtime/llm.py:227-279``)
 ``cref``       ctypes binding of ``oracle/w4g32_ref.c`` (an independent C restatement
                of the byte/integer work, used to cross-check the numpy restatement).
 

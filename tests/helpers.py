@@ -1,0 +1,66 @@
+"""Shared comparison helpers of the GPU parity tests (bars written out in each docstring)."""
+import torch
+
+from oracle import w4g32 as o
+
+ATOL = 1e-2
+RTOL = 1e-2
+
+
+def _assert_close(got, ref, what):
+    got = got.float().cpu()
+    ref = ref.float().cpu()
+    bad = (got - ref).abs() > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{what}: {int(bad.sum())} mismatches, max err {float((got - ref).abs().max())}"
+
+
+def _bits(t):
+    return t.cpu().contiguous().view(torch.int16)
+
+
+def _assert_rne_or_adjacent(got, ref32, abs_sum, k, what):
+    """Exact-dequant outputs are an fp32 dot of the bit-exact bf16 weights with x, so they
+    differ from RNE(oracle fp32) only through fp32 summation order: each must lie within
+    half a bf16 step plus 8 sqrt(K) 2^-24 sum|w x| of the oracle, and at most
+    max(2, 1%) of them may differ from RNE(oracle) at all."""
+    g = got.cpu().float().flatten()
+    r = ref32.float().flatten()
+    gb = got.cpu().contiguous().view(torch.int16).flatten()
+    rb = ref32.bfloat16().contiguous().view(torch.int16).flatten()
+    n_bad = int((gb != rb).sum())
+    assert n_bad <= max(2, int(0.01 * g.numel())), f"{what}: {n_bad} outputs differ from RNE(oracle)"
+    half_step = torch.where(g == 0, torch.zeros_like(g), 2.0 ** (torch.floor(torch.log2(g.abs())) - 8))
+    bound = half_step + 8 * (k ** 0.5) * 2.0 ** -24 * abs_sum.float().flatten()
+    err = (g - r).abs()
+    assert torch.all(err <= bound), f"{what}: max excess {float((err - bound).max())}"
+
+
+def _bf16_choices(v, window=2.0 ** -12):
+    """bf16 roundings of fp32 ``v`` that a different fp32 summation order could produce:
+    the RNE value, plus the other neighbour where ``v`` lies within ``window * |v|`` of the
+    midpoint between them (the GEMV and the oracle sum in different orders, ~1e-6 apart)."""
+    u = v.contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    down = ((u >> 16) << 16).to(torch.int32).view(torch.float32)          # towards zero
+    up = (((u >> 16) + 1) << 16).to(torch.int32).view(torch.float32)      # away from zero
+    rne = v.bfloat16().float()
+    mid = (down + up) / 2
+    near = (v - mid).abs() <= window * v.abs()
+    other = torch.where(rne == down, up, down)
+    return rne, torch.where(near, other, rne)
+
+
+def _assert_epilogue_close(got, gate32, up32, what):
+    """Gate/up outputs: atol/rtol against the oracle's epilogue, where gate and up may take
+    either bf16 rounding when their fp32 value sits on a rounding midpoint."""
+    got = got.float().cpu()[0]
+    gs = _bf16_choices(gate32[0])
+    us = _bf16_choices(up32[0])
+    ok = torch.zeros_like(got, dtype=torch.bool)
+    for g in gs:
+        for u in us:
+            ref = o.silu_mul_rounded(g, u).float()
+            ok |= (got - ref).abs() <= ATOL + RTOL * ref.abs()
+    assert ok.all(), f"{what}: {int((~ok).sum())} outputs outside tolerance"
+    plain = o.silu_mul_rounded(gate32[0], up32[0]).float()
+    strict = (got - plain).abs() <= ATOL + RTOL * plain.abs()
+    assert strict.float().mean() >= 0.999, f"{what}: {int((~strict).sum())} midpoint cases"

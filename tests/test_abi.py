@@ -1,0 +1,82 @@
+"""The C-ABI boundary without a GPU: ``libmoss_hip.so`` loads, exports every function that
+``include/moss_hip.h`` declares, with the parameter count the ctypes binding declares, and
+argument errors come back as ``hipErrorInvalidValue`` before anything is launched."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "moss_hip.h")
+
+
+def _declared() -> dict[str, int]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|const char\s*\*)\s*(moss_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from moss_tts import _build
+    from moss_tts._runtime import native
+
+    if not os.path.exists(native.LIB_PATH):
+        _build.build()
+    return native.lib()
+
+
+def test_header_declares_the_binding():
+    from moss_tts._runtime import native
+
+    decl = _declared()
+    assert len(decl) >= 20
+    assert set(decl) == set(native.SIGNATURES), set(decl) ^ set(native.SIGNATURES)
+    for name, n in decl.items():
+        assert len(native.SIGNATURES[name]) == n, f"{name}: header has {n} parameters"
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from moss_tts._runtime import native
+
+    dyn = subprocess.run(["nm", "-D", "--defined-only", native.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {ln.split()[-1] for ln in dyn.splitlines() if " T " in ln}
+    missing = set(_declared()) - exported
+    assert not missing, f"not exported: {sorted(missing)}"
+    extra = {s for s in exported if s.startswith("moss_")} - set(_declared())
+    assert not extra, f"exported but undeclared: {sorted(extra)}"
+    for name in _declared():
+        assert callable(getattr(lib, name))
+
+
+def test_host_only_entry_points(lib):
+    assert lib.moss_abi_version() == 1
+    assert lib.moss_error_string(0)
+    assert lib.moss_decode_attention_splits(2048) == 32
+    assert lib.moss_decode_attention_splits(96) == 2
+
+
+def test_argument_errors_are_rejected_before_launch(lib):
+    """Null pointers, bad sizes and misalignment return hipErrorInvalidValue (1) on the host;
+    no kernel is launched, so this runs without a GPU."""
+    null = None
+    p = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4097)
+    assert lib.moss_w4g32_gemv(null, p, p, p, p, 1, 4096, 4096, 0, 0, null) == 1
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 2, 4096, 4096, 0, 0, null) == 1          # M must be 1
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4000, 4096, 0, 0, null) == 1          # K % 64
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 3, 0, null) == 1          # rows_per_wave
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 0, 7, null) == 1          # dequant mode
+    assert lib.moss_w4g32_gemm(odd, p, p, p, p, 64, 4096, 4096, null) == 1             # alignment
+    assert lib.moss_fp8_linear(p, p, null, p, 1, 4100, 64, 0, null) == 1                # K % 16
+    assert lib.moss_fp8_linear(p, p, null, p, 2, 4112, 64, 0, null) == 1                # GEMM K % 64
+    assert lib.moss_fp8_gateup_silu(p, p, null, p, 2, 4096, 64, 0, null) == 1           # M must be 1
+    assert lib.moss_fp8_to_bf16(p, p, 6, null) == 1                                     # count % 4
+    assert lib.moss_rmsnorm(p, null, p, null, p, 1, 8200, ctypes.c_float(1e-6), null) == 1   # n <= 8192
