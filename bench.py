@@ -32,6 +32,7 @@ for _p in (os.path.join(ROOT, "moss-tts-optimized_amd"), ROOT):
 
 METRIC = "INT4-G32 GEMV HBM GB/s (% of peak) + 36-layer decode-step ms at bs=1"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER = 4096, 12288
 
 
@@ -144,6 +145,67 @@ def cpu_baseline(torch, budget_s: float):
             "ms_per_step": round(med * 1e3, 3)}
 
 
+def _per_launch(torch, fns, replays: int = 20) -> float:
+    """Seconds per launch of ``fns`` (one launch each) captured into one HIP graph."""
+    graph = _capture(torch, lambda: [f() for f in fns])
+    return _time_graph(torch, graph, replays) / len(fns)
+
+
+def fp8_bench(torch, dev):
+    """FP8 E4M3 weight-only linear, K=4096, N in {4096, 12288}, M in {1, 64}, fp32 row scales;
+    weights rotated over >= 600 MB of distinct copies so HBM, not the Infinity Cache, serves
+    them.  Also the fused gate||up FP8 GEMV (N = 2 x 12288)."""
+    from moss_tts._runtime import fp8
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(99)
+    for n in (4096, 12288, 24576):
+        k = HIDDEN
+        copies = max(2, int(640e6 // (n * k)))
+        ws = [torch.randint(0, 256, (n, k), generator=gen, device=dev, dtype=torch.uint8) & 0xF7
+              for _ in range(copies)]
+        ss = [torch.rand(n, generator=gen, device=dev) for _ in range(copies)]
+        for m in ((1, 64) if n != 24576 else (1,)):
+            x = torch.randn((m, k), generator=gen, device=dev).bfloat16()
+            if n == 24576:
+                sec = _per_launch(torch, [lambda i=i: fp8.fp8_silu_decode(x, ws[i], ss[i]) for i in range(copies)])
+                key = "fp8_gateup_silu_k4096_n24576"
+                nbytes = n * k + 4 * n + 2 * k + 2 * n // 2
+            else:
+                sec = _per_launch(torch, [lambda i=i: fp8.linear(x, ws[i], ss[i]) for i in range(copies)])
+                key = f"fp8_linear_m{m}_k4096_n{n}"
+                nbytes = n * k + 4 * n + 2 * m * k + 2 * m * n
+            gbs = nbytes / sec / 1e9
+            out[key] = {"us_per_call": round(sec * 1e6, 3), "GB/s": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                        "TFLOP/s": round(2 * m * k * n / sec / 1e12, 2), "bytes": nbytes}
+            _log(f"[bench] {key}: {sec * 1e6:.2f} us, {gbs:.0f} GB/s")
+        del ws, ss
+        torch.cuda.empty_cache()
+    return out
+
+
+def prefill_bench(torch, dev):
+    """INT4-G32 prefill GEMMs at M=512 (QKV N=6144, O N=4096, gate||up N=24576, down K=12288):
+    TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak."""
+    from moss_tts._runtime import w4g32
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(98)
+    x = torch.randn((512, INTER), generator=gen, device=dev).bfloat16()
+    for name, k, n in (("qkv", HIDDEN, 6144), ("o", HIDDEN, HIDDEN), ("gate_up", HIDDEN, 2 * INTER),
+                       ("down", INTER, HIDDEN)):
+        pw = _quantized(torch, w4g32, n, k, gen, dev)
+        xk = x[:, :k].contiguous()
+        sec = _per_launch(torch, [lambda: w4g32.gemm(xk, pw)] * 8, replays=10)
+        tf = 2 * 512 * k * n / sec / 1e12
+        out[f"gemm_m512_{name}_k{k}_n{n}"] = {"us_per_call": round(sec * 1e6, 2), "TFLOP/s": round(tf, 1),
+                                               "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        _log(f"[bench] prefill GEMM M=512 {name}: {sec * 1e6:.1f} us, {tf:.0f} TFLOP/s")
+        del pw
+    return out
+
+
 def decode_step_bench(torch, n_layers: int, steps: int, dev):
     """The full batch-1 decode step (embedding -> n_layers -> 32 INT4 heads, KV cache of 2048
     rows filled with N(0,1), current position 2047) captured as one graph; ms per step."""
@@ -184,9 +246,11 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=30,
                     help="timed replays of the 36-layer decode step (0 skips it)")
     ap.add_argument("--decode-layers", type=int, default=36)
-    ap.add_argument("--pmc-pass", action="store_true",
-                    help="eager launches only (for rocprofv3 --pmc): a 512 MiB copy of known size, then "
-                         "one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy")
+    ap.add_argument("--no-extras", action="store_true", help="skip the FP8 and prefill GEMM lines")
+    ap.add_argument("--pmc-pass", choices=("gemv", "gemm"), default=None,
+                    help="eager launches only, for rocprofv3 --pmc: 'gemv' = a 512 MiB copy of known size, "
+                         "then one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy; "
+                         "'gemm' = the four M=512 prefill GEMMs once each")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -218,7 +282,19 @@ def main() -> int:
     resident = sum(gu.nbytes + dn.nbytes for gu, dn in copies)
     _log(f"[bench] {resident / 2**20:.0f} MiB of packed MLP weights resident")
 
-    if args.pmc_pass:
+    if args.pmc_pass == "gemm":
+        del copies
+        torch.cuda.empty_cache()
+        x = torch.randn((512, INTER), generator=gen, device=dev).bfloat16()
+        for k, n in ((HIDDEN, 6144), (HIDDEN, HIDDEN), (HIDDEN, 2 * INTER), (INTER, HIDDEN)):
+            pw = _quantized(torch, w4g32, n, k, gen, dev)
+            xk = x[:, :k].contiguous()
+            torch.cuda.synchronize()
+            w4g32.gemm(xk, pw)
+            torch.cuda.synchronize()
+            _log(f"[bench] pmc pass: GEMM M=512 K={k} N={n} ({2 * 512 * k * n} flop)")
+        return 0
+    if args.pmc_pass == "gemv":
         src = torch.empty(512 * 2**20 // 4, dtype=torch.int32, device=dev).fill_(1)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -305,10 +381,12 @@ def main() -> int:
          f"down K=12288 N=4096: {dn_s * 1e6:.2f} us, {DOWN_BYTES / dn_s / 1e9:.0f} GB/s")
 
     n_copies = len(copies)
+    del copies, gemv_copies, g_cycle, g_unr, g_rem
+    torch.cuda.empty_cache()
+    fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
+    prefill = prefill_bench(torch, dev) if not args.no_extras else None
     decode = None
-    if args.decode_steps > 0 and not args.pmc_pass:
-        del copies, gemv_copies, g_cycle, g_unr
-        torch.cuda.empty_cache()
+    if args.decode_steps > 0:
         decode = decode_step_bench(torch, args.decode_layers, args.decode_steps, dev)
 
     cpu = None
@@ -343,7 +421,7 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "w4g32_gemv_kernel<KG=2,R=2,PAIRED> (fused gate||up + SiLU*mul)",
+            "kernel": "w4g32_gateup_silu_exact<2, 2, true> (fused gate||up GEMV + SiLU*mul)",
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -368,6 +446,8 @@ def main() -> int:
                                        "GB/s": round(DOWN_BYTES / dn_s / 1e9, 1)},
             "wall_s_timed_region": round(wall, 4),
             "decode_step": decode,
+            "fp8": fp8_lines,
+            "prefill_gemm": prefill,
         },
     }
     print(json.dumps(line), flush=True)

@@ -176,11 +176,9 @@ __device__ __forceinline__ void load_row_nt(RowLoad<KG>& r, const uint4* __restr
 
 // n_out output rows; PAIRED reads gate row n and up row n + n_out.
 template <int KG, int R, bool PAIRED, bool FULL, bool EXACT>
-__global__ __launch_bounds__(256) void w4g32_gemv_kernel(const uint16_t* __restrict__ x,
-                                                         const uint4* __restrict__ qw,
-                                                         const uint16_t* __restrict__ sc,
-                                                         const uint8_t* __restrict__ zp,
-                                                         uint16_t* __restrict__ y, int G, int n_out) {
+__device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,
+                                          const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                          uint16_t* __restrict__ y, int G, int n_out) {
     const int lane = threadIdx.x & (kWave - 1);
     // wave-uniform: lets row addressing run on the scalar unit
     const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
@@ -334,11 +332,9 @@ __device__ __forceinline__ void load_row_slice(RowLoad<2>& r, const uint4* __res
 }
 
 template <int W, int R, bool PAIRED, bool EXACT>
-__global__ __launch_bounds__(64 * W) void w4g32_gemv_ksplit(const uint16_t* __restrict__ x,
-                                                            const uint4* __restrict__ qw,
-                                                            const uint16_t* __restrict__ sc,
-                                                            const uint8_t* __restrict__ zp,
-                                                            uint16_t* __restrict__ y, int G, int n_out) {
+__device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,
+                                            const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                            uint16_t* __restrict__ y, int G, int n_out) {
     constexpr int NR = PAIRED ? 2 * R : R;
     __shared__ float part[W][NR];
     const int lane = threadIdx.x & (kWave - 1);
@@ -377,6 +373,57 @@ __global__ __launch_bounds__(64 * W) void w4g32_gemv_ksplit(const uint16_t* __re
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Entry kernels: one name per (role, dequant mode), so profiles tell them apart.
+#define MOSS_ROWS_ENTRY(NAME, PAIRED, EXACT)                                                                 \
+    template <int KG, int R, bool FULL>                                                                      \
+    __global__ __launch_bounds__(256) void NAME(const uint16_t* __restrict__ x, const uint4* __restrict__ qw, \
+                                                const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp, \
+                                                uint16_t* __restrict__ y, int G, int n_out) {                   \
+        gemv_rows<KG, R, PAIRED, FULL, EXACT>(x, qw, sc, zp, y, G, n_out);                                   \
+    }
+MOSS_ROWS_ENTRY(w4g32_gemv_exact, false, true)
+MOSS_ROWS_ENTRY(w4g32_gemv_unrounded, false, false)
+MOSS_ROWS_ENTRY(w4g32_gateup_silu_exact, true, true)
+MOSS_ROWS_ENTRY(w4g32_gateup_silu_unrounded, true, false)
+#undef MOSS_ROWS_ENTRY
+
+#define MOSS_KSPLIT_ENTRY(NAME, PAIRED, EXACT)                                                                  \
+    template <int W, int R>                                                                                     \
+    __global__ __launch_bounds__(64 * W) void NAME(const uint16_t* __restrict__ x, const uint4* __restrict__ qw, \
+                                                   const uint16_t* __restrict__ sc,                             \
+                                                   const uint8_t* __restrict__ zp, uint16_t* __restrict__ y,    \
+                                                   int G, int n_out) {                                          \
+        gemv_ksplit<W, R, PAIRED, EXACT>(x, qw, sc, zp, y, G, n_out);                                           \
+    }
+MOSS_KSPLIT_ENTRY(w4g32_gemv_ksplit_exact, false, true)
+MOSS_KSPLIT_ENTRY(w4g32_gemv_ksplit_unrounded, false, false)
+MOSS_KSPLIT_ENTRY(w4g32_gateup_silu_ksplit_exact, true, true)
+MOSS_KSPLIT_ENTRY(w4g32_gateup_silu_ksplit_unrounded, true, false)
+#undef MOSS_KSPLIT_ENTRY
+
+template <int KG, int R, bool PAIRED, bool FULL, bool EXACT>
+constexpr auto rows_kernel() {
+    if constexpr (PAIRED) {
+        if constexpr (EXACT) return &w4g32_gateup_silu_exact<KG, R, FULL>;
+        else return &w4g32_gateup_silu_unrounded<KG, R, FULL>;
+    } else {
+        if constexpr (EXACT) return &w4g32_gemv_exact<KG, R, FULL>;
+        else return &w4g32_gemv_unrounded<KG, R, FULL>;
+    }
+}
+
+template <int W, int R, bool PAIRED, bool EXACT>
+constexpr auto ksplit_kernel() {
+    if constexpr (PAIRED) {
+        if constexpr (EXACT) return &w4g32_gateup_silu_ksplit_exact<W, R>;
+        else return &w4g32_gateup_silu_ksplit_unrounded<W, R>;
+    } else {
+        if constexpr (EXACT) return &w4g32_gemv_ksplit_exact<W, R>;
+        else return &w4g32_gemv_ksplit_unrounded<W, R>;
+    }
+}
+
 template <bool PAIRED, bool EXACT>
 int launch_ksplit(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
                   int rows, hipStream_t st) {
@@ -390,7 +437,7 @@ int launch_ksplit(const void* x, const void* qw, const void* sc, const void* zp,
     auto* yp = (uint16_t*)y;
 #define MOSS_KS(WV, RV)                                                                                      \
     if (W == WV && rows == RV) {                                                                             \
-        hipLaunchKernelGGL((w4g32_gemv_ksplit<WV, RV, PAIRED, EXACT>), grid, dim3(64 * WV), 0, st, xp, qp, sp, \
+        hipLaunchKernelGGL((ksplit_kernel<WV, RV, PAIRED, EXACT>()), grid, dim3(64 * WV), 0, st, xp, qp, sp, \
                            zpp, yp, G, n_out);                                                               \
         return moss_launch_status();                                                                         \
     }
@@ -454,10 +501,10 @@ int launch_rows(const void* x, const void* qw, const void* sc, const void* zp, v
 #define MOSS_KG_CASE(KGV)                                                                                          \
     case KGV:                                                                                                      \
         if (full)                                                                                                  \
-            hipLaunchKernelGGL((w4g32_gemv_kernel<KGV, R, PAIRED, (KGV % 2 == 0), EXACT>), grid, block, 0, st, xp, qp, sp, \
+            hipLaunchKernelGGL((rows_kernel<KGV, R, PAIRED, (KGV % 2 == 0), EXACT>()), grid, block, 0, st, xp, qp, sp, \
                                zpp, yp, G, n_out);                                                                 \
         else                                                                                                       \
-            hipLaunchKernelGGL((w4g32_gemv_kernel<KGV, R, PAIRED, false, EXACT>), grid, block, 0, st, xp, qp, sp, zpp, yp, \
+            hipLaunchKernelGGL((rows_kernel<KGV, R, PAIRED, false, EXACT>()), grid, block, 0, st, xp, qp, sp, zpp, yp, \
                                G, n_out);                                                                          \
         break;
         MOSS_KG_CASE(1)
