@@ -136,6 +136,36 @@ class DecodeStepG32:
         kv = len(self.layers) * 2 * KH * (position + 1) * HD * 2
         return self.weight_bytes + kv + (CODEBOOKS + 1) * HIDDEN * 2
 
+    # ------------------------------------------------------------ installed model
+    @classmethod
+    @torch.no_grad()
+    def from_model(cls, model, *, max_length: int, dequant: int = w4g32.EXACT) -> "DecodeStepG32":
+        """The decode step of a MOSS-TTS model after ``install_gptq``: its quantized projections,
+        norm weights and embeddings as they are (no copies); the 32 audio heads (rows
+        ``[:1024]`` of ``lm_heads[1:]``, ``src/moss_tts/_runtime/llm.py:188-191``) concatenated
+        and min-max quantized to INT4-G32 here (the reference keeps them bf16)."""
+        lm = model.language_model
+        layers = []
+        for i, layer in enumerate(lm.layers):
+            a, m = layer.self_attn, layer.mlp
+            if not (isinstance(getattr(a, "qkv_proj", None), QuantLinearG32)
+                    and isinstance(getattr(m, "gate_up_proj", None), QuantGateUpG32)):
+                raise ValueError(f"layer {i} has no installed quantized projections (run install_gptq first)")
+            layers.append(DecoderLayerG32(a.qkv_proj, a.o_proj, m.gate_up_proj, m.down_proj,
+                                          layer.input_layernorm.weight, layer.post_attention_layernorm.weight,
+                                          a.q_norm.weight, a.k_norm.weight))
+        cfg = getattr(model, "config", None)
+        lc = getattr(cfg, "language_config", None)
+        eps = float(getattr(lc, "rms_norm_eps", 1e-6)) if lc is not None else 1e-6
+        theta = getattr(lc, "rope_theta", None) if lc is not None else None
+        if theta is None and lc is not None:
+            theta = (getattr(lc, "rope_parameters", None) or {}).get("rope_theta")
+        heads_bf16 = torch.cat([h.weight[:AUDIO_VOCAB - 1] for h in model.lm_heads[1:]], 0)
+        heads = QuantLinearG32(w4g32.quantize_minmax(heads_bf16.float().contiguous()), dequant=dequant)
+        audio = torch.stack([e.weight for e in model.emb_ext]).contiguous()
+        return cls(layers, lm.norm.weight, heads, lm.embed_tokens.weight.contiguous(), audio,
+                   max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6)
+
     # -------------------------------------------------------------- synthetic model
     @classmethod
     @torch.inference_mode()

@@ -1,0 +1,148 @@
+"""Public entry point: ``MossTTS.from_pretrained(preset="gptq", calibration_path=...)``.
+
+Signature, argument meaning and the configuration errors raised before anything is loaded
+follow the reference (``src/moss_tts/api.py:36-99``; its checks are pinned by
+``tests/test_api.py:101-114``).  The SM90 / Triton / nvcc checks of the reference
+(``api.py:79-82,99``) become a gfx950 device check and a check that ``libmoss_hip.so`` loads.
+What this library provides after loading is the INT4-G32 decode path: the model's projections
+swapped for quantized modules (``install_gptq``) and the batch-1 decode step captured as one
+HIP graph (``step``).  The streaming product loop, codec and voice cloning of the reference
+are not part of it.
+"""
+from __future__ import annotations
+
+import threading
+from contextlib import contextmanager
+from pathlib import Path
+from typing import Literal
+
+
+class GptqEngine:
+    """The installed model plus its decode step (``DecodeStepG32``)."""
+
+    def __init__(self, model, *, max_length: int):
+        from ._runtime.decode import DecodeStepG32
+
+        self.model = model
+        self.max_length = max_length
+        self.decode = DecodeStepG32.from_model(model, max_length=max_length)
+
+    @property
+    def graph(self):
+        return self.decode.graph
+
+    def warmup(self) -> None:
+        self.decode.capture()
+
+    def step(self, ids, position: int):
+        return self.decode.step(ids, position)
+
+
+class MossTTS:
+    """One HIP device, one active request, all 32 acoustic codebooks."""
+
+    sample_rate = 48000
+    codebooks = 32
+
+    def __init__(self, engine, *, device, preset: str):
+        self._engine = engine
+        self.device = device
+        self.preset = preset
+        self._lock = threading.Lock()
+        self._closed = False
+
+    @classmethod
+    def from_pretrained(
+        cls,
+        *,
+        preset: Literal["bf16", "gptq"] = "bf16",
+        calibration_path: str | Path | None = None,
+        device: str = "cuda:0",
+        cache_dir: str | Path | None = None,
+        local_files_only: bool = False,
+        max_length: int = 1024,
+        cpu_threads: int = 4,
+        model=None,
+    ) -> "MossTTS":
+        """Validate the configuration, install the calibrated export into ``model`` and capture
+        the decode graph.  ``model`` is an already loaded MOSS-TTS model on ``device`` (this
+        library does not download checkpoints)."""
+        if preset not in ("bf16", "gptq"):
+            raise ValueError("preset must be 'bf16' or 'gptq'")
+        if (preset == "gptq") != (calibration_path is not None):
+            raise ValueError("Provide calibration_path exactly when preset='gptq'")
+        if not isinstance(max_length, int) or max_length < 128 or max_length % 128:
+            raise ValueError("max_length must be a positive multiple of 128")
+        if preset == "gptq" and max_length != 1024:
+            raise ValueError("Bundled gptq kernels require max_length=1024")
+        if not isinstance(cpu_threads, int) or cpu_threads < 1:
+            raise ValueError("cpu_threads must be positive")
+        if preset != "gptq":
+            raise ValueError("This library provides the 'gptq' (INT4-G32) preset only")
+        from ._runtime import export
+
+        export.read_config(calibration_path)
+
+        import torch
+
+        target = torch.device(device)
+        if target.type != "cuda" or not torch.cuda.is_available():
+            raise RuntimeError("MOSS-TTS 8B on this library requires an AMD Instinct MI355X (gfx950) HIP device")
+        if target.index is None:
+            target = torch.device("cuda", torch.cuda.current_device())
+        from ._runtime import native
+
+        native.lib()  # raises when libmoss_hip.so is not built
+        try:
+            native.device_arch(target.index)
+        except RuntimeError as exc:
+            raise ValueError(f"The gptq preset is qualified for gfx950 (MI355X) only: {exc}") from None
+
+        if model is None:
+            from .models import load_models
+
+            model = load_models(cache_dir=cache_dir, local_files_only=local_files_only)
+        from ._runtime.presets import install_gptq
+
+        torch.set_num_threads(cpu_threads)
+        with torch.cuda.device(target):
+            install_gptq(model, calibration_path)
+            engine = GptqEngine(model, max_length=max_length)
+            engine.warmup()
+        return cls(engine, device=target, preset=preset)
+
+    @contextmanager
+    def _request(self):
+        if not self._lock.acquire(blocking=False):
+            raise RuntimeError("This model is busy; finish or close the active stream first")
+        try:
+            if self._closed:
+                raise RuntimeError("This model is closed")
+            yield
+        finally:
+            self._lock.release()
+
+    def step(self, ids, position: int):
+        """One batch-1 decode step: ``ids`` int64 ``[1, 33]`` (text token, 32 codebook codes) at
+        cache row ``position`` -> audio logits bf16 ``[32 * 1024]`` (a view of the graph's
+        output buffer, valid until the next step)."""
+        with self._request():
+            return self._engine.step(ids, position)
+
+    @property
+    def engine(self):
+        return self._engine
+
+    def close(self) -> None:
+        if not self._lock.acquire(blocking=False):
+            raise RuntimeError("Close the active stream before closing the model")
+        try:
+            self._closed = True
+        finally:
+            self._lock.release()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

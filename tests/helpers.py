@@ -64,3 +64,30 @@ def _assert_epilogue_close(got, gate32, up32, what):
     plain = o.silu_mul_rounded(gate32[0], up32[0]).float()
     strict = (got - plain).abs() <= ATOL + RTOL * plain.abs()
     assert strict.float().mean() >= 0.999, f"{what}: {int((~strict).sum())} midpoint cases"
+
+
+def write_export(folder, weights, *, n_layers, revision=None, complete=True, record_sha=True):
+    """Write a calibrated export in the reference's format (``src/moss_tts/calibration.py:156-212``)
+    from fp32 weights ``{(layer, name): [N, K]}``: static bf16 absmax/7 scales, round-to-nearest
+    codes in [-7, 7], two's-complement nibbles.  Returns ``{(layer, name): (codes, scales)}``."""
+    import hashlib
+    import json
+    from pathlib import Path
+
+    from moss_tts.models import TTS_REVISION
+
+    folder = Path(folder)
+    folder.mkdir(parents=True, exist_ok=True)
+    config = {"complete": complete, "group": 32, "tts_revision": revision or TTS_REVISION, "projections": {}}
+    out = {}
+    for (layer, name), w in weights.items():
+        s = o.static_scales(w)
+        c = o.quantize_symmetric(w, s)
+        path = folder / f"{layer:02d}_{name}.pt"
+        torch.save({"packed": o.pack_signed(c), "scales": s, "shape": list(w.shape), "group": 32}, path)
+        if record_sha:
+            config["projections"][f"{layer:02d}_{name}"] = {"sha256": hashlib.sha256(path.read_bytes()).hexdigest()}
+        out[layer, name] = (c, s)
+    assert n_layers * 4 == len(weights)
+    (folder / "config.json").write_text(json.dumps(config))
+    return out
