@@ -2,15 +2,15 @@
 """Benchmark: the INT4-G32 quantized-linear path on one MI355X.
 
 Step (the headline workload): one batch-1 decoder MLP pass, INT4 group-32 weights --
-RMSNorm(4096, eps 1e-6) -> fused gate||up GEMV K=4096 -> N=2x12288 with the SiLU*mul
-epilogue -> down GEMV K=12288 -> N=4096.  ``value`` is algorithmic HBM bytes per step
+RMSNorm(4096, eps 1e-6) + fused gate||up GEMV K=4096 -> N=2x12288 with the SiLU*mul
+epilogue (one kernel) -> down GEMV K=12288 -> N=4096.  ``value`` is algorithmic HBM bytes per step
 (87,359,488 B: packed codes + bf16 scales + 4-bit zeros + activations in/out) divided by
 the measured time per step, in GB/s.  Inputs are resident in HBM; the steps rotate over
 ``--copies`` distinct weight copies (>= 512 MiB in total) so the 256 MiB Infinity Cache
 cannot serve them, and are replayed from one HIP graph.
 
 The JSON line also carries:
-  roofline      the dominant kernel (fused gate||up GEMV) timed alone with HIP events on its
+  roofline      the dominant kernel (RMSNorm + fused gate||up GEMV) timed alone with HIP events on its
                 launch stream: achieved GB/s on its algorithmic bytes vs the 8 TB/s HBM peak;
                 ``traffic`` comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in
                 profiles/ when present
@@ -46,6 +46,7 @@ GATEUP_BYTES = gemv_bytes(HIDDEN, 2 * INTER) - 2 * 2 * INTER + 2 * INTER   # out
 DOWN_BYTES = gemv_bytes(INTER, HIDDEN)
 MLP_BYTES = GATEUP_BYTES + DOWN_BYTES                                      # 87,359,488
 NORM_BYTES = 3 * 2 * HIDDEN                                                # x, weight, y
+NORM_GATEUP_BYTES = GATEUP_BYTES + 2 * HIDDEN                              # + the RMSNorm weight
 
 
 def _log(msg: str) -> None:
@@ -302,13 +303,13 @@ def main() -> int:
         torch.cuda.synchronize()
         xs = pointwise.rmsnorm(h, norm_w, 1e-6)
         for gu, _ in copies:
-            w4g32.gateup_silu(xs, gu)
+            w4g32.norm_gateup_silu(h, norm_w, 1e-6, gu)
         torch.cuda.synchronize()
         for gu, _ in copies:
             w4g32.gemv(xs, gu.rows(0, INTER))
         torch.cuda.synchronize()
         _log(f"[bench] pmc pass done: copy {src.numel() * 4} B; {len(copies)} gate||up launches "
-             f"({GATEUP_BYTES} algorithmic B each); {len(copies)} GEMV K=4096 N=12288 launches "
+             f"({NORM_GATEUP_BYTES} algorithmic B each); {len(copies)} GEMV K=4096 N=12288 launches "
              f"({gemv_bytes(HIDDEN, INTER)} B each)")
         return 0
 
@@ -316,8 +317,7 @@ def main() -> int:
         def run():
             for i in range(count):
                 gu, dn = copies[(offset + i) % len(copies)]
-                x = pointwise.rmsnorm(h, norm_w, 1e-6)
-                a = w4g32.gateup_silu(x, gu, dequant=dequant)
+                a = w4g32.norm_gateup_silu(h, norm_w, 1e-6, gu, dequant=dequant)
                 w4g32.gemv(a, dn, dequant=dequant)
         return run
 
@@ -361,10 +361,10 @@ def main() -> int:
         graph = _capture(torch, fn)
         return _time_graph(torch, graph, 50) / launches
 
-    gu_s = per_launch(lambda: [w4g32.gateup_silu(xs, gu) for gu, _ in copies], len(copies))
-    gu_gbs = GATEUP_BYTES / gu_s / 1e9
-    gu_unr_s = per_launch(lambda: [w4g32.gateup_silu(xs, gu, dequant=w4g32.UNROUNDED) for gu, _ in copies],
-                          len(copies))
+    gu_s = per_launch(lambda: [w4g32.norm_gateup_silu(h, norm_w, 1e-6, gu) for gu, _ in copies], len(copies))
+    gu_gbs = NORM_GATEUP_BYTES / gu_s / 1e9
+    gu_unr_s = per_launch(lambda: [w4g32.norm_gateup_silu(h, norm_w, 1e-6, gu, dequant=w4g32.UNROUNDED)
+                                   for gu, _ in copies], len(copies))
     _log(f"[bench] gate||up GEMV: {gu_s * 1e6:.2f} us/launch, {gu_gbs:.0f} GB/s "
          f"(unrounded {gu_unr_s * 1e6:.2f} us)")
 
@@ -421,14 +421,14 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "w4g32_gateup_silu_exact<2, 2, true> (fused gate||up GEMV + SiLU*mul)",
+            "kernel": "w4g32_norm_gateup_silu_exact<2, 2, true> (RMSNorm + gate||up GEMV + SiLU*mul, one kernel)",
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
             "traffic": _traffic(),
-            "algorithmic_bytes_per_launch": GATEUP_BYTES,
+            "algorithmic_bytes_per_launch": NORM_GATEUP_BYTES,
             "us_per_launch": round(gu_s * 1e6, 3),
         },
         "cpu_baseline": cpu,
@@ -440,7 +440,7 @@ def main() -> int:
                                             "GB/s": round(ns_bytes / ns_unr_s / 1e9, 1),
                                             "frac_of_peak": round(ns_bytes / ns_unr_s / 1e9 / HBM_PEAK_GBS, 4)},
             "gateup_unrounded": {"us_per_call": round(gu_unr_s * 1e6, 3),
-                                 "GB/s": round(GATEUP_BYTES / gu_unr_s / 1e9, 1)},
+                                 "GB/s": round(NORM_GATEUP_BYTES / gu_unr_s / 1e9, 1)},
             "mlp_step_unrounded": {"us_per_step": round(unr_s * 1e6, 3), "GB/s": round(MLP_BYTES / unr_s / 1e9, 1)},
             "gemv_down_k12288_n4096": {"us_per_call": round(dn_s * 1e6, 3),
                                        "GB/s": round(DOWN_BYTES / dn_s / 1e9, 1)},

@@ -82,6 +82,24 @@ int moss_w4g32_gemv(const void *x, const void *qw, const void *sc, const void *z
 int moss_w4g32_gateup_silu(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K,
                            int N_half, int rows_per_wave, int dequant_mode, void *stream);
 
+/* Fused (add+)RMSNorm + decode GEMV: the projection's input is normalized inside the kernel
+ * (each workgroup recomputes it into LDS while its weight loads are in flight).
+ * res == NULL:  xn = rmsnorm(x) * norm_w;
+ * res != NULL:  s = bf16(x + res) is stored to sum_out (which must not overlap x or res) and
+ *               xn = rmsnorm(s) * norm_w.
+ * Rounding points and summation order are those of moss_rmsnorm, so the result is bit-identical
+ * to moss_rmsnorm followed by moss_w4g32_gemv.  K % 2048 == 0, K <= 8192, M is 1.
+ * Replaces the fused add+RMSNorm+quant+projection of
+ * src/moss_tts/_runtime/dp4a_norm_projection.py:48-166 (and gateup_cluster.py:44-157). */
+int moss_w4g32_norm_gemv(const void *x, const void *res, const void *norm_w, void *sum_out, float eps, const void *qw,
+                         const void *sc, const void *zp, void *y, int K, int N, int rows_per_wave, int dequant_mode,
+                         void *stream);
+
+/* The same in front of the fused gate||up GEMV with the SiLU*mul epilogue (W has 2*N_half rows). */
+int moss_w4g32_norm_gateup_silu(const void *x, const void *res, const void *norm_w, void *sum_out, float eps,
+                                const void *qw, const void *sc, const void *zp, void *y, int K, int N_half,
+                                int rows_per_wave, int dequant_mode, void *stream);
+
 /* ------------------------------------------------------------- prefill GEMM */
 /* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);
  * weights are dequantized bit-exactly (bf16_rne((q-z)*s)) into LDS and multiplied with

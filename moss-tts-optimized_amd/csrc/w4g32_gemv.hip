@@ -169,54 +169,7 @@ __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int KG, bool FULL>
-__device__ __forceinline__ void load_row_nt(RowLoad<KG>& r, const uint4* __restrict__ qw,
-                                            const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-                                            int n, int lane, int G);
-
-// n_out output rows; PAIRED reads gate row n and up row n + n_out.
-template <int KG, int R, bool PAIRED, bool FULL, bool EXACT>
-__device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,
-                                          const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-                                          uint16_t* __restrict__ y, int G, int n_out) {
-    const int lane = threadIdx.x & (kWave - 1);
-    // wave-uniform: lets row addressing run on the scalar unit
-    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
-    const int row0 = wave * R;
-    if (row0 >= n_out) return;  // wave-uniform
-
-    constexpr int NR = PAIRED ? 2 * R : R;
-    RowLoad<KG> rows[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        const int local = PAIRED ? (r % R) : r;
-        const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
-        load_row_nt<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
-    }
-    XSlice<KG> xs;
-    load_x<KG, !EXACT, FULL>(xs, x, lane, G);
-
-    const Magic m = make_magic();
-    float out[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r)
-        out[r] = wave_sum(EXACT ? row_partial_exact(xs, rows[r], m) : row_partial_unrounded(xs, rows[r], m));
-
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = row0 + r;
-            if (n < n_out) y[n] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------
-// Streaming variant: a fixed grid of waves, each walking rows n = wave, wave + stride, ...
-// with the next row's codes/scales/zeros loaded (non-temporally: read once, never reused)
-// while the current row is computed, so VALU work overlaps the HBM stream instead of
-// bunching up after it.
-
+// Non-temporal loads: every weight byte is read once.
 template <int KG, bool FULL>
 __device__ __forceinline__ void load_row_nt(RowLoad<KG>& r, const uint4* __restrict__ qw,
                                             const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
@@ -254,52 +207,135 @@ __device__ __forceinline__ void load_row_nt(RowLoad<KG>& r, const uint4* __restr
     }
 }
 
-template <int KG, bool PAIRED, bool FULL, bool EXACT>
-__device__ __forceinline__ void stream_row(const XSlice<KG>& xs, const RowLoad<KG>* rows, Magic m, int n, int lane,
-                                           uint16_t* __restrict__ y) {
-    const float a = wave_sum(EXACT ? row_partial_exact(xs, rows[0], m) : row_partial_unrounded(xs, rows[0], m));
-    if constexpr (PAIRED) {
-        const float b = wave_sum(EXACT ? row_partial_exact(xs, rows[1], m) : row_partial_unrounded(xs, rows[1], m));
-        if (lane == 0) y[n] = silu_mul_bf16(a, b);
-    } else {
-        if (lane == 0) y[n] = f32_to_bf16(a);
+
+// Fused normalization in front of the projection (the reference's fused add+RMSNorm+projection,
+// src/moss_tts/_runtime/dp4a_norm_projection.py:48-96, with the rounding points of
+// src/moss_tts/_runtime/kernels.py:50-90):
+//   NORM 1: xn = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)
+//   NORM 2: s = bf16(x + res), xn = the same on s; workgroup 0 also stores s to sum_out.
+// Every workgroup (256 threads) recomputes it from the 8 KB row (an L2 hit) into LDS while its
+// weight loads are in flight; thread t owns 8-value chunks t + 256 c, c < K / 2048, exactly
+// as rmsnorm_rows does, so the normalized row is bit-identical to moss_rmsnorm's.
+struct NormArgs {
+    const uint16_t* __restrict__ res;
+    const uint16_t* __restrict__ w;
+    uint16_t* __restrict__ sum_out;
+    float eps;
+};
+
+template <int CH>
+struct NormLoad {
+    uint4 x[CH], r[CH], w[CH];
+};
+
+// Issued before the weight-row loads: vector-memory completions are counted in order, so the
+// normalization below then waits only for these and overlaps the weight stream.
+template <int NORM, int CH>
+__device__ __forceinline__ void norm_load(NormLoad<CH>& nl, const uint16_t* __restrict__ x, const NormArgs& na) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int ci = t + 256 * c;
+        nl.x[c] = reinterpret_cast<const uint4*>(x)[ci];
+        if constexpr (NORM == 2) nl.r[c] = reinterpret_cast<const uint4*>(na.res)[ci];
+        nl.w[c] = reinterpret_cast<const uint4*>(na.w)[ci];
     }
 }
 
-template <int KG, bool PAIRED, bool FULL, bool EXACT>
-__global__ __launch_bounds__(256) void w4g32_gemv_stream(const uint16_t* __restrict__ x,
-                                                         const uint4* __restrict__ qw,
-                                                         const uint16_t* __restrict__ sc,
-                                                         const uint8_t* __restrict__ zp,
-                                                         uint16_t* __restrict__ y, int G, int n_out) {
+template <int NORM, int CH>
+__device__ __forceinline__ void norm_into_lds(const NormLoad<CH>& nl, const NormArgs& na, uint16_t* xn, float* red,
+                                              int K) {
+    const int t = threadIdx.x;
+    float v[CH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int ci = t + 256 * c;
+        uint32_t sw[4] = {nl.x[c].x, nl.x[c].y, nl.x[c].z, nl.x[c].w};
+        if constexpr (NORM == 2) {
+            const uint32_t bw[4] = {nl.r[c].x, nl.r[c].y, nl.r[c].z, nl.r[c].w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t lo = f32_to_bf16(bf16_lo(sw[p]) + bf16_lo(bw[p]));
+                const uint32_t hi = f32_to_bf16(bf16_hi(sw[p]) + bf16_hi(bw[p]));
+                sw[p] = lo | (hi << 16);
+            }
+            if (blockIdx.x == 0)
+                reinterpret_cast<uint4*>(na.sum_out)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            v[c][2 * p] = bf16_lo(sw[p]);
+            v[c][2 * p + 1] = bf16_hi(sw[p]);
+            ss = fmaf(v[c][2 * p], v[c][2 * p], ss);
+            ss = fmaf(v[c][2 * p + 1], v[c][2 * p + 1], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((t & (kWave - 1)) == 0) red[t / kWave] = ss;
+    __syncthreads();
+    const float inv = rsqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)K + na.eps);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int ci = t + 256 * c;
+        const uint32_t wv[4] = {nl.w[c].x, nl.w[c].y, nl.w[c].z, nl.w[c].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
+            const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
+            o[p] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+        }
+        reinterpret_cast<uint4*>(xn)[ci] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    __syncthreads();
+}
+
+// n_out output rows; PAIRED reads gate row n and up row n + n_out.  NORM > 0 needs
+// K = 2048 KG (the whole workgroup takes part in the normalization, so no wave leaves early).
+template <int KG, int R, bool PAIRED, bool FULL, bool EXACT, int NORM>
+__device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,
+                                          const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+                                          uint16_t* __restrict__ y, int G, int n_out, const NormArgs& na) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int stride = gridDim.x * (blockDim.x / kWave);
-    int n = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
-    if (n >= n_out) return;  // wave-uniform
-    constexpr int NR = PAIRED ? 2 : 1;
-    RowLoad<KG> buf0[NR], buf1[NR];
+    // wave-uniform: lets row addressing run on the scalar unit
+    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
+    const int row0 = wave * R;
+    if (NORM == 0 && row0 >= n_out) return;  // wave-uniform
+
+    constexpr int NR = PAIRED ? 2 * R : R;
+    NormLoad<(NORM > 0 ? KG : 1)> nl;
+    if constexpr (NORM > 0) norm_load<NORM, KG>(nl, x, na);
+    RowLoad<KG> rows[NR];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) load_row_nt<KG, FULL>(buf0[r], qw, sc, zp, n + r * n_out, lane, G);
+    for (int r = 0; r < NR; ++r) {
+        const int local = PAIRED ? (r % R) : r;
+        const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
+        load_row_nt<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
+    }
     XSlice<KG> xs;
-    load_x<KG, !EXACT, FULL>(xs, x, lane, G);
+    if constexpr (NORM > 0) {
+        __shared__ __attribute__((aligned(16))) uint16_t xn[2048 * KG];
+        __shared__ float red[4];
+        norm_into_lds<NORM, KG>(nl, na, xn, red, 32 * G);
+        if (row0 >= n_out) return;  // after the workgroup's barriers
+        load_x<KG, !EXACT, FULL>(xs, xn, lane, G);
+    } else {
+        load_x<KG, !EXACT, FULL>(xs, x, lane, G);
+    }
+
     const Magic m = make_magic();
-    // ping-pong between two register buffers so no copy is needed between iterations
-    while (true) {
-        const int n1 = n + stride;
-        if (n1 < n_out) {
+    float out[NR];
 #pragma unroll
-            for (int r = 0; r < NR; ++r) load_row_nt<KG, FULL>(buf1[r], qw, sc, zp, n1 + r * n_out, lane, G);
-        }
-        stream_row<KG, PAIRED, FULL, EXACT>(xs, buf0, m, n, lane, y);
-        if (n1 >= n_out) break;
-        const int n2 = n1 + stride;
-        if (n2 < n_out) {
+    for (int r = 0; r < NR; ++r)
+        out[r] = wave_sum(EXACT ? row_partial_exact(xs, rows[r], m) : row_partial_unrounded(xs, rows[r], m));
+
+    if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < NR; ++r) load_row_nt<KG, FULL>(buf0[r], qw, sc, zp, n2 + r * n_out, lane, G);
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            if (n < n_out) y[n] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
         }
-        stream_row<KG, PAIRED, FULL, EXACT>(xs, buf1, m, n1, lane, y);
-        if (n2 >= n_out) break;
-        n = n2;
     }
 }
 
@@ -375,17 +411,25 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
 
 // ---------------------------------------------------------------------------------------
 // Entry kernels: one name per (role, dequant mode), so profiles tell them apart.
-#define MOSS_ROWS_ENTRY(NAME, PAIRED, EXACT)                                                                 \
-    template <int KG, int R, bool FULL>                                                                      \
-    __global__ __launch_bounds__(256) void NAME(const uint16_t* __restrict__ x, const uint4* __restrict__ qw, \
+#define MOSS_ROWS_ENTRY(NAME, PAIRED, EXACT, NORM)                                                           \
+    template <int KG, int R, bool FULL>                                                                          \
+    __global__ __launch_bounds__(256) void NAME(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,     \
                                                 const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp, \
-                                                uint16_t* __restrict__ y, int G, int n_out) {                   \
-        gemv_rows<KG, R, PAIRED, FULL, EXACT>(x, qw, sc, zp, y, G, n_out);                                   \
+                                                uint16_t* __restrict__ y, int G, int n_out, NormArgs na) {      \
+        gemv_rows<KG, R, PAIRED, FULL, EXACT, NORM>(x, qw, sc, zp, y, G, n_out, na);                             \
     }
-MOSS_ROWS_ENTRY(w4g32_gemv_exact, false, true)
-MOSS_ROWS_ENTRY(w4g32_gemv_unrounded, false, false)
-MOSS_ROWS_ENTRY(w4g32_gateup_silu_exact, true, true)
-MOSS_ROWS_ENTRY(w4g32_gateup_silu_unrounded, true, false)
+MOSS_ROWS_ENTRY(w4g32_gemv_exact, false, true, 0)
+MOSS_ROWS_ENTRY(w4g32_gemv_unrounded, false, false, 0)
+MOSS_ROWS_ENTRY(w4g32_gateup_silu_exact, true, true, 0)
+MOSS_ROWS_ENTRY(w4g32_gateup_silu_unrounded, true, false, 0)
+MOSS_ROWS_ENTRY(w4g32_norm_gemv_exact, false, true, 1)
+MOSS_ROWS_ENTRY(w4g32_norm_gemv_unrounded, false, false, 1)
+MOSS_ROWS_ENTRY(w4g32_norm_gateup_silu_exact, true, true, 1)
+MOSS_ROWS_ENTRY(w4g32_norm_gateup_silu_unrounded, true, false, 1)
+MOSS_ROWS_ENTRY(w4g32_addnorm_gemv_exact, false, true, 2)
+MOSS_ROWS_ENTRY(w4g32_addnorm_gemv_unrounded, false, false, 2)
+MOSS_ROWS_ENTRY(w4g32_addnorm_gateup_silu_exact, true, true, 2)
+MOSS_ROWS_ENTRY(w4g32_addnorm_gateup_silu_unrounded, true, false, 2)
 #undef MOSS_ROWS_ENTRY
 
 #define MOSS_KSPLIT_ENTRY(NAME, PAIRED, EXACT)                                                                  \
@@ -402,14 +446,32 @@ MOSS_KSPLIT_ENTRY(w4g32_gateup_silu_ksplit_exact, true, true)
 MOSS_KSPLIT_ENTRY(w4g32_gateup_silu_ksplit_unrounded, true, false)
 #undef MOSS_KSPLIT_ENTRY
 
-template <int KG, int R, bool PAIRED, bool FULL, bool EXACT>
+template <int KG, int R, bool PAIRED, bool FULL, bool EXACT, int NORM>
 constexpr auto rows_kernel() {
-    if constexpr (PAIRED) {
-        if constexpr (EXACT) return &w4g32_gateup_silu_exact<KG, R, FULL>;
-        else return &w4g32_gateup_silu_unrounded<KG, R, FULL>;
+    if constexpr (NORM == 0) {
+        if constexpr (PAIRED) {
+            if constexpr (EXACT) return &w4g32_gateup_silu_exact<KG, R, FULL>;
+            else return &w4g32_gateup_silu_unrounded<KG, R, FULL>;
+        } else {
+            if constexpr (EXACT) return &w4g32_gemv_exact<KG, R, FULL>;
+            else return &w4g32_gemv_unrounded<KG, R, FULL>;
+        }
+    } else if constexpr (NORM == 1) {
+        if constexpr (PAIRED) {
+            if constexpr (EXACT) return &w4g32_norm_gateup_silu_exact<KG, R, FULL>;
+            else return &w4g32_norm_gateup_silu_unrounded<KG, R, FULL>;
+        } else {
+            if constexpr (EXACT) return &w4g32_norm_gemv_exact<KG, R, FULL>;
+            else return &w4g32_norm_gemv_unrounded<KG, R, FULL>;
+        }
     } else {
-        if constexpr (EXACT) return &w4g32_gemv_exact<KG, R, FULL>;
-        else return &w4g32_gemv_unrounded<KG, R, FULL>;
+        if constexpr (PAIRED) {
+            if constexpr (EXACT) return &w4g32_addnorm_gateup_silu_exact<KG, R, FULL>;
+            else return &w4g32_addnorm_gateup_silu_unrounded<KG, R, FULL>;
+        } else {
+            if constexpr (EXACT) return &w4g32_addnorm_gemv_exact<KG, R, FULL>;
+            else return &w4g32_addnorm_gemv_unrounded<KG, R, FULL>;
+        }
     }
 }
 
@@ -448,46 +510,9 @@ int launch_ksplit(const void* x, const void* qw, const void* sc, const void* zp,
     return (int)hipErrorInvalidValue;
 }
 
-template <bool PAIRED, bool EXACT>
-int launch_stream(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
-                  int waves, hipStream_t st) {
-    const int KG = (G + kWave - 1) / kWave;
-    if (waves <= 0) waves = 2048;
-    waves = min(waves, n_out);
-    const dim3 grid((waves + 3) / 4), block(256);
-    const auto* xp = (const uint16_t*)x;
-    const auto* qp = (const uint4*)qw;
-    const auto* sp = (const uint16_t*)sc;
-    const auto* zpp = (const uint8_t*)zp;
-    auto* yp = (uint16_t*)y;
-    const bool full = (G == kWave * KG) && (KG % 2 == 0);
-    switch (KG) {
-#define MOSS_KG_CASE(KGV)                                                                                        \
-    case KGV:                                                                                                    \
-        if (full)                                                                                                \
-            hipLaunchKernelGGL((w4g32_gemv_stream<KGV, PAIRED, (KGV % 2 == 0), EXACT>), grid, block, 0, st, xp, \
-                               qp, sp, zpp, yp, G, n_out);                                                       \
-        else                                                                                                     \
-            hipLaunchKernelGGL((w4g32_gemv_stream<KGV, PAIRED, false, EXACT>), grid, block, 0, st, xp, qp, sp,   \
-                               zpp, yp, G, n_out);                                                               \
-        break;
-        MOSS_KG_CASE(1)
-        MOSS_KG_CASE(2)
-        MOSS_KG_CASE(3)
-        MOSS_KG_CASE(4)
-        MOSS_KG_CASE(5)
-        MOSS_KG_CASE(6)
-        MOSS_KG_CASE(7)
-        MOSS_KG_CASE(8)
-#undef MOSS_KG_CASE
-        default: return (int)hipErrorInvalidValue;
-    }
-    return moss_launch_status();
-}
-
-template <bool PAIRED, int R, bool EXACT>
+template <bool PAIRED, int R, bool EXACT, int NORM>
 int launch_rows(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
-                hipStream_t st) {
+                const NormArgs& na, hipStream_t st) {
     const int KG = (G + kWave - 1) / kWave;
     const int waves = (n_out + R - 1) / R;
     const dim3 grid((waves + 3) / 4), block(256);
@@ -500,13 +525,17 @@ int launch_rows(const void* x, const void* qw, const void* sc, const void* zp, v
     switch (KG) {
 #define MOSS_KG_CASE(KGV)                                                                                          \
     case KGV:                                                                                                      \
-        if (full)                                                                                                  \
-            hipLaunchKernelGGL((rows_kernel<KGV, R, PAIRED, (KGV % 2 == 0), EXACT>()), grid, block, 0, st, xp, qp, sp, \
-                               zpp, yp, G, n_out);                                                                 \
-        else                                                                                                       \
-            hipLaunchKernelGGL((rows_kernel<KGV, R, PAIRED, false, EXACT>()), grid, block, 0, st, xp, qp, sp, zpp, yp, \
-                               G, n_out);                                                                          \
-        break;
+        if constexpr (NORM == 0 || KGV <= 4) {                                                                     \
+            if (full)                                                                                              \
+                hipLaunchKernelGGL((rows_kernel<KGV, R, PAIRED, (KGV % 2 == 0), EXACT, NORM>()), grid, block, 0, st, \
+                                   xp, qp, sp, zpp, yp, G, n_out, na);                                             \
+            else                                                                                                   \
+                hipLaunchKernelGGL((rows_kernel<KGV, R, PAIRED, false, EXACT, NORM>()), grid, block, 0, st, xp, qp, \
+                                   sp, zpp, yp, G, n_out, na);                                                     \
+            break;                                                                                                 \
+        } else {                                                                                                   \
+            return (int)hipErrorInvalidValue;                                                                      \
+        }
         MOSS_KG_CASE(1)
         MOSS_KG_CASE(2)
         MOSS_KG_CASE(3)
@@ -521,35 +550,32 @@ int launch_rows(const void* x, const void* qw, const void* sc, const void* zp, v
     return moss_launch_status();
 }
 
-template <bool PAIRED, bool EXACT>
+template <bool PAIRED, bool EXACT, int NORM>
 int launch_gemv_mode(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
-                     int rows, hipStream_t st) {
+                     int rows, const NormArgs& na, hipStream_t st) {
     switch (rows) {
-        case 1: return launch_rows<PAIRED, 1, EXACT>(x, qw, sc, zp, y, G, n_out, st);
-        case 2: return launch_rows<PAIRED, 2, EXACT>(x, qw, sc, zp, y, G, n_out, st);
-        case 4: return launch_rows<PAIRED, 4, EXACT>(x, qw, sc, zp, y, G, n_out, st);
+        case 1: return launch_rows<PAIRED, 1, EXACT, NORM>(x, qw, sc, zp, y, G, n_out, na, st);
+        case 2: return launch_rows<PAIRED, 2, EXACT, NORM>(x, qw, sc, zp, y, G, n_out, na, st);
+        case 4: return launch_rows<PAIRED, 4, EXACT, NORM>(x, qw, sc, zp, y, G, n_out, na, st);
         default: return (int)hipErrorInvalidValue;
     }
 }
 
-template <bool PAIRED>
+template <bool PAIRED, int NORM>
 int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
-                int rows, int mode, hipStream_t st) {
+                int rows, int mode, const NormArgs& na, hipStream_t st) {
     const int G = K / 32;
-    if (rows < 0) {
-        if (mode == MOSS_DEQUANT_EXACT) return launch_stream<PAIRED, true>(x, qw, sc, zp, y, G, n_out, -rows * 256, st);
-        if (mode == MOSS_DEQUANT_UNROUNDED)
-            return launch_stream<PAIRED, false>(x, qw, sc, zp, y, G, n_out, -rows * 256, st);
-        return (int)hipErrorInvalidValue;
-    }
-    if (G % 128 == 0 && G >= 256 && G <= 512 && rows >= 0 && rows <= 4 && rows != 3) {
+    if (rows < 0 || rows == 3 || rows > 4) return (int)hipErrorInvalidValue;
+    if (NORM == 0 && G % 128 == 0 && G >= 256 && G <= 512) {
         if (mode == MOSS_DEQUANT_EXACT) return launch_ksplit<PAIRED, true>(x, qw, sc, zp, y, G, n_out, rows, st);
         if (mode == MOSS_DEQUANT_UNROUNDED) return launch_ksplit<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
         return (int)hipErrorInvalidValue;
     }
     if (rows == 0) rows = (G <= 128) ? (PAIRED ? 2 : 4) : (G <= 256 ? 2 : 1);
-    if (mode == MOSS_DEQUANT_EXACT) return launch_gemv_mode<PAIRED, true>(x, qw, sc, zp, y, G, n_out, rows, st);
-    if (mode == MOSS_DEQUANT_UNROUNDED) return launch_gemv_mode<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
+    if (mode == MOSS_DEQUANT_EXACT)
+        return launch_gemv_mode<PAIRED, true, NORM>(x, qw, sc, zp, y, G, n_out, rows, na, st);
+    if (mode == MOSS_DEQUANT_UNROUNDED)
+        return launch_gemv_mode<PAIRED, false, NORM>(x, qw, sc, zp, y, G, n_out, rows, na, st);
     return (int)hipErrorInvalidValue;
 }
 
@@ -566,7 +592,7 @@ MOSS_API int moss_w4g32_gemv(const void* x, const void* qw, const void* sc, cons
     MOSS_CHECK_ARG(x && qw && sc && zp && y);
     MOSS_CHECK_ARG(M == 1 && K > 0 && N > 0 && K % 64 == 0 && K <= kMaxGemvK);
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
-    return launch_gemv<false>(x, qw, sc, zp, y, K, N, rows_per_wave, dequant_mode, (hipStream_t)stream);
+    return launch_gemv<false, 0>(x, qw, sc, zp, y, K, N, rows_per_wave, dequant_mode, NormArgs{}, (hipStream_t)stream);
 }
 
 MOSS_API int moss_w4g32_gateup_silu(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M,
@@ -574,5 +600,44 @@ MOSS_API int moss_w4g32_gateup_silu(const void* x, const void* qw, const void* s
     MOSS_CHECK_ARG(x && qw && sc && zp && y);
     MOSS_CHECK_ARG(M == 1 && K > 0 && N_half > 0 && K % 64 == 0 && K <= kMaxGemvK);
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
-    return launch_gemv<true>(x, qw, sc, zp, y, K, N_half, rows_per_wave, dequant_mode, (hipStream_t)stream);
+    return launch_gemv<true, 0>(x, qw, sc, zp, y, K, N_half, rows_per_wave, dequant_mode, NormArgs{},
+                                (hipStream_t)stream);
+}
+
+// The fused forms: res == NULL normalizes x; otherwise s = bf16(x + res) is normalized and
+// stored to sum_out (which must not overlap x or res: other workgroups still read them).
+static int check_norm_args(const void* x, const void* res, const void* norm_w, void* sum_out, int K, float eps) {
+    MOSS_CHECK_ARG(x && norm_w && K > 0 && K % 2048 == 0 && K <= 8192 && eps >= 0.f);
+    MOSS_CHECK_ARG((res == nullptr) == (sum_out == nullptr));
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(res, 16) &&
+                   MOSS_ALIGNED(sum_out, 16));
+    if (sum_out) {
+        const uintptr_t so = (uintptr_t)sum_out, n = (uintptr_t)K * 2;
+        MOSS_CHECK_ARG((so + n <= (uintptr_t)x || (uintptr_t)x + n <= so) &&
+                       (so + n <= (uintptr_t)res || (uintptr_t)res + n <= so));
+    }
+    return 0;
+}
+
+MOSS_API int moss_w4g32_norm_gemv(const void* x, const void* res, const void* norm_w, void* sum_out, float eps,
+                                  const void* qw, const void* sc, const void* zp, void* y, int K, int N,
+                                  int rows_per_wave, int dequant_mode, void* stream) {
+    if (int rc = check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
+    MOSS_CHECK_ARG(qw && sc && zp && y && N > 0 && MOSS_ALIGNED(qw, 16));
+    const NormArgs na{(const uint16_t*)res, (const uint16_t*)norm_w, (uint16_t*)sum_out, eps};
+    if (res)
+        return launch_gemv<false, 2>(x, qw, sc, zp, y, K, N, rows_per_wave, dequant_mode, na, (hipStream_t)stream);
+    return launch_gemv<false, 1>(x, qw, sc, zp, y, K, N, rows_per_wave, dequant_mode, na, (hipStream_t)stream);
+}
+
+MOSS_API int moss_w4g32_norm_gateup_silu(const void* x, const void* res, const void* norm_w, void* sum_out,
+                                         float eps, const void* qw, const void* sc, const void* zp, void* y, int K,
+                                         int N_half, int rows_per_wave, int dequant_mode, void* stream) {
+    if (int rc = check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
+    MOSS_CHECK_ARG(qw && sc && zp && y && N_half > 0 && MOSS_ALIGNED(qw, 16));
+    const NormArgs na{(const uint16_t*)res, (const uint16_t*)norm_w, (uint16_t*)sum_out, eps};
+    if (res)
+        return launch_gemv<true, 2>(x, qw, sc, zp, y, K, N_half, rows_per_wave, dequant_mode, na,
+                                    (hipStream_t)stream);
+    return launch_gemv<true, 1>(x, qw, sc, zp, y, K, N_half, rows_per_wave, dequant_mode, na, (hipStream_t)stream);
 }

@@ -1,8 +1,8 @@
 """Batch-1 decode step of the Qwen3-8B backbone on the gfx950 kernels, captured as one graph.
 
 Per layer (the order of ``src/moss_tts/_runtime/llm.py:227-260`` with fused residuals):
-add-RMSNorm -> q||k||v GEMV -> q/k head-norm + RoPE + KV write -> split-K GQA attention ->
-O GEMV -> add-RMSNorm -> gate||up GEMV with SiLU*mul -> down GEMV.  The step starts with the
+add-RMSNorm + q||k||v GEMV (one kernel) -> q/k head-norm + RoPE + KV write -> split-K GQA
+attention -> O GEMV -> add-RMSNorm + gate||up GEMV with SiLU*mul (one kernel) -> down GEMV.  The step starts with the
 33-row embedding sum (``src/moss_tts/_runtime/kernels.py:7-26``) and ends with the final norm
 and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``),
 here INT4-G32 as well.  Static input buffers (ids, position) make the step graph-capturable;
@@ -81,23 +81,28 @@ class DecodeStepG32:
 
     # ------------------------------------------------------------------ forward
     def forward(self) -> torch.Tensor:
-        """One step from the static ``ids``/``position`` buffers -> logits bf16 ``[N_heads]``."""
+        """One step from the static ``ids``/``position`` buffers -> logits bf16 ``[N_heads]``.
+        Every (add+)RMSNorm runs inside the projection that consumes it (``norm_gemv``)."""
+        eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
-        h = pointwise.rmsnorm(x, self.layers[0].input_norm, self.eps)
         mlp = None
         for i, layer in enumerate(self.layers):
-            if i > 0:
-                residual, h = pointwise.add_rmsnorm(mlp, residual, layer.input_norm, self.eps)
-            qkv = layer.qkv(h)
+            if i == 0:
+                qkv = w4g32.norm_gemv(x, layer.input_norm, eps, layer.qkv.packed, dequant=layer.qkv.dequant)
+            else:
+                residual, qkv = w4g32.norm_gemv(mlp, layer.input_norm, eps, layer.qkv.packed, residual=residual,
+                                                dequant=layer.qkv.dequant)
             q = pointwise.qk_rope(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
-                                  self.values[i], self.position, self.eps, cos_by_position=True)
+                                  self.values[i], self.position, eps, cos_by_position=True)
             attn = attention.decode_attention(q, self.keys[i], self.values[i], self.position, ws=self.ws)
             o = layer.o(attn.view(1, HIDDEN))
-            residual, h = pointwise.add_rmsnorm(o, residual, layer.post_norm, self.eps)
-            mlp = layer.down(layer.gate_up(h))
-        _, h = pointwise.add_rmsnorm(mlp, residual, self.final_norm, self.eps)
-        return self.heads(h).view(-1)
+            residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
+                                                   residual=residual, dequant=layer.gate_up.dequant)
+            mlp = layer.down(act)
+        _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
+                                    dequant=self.heads.dequant)
+        return logits.view(-1)
 
     @torch.inference_mode()
     def capture(self) -> None:

@@ -219,6 +219,42 @@ def gateup_silu(x: torch.Tensor, w: PackedW4G32, *, rows_per_wave: int = 0, dequ
     return y
 
 
+def _norm_call(name, x, norm_weight, eps, w, n_out, residual, rows_per_wave, dequant):
+    _check_row(x, w)
+    _require(w.K % 2048 == 0 and w.K <= 8192, "the fused norm needs K % 2048 == 0 and K <= 8192")
+    _cuda_contig("norm_weight", norm_weight, torch.bfloat16, w.device)
+    _require(norm_weight.numel() == w.K, f"norm_weight must hold {w.K} values")
+    _require(_aligned(norm_weight, 16), "norm_weight must be 16-byte aligned")
+    rows = _rows_arg(rows_per_wave)
+    mode = _mode_arg(dequant)
+    summed = None
+    if residual is not None:
+        _cuda_contig("residual", residual, torch.bfloat16, w.device)
+        _require(residual.numel() == w.K and _aligned(residual, 16), f"residual must be an aligned row of {w.K}")
+        summed = torch.empty_like(x)
+    y = torch.empty((*x.shape[:-1], n_out), dtype=torch.bfloat16, device=x.device)
+    native.call(name, native.ptr(x), native.ptr(residual) if residual is not None else None, native.ptr(norm_weight),
+                native.ptr(summed) if summed is not None else None, float(eps), native.ptr(w.qw),
+                native.ptr(w.scales), native.ptr(w.zeros), native.ptr(y), w.K, n_out, rows, mode,
+                native.stream_of(x))
+    return y if summed is None else (summed, y)
+
+
+def norm_gemv(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: PackedW4G32, *,
+              residual: torch.Tensor | None = None, rows_per_wave: int = 0, dequant: int = EXACT):
+    """``gemv(rmsnorm(x))`` in one kernel; with ``residual``: ``s = bf16(x + residual)``,
+    returns ``(s, gemv(rmsnorm(s)))`` (``src/moss_tts/_runtime/dp4a_norm_projection.py:132-166``)."""
+    return _norm_call("moss_w4g32_norm_gemv", x, norm_weight, eps, w, w.N, residual, rows_per_wave, dequant)
+
+
+def norm_gateup_silu(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: PackedW4G32, *,
+                     residual: torch.Tensor | None = None, rows_per_wave: int = 0, dequant: int = EXACT):
+    """``gateup_silu(rmsnorm(x))`` in one kernel (optionally after the residual add)."""
+    _require(w.N % 2 == 0, "gate||up weight needs an even number of rows")
+    return _norm_call("moss_w4g32_norm_gateup_silu", x, norm_weight, eps, w, w.N // 2, residual, rows_per_wave,
+                      dequant)
+
+
 def gemm(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
     """Prefill projection: bf16 ``[..., M, K]`` -> bf16 ``[..., M, N]`` on the matrix cores, with
     bit-exact bf16 dequantized weights and fp32 accumulation."""

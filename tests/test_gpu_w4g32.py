@@ -207,3 +207,64 @@ def test_gemm_rows_match_gemv(dev):
     for r in (0, 17, 63):
         g = w4g32.gemv(x[r:r + 1].contiguous(), pw).float()
         assert torch.allclose(y[r], g[0], atol=2e-2, rtol=1e-2)
+
+
+# ------------------------------------------------------- fused (add+)RMSNorm + GEMV
+@pytest.mark.parametrize("k,n,paired", [(4096, 6144, False), (4096, 12288, True), (2048, 200, False),
+                                        (8192, 64, True), (4096, 32800, False)])
+@pytest.mark.parametrize("mode", ["exact", "unrounded"])
+@pytest.mark.parametrize("residual", [False, True])
+def test_norm_gemv_equals_rmsnorm_then_gemv(dev, k, n, paired, mode, residual):
+    """The fused kernel reproduces moss_rmsnorm followed by the GEMV bit for bit (same rounding
+    points and summation order); the residual sum is bf16(x + r) exactly."""
+    from moss_tts._runtime import pointwise, w4g32
+
+    print(f"norm gemv K={k} N={n} paired={paired} mode={mode} residual={residual}", flush=True)
+    dq = w4g32.EXACT if mode == "exact" else w4g32.UNROUNDED
+    g = torch.Generator(device=dev).manual_seed(k + n)
+    pw = w4g32.quantize_minmax((torch.randn((n, k), device=dev, generator=g) * 0.02).contiguous())
+    x = (torch.randn((1, k), device=dev, generator=g) * 3).bfloat16()
+    nw = (1 + 0.01 * torch.randn(k, device=dev, generator=g)).bfloat16()
+    r = (torch.randn((1, k), device=dev, generator=g) * 5).bfloat16() if residual else None
+    fused = w4g32.norm_gateup_silu if paired else w4g32.norm_gemv
+    plain = w4g32.gateup_silu if paired else w4g32.gemv
+    out = fused(x, nw, 1e-6, pw, residual=r, dequant=dq)
+    if residual:
+        s, y = out
+        s_ref, h = pointwise.add_rmsnorm(x, r, nw, 1e-6)
+        assert torch.equal(s, s_ref)
+    else:
+        y, h = out, pointwise.rmsnorm(x, nw, 1e-6)
+    assert torch.equal(y, plain(h, pw, dequant=dq))
+
+
+def test_norm_gemv_parity_with_oracle(dev):
+    from moss_tts._runtime import w4g32
+    from oracle import pointwise as op
+
+    q, z, s = _case(6144, 4096, 17)
+    x = (torch.randn((1, 4096), generator=torch.Generator().manual_seed(9)) * 2).bfloat16()
+    r = torch.randn((1, 4096), generator=torch.Generator().manual_seed(10)).bfloat16()
+    nw = (1 + 0.01 * torch.randn(4096, generator=torch.Generator().manual_seed(11))).bfloat16()
+    summed, y = w4g32.norm_gemv(x.to(dev), nw.to(dev), 1e-6, _packed(q, z, s, dev), residual=r.to(dev))
+    s_ref, h_ref = op.add_rmsnorm(x, r, nw, 1e-6)
+    assert torch.equal(summed.cpu(), s_ref)
+    _assert_close(y, o.w4g32_linear(h_ref, q, z, s), "norm gemv vs oracle")
+
+
+def test_norm_gemv_rejects_bad_inputs(dev):
+    from moss_tts._runtime import native, w4g32
+
+    pw = w4g32.quantize_minmax(torch.randn((64, 4096), device=dev))
+    x = torch.randn((1, 4096), device=dev).bfloat16()
+    nw = torch.ones(4096, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        w4g32.norm_gemv(x, nw[:2048], 1e-6, pw)
+    pw2 = w4g32.quantize_minmax(torch.randn((64, 1024), device=dev))
+    with pytest.raises(ValueError):
+        w4g32.norm_gemv(x[:, :1024].contiguous(), nw[:1024].contiguous(), 1e-6, pw2)     # K % 2048
+    y = torch.empty((1, 64), device=dev, dtype=torch.bfloat16)
+    rc = native.lib().moss_w4g32_norm_gemv(native.ptr(x), native.ptr(x), native.ptr(nw), native.ptr(x), 1e-6,
+                                           native.ptr(pw.qw), native.ptr(pw.scales), native.ptr(pw.zeros),
+                                           native.ptr(y), 4096, 64, 0, 0, native.stream_of(x))
+    assert rc == 1                                                   # sum_out overlaps x
