@@ -157,14 +157,26 @@ int moss_silu_mul(const void *x, void *y, int rows, int n, void *stream);
 int moss_decode_attention_splits(int L);
 
 /* One query token, Qwen3-8B GQA (32 query / 8 KV heads, head_dim 128): q bf16 [32,128],
- * caches bf16 [8, L, 128] (one layer of the [1, 8, L, 128] static cache), position int64 [1]
- * on the device (rows 0..position are attended; clamped to L-1), caller-owned workspaces
- * partial fp32 [32, S, 128] and lse fp32 [32, S], out bf16 [32 * 128].  Split + LSE merge.
+ * caches bf16 [8, L, 128] (one layer of the [1, 8, L, 128] static cache, L % 64 == 0,
+ * L <= 32768), position int64 [1] on the device (rows 0..position are attended; clamped to
+ * L-1), caller-owned workspace partial fp32 [32, S, 128] and lse fp32 [32, S] (S = L / 64;
+ * calls sharing a workspace must not overlap), out bf16 [32 * 128].  Two launches: 64-row
+ * splits, then a log-sum-exp merge in split order.
  * Replaces _decode_attn/_decode_attn_reduce (src/moss_tts/_runtime/kernels.py:173-208,
  * driven from qk_rope_decode :211-251) and launch_attention_ordered
  * (src/moss_tts/_runtime/attention_native.cu:91-97). */
 int moss_decode_attention(const void *q, const void *k_cache, const void *v_cache, const void *position,
                           void *partial, void *lse, void *out, int L, void *stream);
+
+/* q/k head-norm + RoPE + KV-cache write + decode attention in one pass: qkv bf16 [6144]
+ * (q 32x128 | k 8x128 | v 8x128, raw projection output), q/k head-norm weights bf16 [128],
+ * cos/sin bf16 [L, 128] tables (row = position), the rest as moss_decode_attention.  Row
+ * `position` of both caches is written (by the one split that holds it, which also uses the new
+ * row directly).  Bit-identical to moss_qk_norm_rope_kv (ntok 1, cos_by_position 1) followed by
+ * moss_decode_attention.  Replaces qk_rope_decode, src/moss_tts/_runtime/kernels.py:211-251. */
+int moss_decode_attention_qkv(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
+                              const void *sin_t, void *k_cache, void *v_cache, const void *position, void *partial,
+                              void *lse, void *out, int L, float eps, void *stream);
 
 /* ids int64 [T, Q+1] (text token then Q codebook codes), text bf16 [Vt, H], audio bf16
  * [Q, V, H] -> out bf16 [T, H] with a bf16 rounding after each addition; ids are clamped

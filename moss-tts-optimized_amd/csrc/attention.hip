@@ -17,58 +17,121 @@ constexpr int kGroup = kQHeads / kKvHeads;  // 4 query heads per KV head
 constexpr int kSplit = 64;                  // cache rows per workgroup
 constexpr float kScale = 0.08838834764831845f;
 
-// grid (8 KV heads, S splits), 256 threads.
+constexpr int kMaxSplits = 512;             // L <= 32768
+
+// grid (8 KV heads, S splits), 256 threads.  Each workgroup issues all of its K and V loads
+// (64 rows x 256 B each) before any arithmetic, stages V in LDS, and writes the split's
+// normalized partial output and log-sum-exp.  Splits after the position write nothing.
+//
+// FUSED: q, k and v come raw from the q||k||v projection row.  Every workgroup puts its 4
+// query heads through head RMSNorm + RoPE (row `position` of the cos/sin tables); the one
+// workgroup whose split holds the position also forms the new K row (k-norm + RoPE) and V row,
+// stores both into the cache and uses them in place of the cache row it loaded, so no
+// workgroup reads a row another one writes (src/moss_tts/_runtime/kernels.py:142-170,211-251).
+struct QkvArgs {
+    const uint16_t* __restrict__ qnw;  // q head-norm weight [128]
+    const uint16_t* __restrict__ knw;  // k head-norm weight [128]
+    const uint16_t* __restrict__ cos_t;
+    const uint16_t* __restrict__ sin_t;  // [L, 128] tables, row = position
+    float eps;
+};
+
+template <bool FUSED>
 __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restrict__ q,
-                                                         const uint16_t* __restrict__ kc,
-                                                         const uint16_t* __restrict__ vc,
+                                                         uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                          const int64_t* __restrict__ pos, float* __restrict__ part,
-                                                         float* __restrict__ lse, int L, int S) {
+                                                         float* __restrict__ lse, int L, int S, QkvArgs qa) {
     __shared__ float qs[kGroup][kHeadDim];
     __shared__ float pr[kGroup][kSplit];
     __shared__ float denom_s[kGroup];
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kSplit][kHeadDim];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kSplit][kHeadDim];
     const int hk = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
     // rows [0, p] are attended; a position beyond the cache is clamped to its last row (the
     // host API rejects it first; the clamp keeps every access inside the cache regardless)
     const int p = (int)min(max(pos[0], (int64_t)0), (int64_t)(L - 1));
     const int t0 = split * kSplit;
-    if (t0 > p) {  // every row of this split is masked (uniform over the workgroup)
-        const int j = tid / kWave, l = tid & (kWave - 1);
-        const int hq = hk * kGroup + j;
-        part[((size_t)hq * S + split) * kHeadDim + l] = 0.f;
-        part[((size_t)hq * S + split) * kHeadDim + l + 64] = 0.f;
-        if (l == 0) lse[hq * S + split] = -INFINITY;
-        return;
-    }
-    // the 4 query heads of this KV head, fp32 in LDS
+    if (t0 > p) return;  // uniform over the workgroup
+    const bool owner = FUSED && p < t0 + kSplit;  // this split holds the new row (uniform)
+
+    // all global loads first, staged in LDS: 4 threads per cache row, each a 32-dim quarter
+    // (64 contiguous bytes) of K and of V; rows t0..t0+63 lie inside the cache (L % 64 == 0)
+    const int tl = tid >> 2, qd = tid & 3, t = t0 + tl;
     {
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
+        const uint4* vr = reinterpret_cast<const uint4*>(vc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
+        uint4* kd = reinterpret_cast<uint4*>(&ks[tl][32 * qd]);
+        uint4* vd = reinterpret_cast<uint4*>(&vs[tl][32 * qd]);
+        const uint4 a0 = kr[0], a1 = kr[1], a2 = kr[2], a3 = kr[3];
+        const uint4 b0 = vr[0], b1 = vr[1], b2 = vr[2], b3 = vr[3];
+        kd[0] = a0; kd[1] = a1; kd[2] = a2; kd[3] = a3;
+        vd[0] = b0; vd[1] = b1; vd[2] = b2; vd[3] = b3;
+    }
+    const int j = tid / kWave, l = tid & (kWave - 1);
+    uint16_t nk0 = 0, nk1 = 0, nv0 = 0, nv1 = 0;
+    if constexpr (FUSED) {
+        // wave j: query head 4 hk + j; lane l: dims l and l + 64
+        constexpr int D = kHeadDim;
+        const uint16_t* cr = qa.cos_t + (size_t)p * D;
+        const uint16_t* sr = qa.sin_t + (size_t)p * D;
+        const float c0 = bf16_bits(cr[l]), c1 = bf16_bits(cr[l + 64]);
+        const float s0 = bf16_bits(sr[l]), s1 = bf16_bits(sr[l + 64]);
+        const uint16_t* qh = q + (size_t)(hk * kGroup + j) * D;
+        uint16_t o0, o1;
+        head_norm_rope(bf16_bits(qh[l]), bf16_bits(qh[l + 64]), bf16_bits(qa.qnw[l]), bf16_bits(qa.qnw[l + 64]), c0,
+                       c1, s0, s1, qa.eps, o0, o1);
+        qs[j][l] = bf16_bits(o0);
+        qs[j][l + 64] = bf16_bits(o1);
+        if (owner && j == 0) {  // the new K row of this KV head, into the cache
+            const uint16_t* kh = q + (size_t)(kQHeads + hk) * D;
+            head_norm_rope(bf16_bits(kh[l]), bf16_bits(kh[l + 64]), bf16_bits(qa.knw[l]), bf16_bits(qa.knw[l + 64]),
+                           c0, c1, s0, s1, qa.eps, nk0, nk1);
+            uint16_t* kd = kc + ((size_t)hk * L + p) * D;
+            kd[l] = nk0;
+            kd[l + 64] = nk1;
+        } else if (owner && j == 1) {  // the new V row (a copy), into the cache
+            const uint16_t* vh = q + (size_t)(kQHeads + kKvHeads + hk) * D;
+            nv0 = vh[l];
+            nv1 = vh[l + 64];
+            uint16_t* vd = vc + ((size_t)hk * L + p) * D;
+            vd[l] = nv0;
+            vd[l + 64] = nv1;
+        }
+    } else {
         const uint32_t w = reinterpret_cast<const uint32_t*>(q + (size_t)hk * kGroup * kHeadDim)[tid];
-        const int j = (2 * tid) / kHeadDim, d = (2 * tid) % kHeadDim;
-        qs[j][d] = bf16_lo(w);
-        qs[j][d + 1] = bf16_hi(w);
+        const int jj = (2 * tid) / kHeadDim, d = (2 * tid) % kHeadDim;
+        qs[jj][d] = bf16_lo(w);
+        qs[jj][d + 1] = bf16_hi(w);
     }
     __syncthreads();
-    // scores: four threads per cache row, each a 32-dim quarter (64 contiguous bytes)
+    if (owner) {  // the new row replaces the stale cache row staged above
+        if (j == 0) {
+            ks[p - t0][l] = nk0;
+            ks[p - t0][l + 64] = nk1;
+        } else if (j == 1) {
+            vs[p - t0][l] = nv0;
+            vs[p - t0][l + 64] = nv1;
+        }
+        __syncthreads();
+    }
+    // scores of the 4 query heads for this thread's row quarter, summed over the DPP quad
     {
-        const int tl = tid >> 2, qd = tid & 3, t = t0 + tl;
         float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-        if (t <= p) {
-            const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
+        const uint4* kq = reinterpret_cast<const uint4*>(&ks[tl][32 * qd]);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint4 v = kr[c];
-                const uint32_t kw[4] = {v.x, v.y, v.z, v.w};
+        for (int c = 0; c < 4; ++c) {
+            const uint4 kv = kq[c];
+            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int d = 32 * qd + 8 * c + 2 * e;
-                    const float k0 = bf16_lo(kw[e]), k1 = bf16_hi(kw[e]);
-                    s0 = fmaf(k1, qs[0][d + 1], fmaf(k0, qs[0][d], s0));
-                    s1 = fmaf(k1, qs[1][d + 1], fmaf(k0, qs[1][d], s1));
-                    s2 = fmaf(k1, qs[2][d + 1], fmaf(k0, qs[2][d], s2));
-                    s3 = fmaf(k1, qs[3][d + 1], fmaf(k0, qs[3][d], s3));
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int d = 32 * qd + 8 * c + 2 * e;
+                const float k0 = bf16_lo(kw[e]), k1 = bf16_hi(kw[e]);
+                s0 = fmaf(k1, qs[0][d + 1], fmaf(k0, qs[0][d], s0));
+                s1 = fmaf(k1, qs[1][d + 1], fmaf(k0, qs[1][d], s1));
+                s2 = fmaf(k1, qs[2][d + 1], fmaf(k0, qs[2][d], s2));
+                s3 = fmaf(k1, qs[3][d + 1], fmaf(k0, qs[3][d], s3));
             }
         }
-        // sum the four quarters (lanes of one DPP quad)
         s0 += dpp_move<0xB1>(s0); s0 += dpp_move<0x4E>(s0);
         s1 += dpp_move<0xB1>(s1); s1 += dpp_move<0x4E>(s1);
         s2 += dpp_move<0xB1>(s2); s2 += dpp_move<0x4E>(s2);
@@ -83,7 +146,6 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
     }
     __syncthreads();
     // softmax within the split: wave j handles query head j, lane l cache row t0 + l
-    const int j = tid / kWave, l = tid & (kWave - 1);
     float m;
     {
         const float v = pr[j][l];
@@ -94,38 +156,62 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
         if (l == 0) denom_s[j] = d;
     }
     __syncthreads();
-    // P.V: lane l owns dims 2l, 2l+1 of query head j
+    // P.V from LDS: lane l owns dims 2l, 2l+1 of query head j (rows after p never enter)
     const int hq = hk * kGroup + j;
     float a0 = 0.f, a1 = 0.f;
     const int rows = min(kSplit, p - t0 + 1);
-    const uint32_t* vr = reinterpret_cast<const uint32_t*>(vc + ((size_t)hk * L + t0) * kHeadDim) + l;
-#pragma unroll 8
-    for (int tl = 0; tl < rows; ++tl) {
-        const uint32_t v = vr[(size_t)tl * (kHeadDim / 2)];
-        const float e = pr[j][tl];
+    for (int r = 0; r < rows; ++r) {
+        const uint32_t v = reinterpret_cast<const uint32_t*>(&vs[r][0])[l];
+        const float e = pr[j][r];
         a0 = fmaf(e, bf16_lo(v), a0);
         a1 = fmaf(e, bf16_hi(v), a1);
     }
     const float den = denom_s[j];
     float* dst = part + ((size_t)hq * S + split) * kHeadDim;
-    dst[2 * l] = a0 / den;
-    dst[2 * l + 1] = a1 / den;
+    reinterpret_cast<float2*>(dst)[l] = make_float2(a0 / den, a1 / den);
     if (l == 0) lse[hq * S + split] = m + logf(den);
 }
 
-// grid 32 query heads, 128 threads (one per dim): merge the splits, bf16 out [32 * 128].
+// grid 32 query heads, 128 threads (one per dim).  The splits holding attended rows are
+// weighted by exp(lse - max lse) and summed in split order.  The first 64 splits' partials
+// (L <= 4096) are loaded together with the lse values, so a typical merge is one round trip.
+constexpr int kMergeChunk = 64;
+
 __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict__ part,
-                                                         const float* __restrict__ lse, uint16_t* __restrict__ out,
-                                                         int S) {
-    const int hq = blockIdx.x, d = threadIdx.x;
+                                                         const float* __restrict__ lse,
+                                                         const int64_t* __restrict__ pos, uint16_t* __restrict__ out,
+                                                         int L, int S) {
+    __shared__ float wts[kMaxSplits];
+    __shared__ float red[2];
+    const int hq = blockIdx.x, d = threadIdx.x, w = d / kWave;
+    const int p = (int)min(max(pos[0], (int64_t)0), (int64_t)(L - 1));
+    const int active = p / kSplit + 1;
+    const float* src = part + (size_t)hq * S * kHeadDim + d;
+    float v[kMergeChunk];
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u) v[u] = u < active ? src[(size_t)u * kHeadDim] : 0.f;
     float mx = -INFINITY;
-    for (int s = 0; s < S; ++s) mx = fmaxf(mx, lse[hq * S + s]);
-    float wsum = 0.f, acc = 0.f;
-    for (int s = 0; s < S; ++s) {
-        const float w = expf(lse[hq * S + s] - mx);  // exp(-inf) = 0 for masked splits
-        wsum += w;
-        acc = fmaf(w, part[((size_t)hq * S + s) * kHeadDim + d], acc);
+    for (int s = d; s < active; s += 128) mx = fmaxf(mx, lse[hq * S + s]);
+    mx = wave_max(mx);
+    if ((d & (kWave - 1)) == 0) red[w] = mx;
+    __syncthreads();
+    mx = fmaxf(red[0], red[1]);
+    __syncthreads();
+    float ws = 0.f;
+    for (int s = d; s < active; s += 128) {
+        const float e = expf(lse[hq * S + s] - mx);
+        wts[s] = e;
+        ws += e;
     }
+    ws = wave_sum(ws);
+    if ((d & (kWave - 1)) == 0) red[w] = ws;
+    __syncthreads();
+    const float wsum = red[0] + red[1];
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u)
+        if (u < active) acc = fmaf(wts[u], v[u], acc);
+    for (int s = kMergeChunk; s < active; ++s) acc = fmaf(wts[s], src[(size_t)s * kHeadDim], acc);
     out[hq * kHeadDim + d] = f32_to_bf16(acc / wsum);
 }
 
@@ -156,15 +242,37 @@ MOSS_API int moss_decode_attention_splits(int L) { return (L + kSplit - 1) / kSp
 
 MOSS_API int moss_decode_attention(const void* q, const void* k_cache, const void* v_cache, const void* position,
                                    void* partial, void* lse, void* out, int L, void* stream) {
-    MOSS_CHECK_ARG(q && k_cache && v_cache && position && partial && lse && out && L > 0);
-    MOSS_CHECK_ARG(MOSS_ALIGNED(k_cache, 16) && MOSS_ALIGNED(v_cache, 16) && MOSS_ALIGNED(q, 4));
-    const int S = (L + kSplit - 1) / kSplit;
+    MOSS_CHECK_ARG(q && k_cache && v_cache && position && partial && lse && out);
+    MOSS_CHECK_ARG(L > 0 && L % kSplit == 0 && L / kSplit <= kMaxSplits);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(k_cache, 16) && MOSS_ALIGNED(v_cache, 16) && MOSS_ALIGNED(q, 4) &&
+                   MOSS_ALIGNED(partial, 8) && MOSS_ALIGNED(out, 2));
+    const int S = L / kSplit;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(decode_attn_split, dim3(kKvHeads, S), dim3(256), 0, st, (const uint16_t*)q,
-                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
-                       (float*)lse, L, S);
+    hipLaunchKernelGGL(decode_attn_split<false>, dim3(kKvHeads, S), dim3(256), 0, st, (const uint16_t*)q,
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
+                       (float*)lse, L, S, QkvArgs{});
     hipLaunchKernelGGL(decode_attn_merge, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
-                       (const float*)lse, (uint16_t*)out, S);
+                       (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_decode_attention_qkv(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_t,
+                                       const void* sin_t, void* k_cache, void* v_cache, const void* position,
+                                       void* partial, void* lse, void* out, int L, float eps, void* stream) {
+    MOSS_CHECK_ARG(qkv && q_norm_w && k_norm_w && cos_t && sin_t && k_cache && v_cache && position && partial &&
+                   lse && out && eps >= 0.f);
+    MOSS_CHECK_ARG(L > 0 && L % kSplit == 0 && L / kSplit <= kMaxSplits);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(k_cache, 16) && MOSS_ALIGNED(v_cache, 16) && MOSS_ALIGNED(qkv, 4) &&
+                   MOSS_ALIGNED(partial, 8) && MOSS_ALIGNED(out, 2));
+    const int S = L / kSplit;
+    hipStream_t st = (hipStream_t)stream;
+    const QkvArgs qa{(const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,
+                     (const uint16_t*)sin_t, eps};
+    hipLaunchKernelGGL(decode_attn_split<true>, dim3(kKvHeads, S), dim3(256), 0, st, (const uint16_t*)qkv,
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
+                       (float*)lse, L, S, qa);
+    hipLaunchKernelGGL(decode_attn_merge, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
+                       (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S);
     return moss_launch_status();
 }
 

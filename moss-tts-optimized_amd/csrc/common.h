@@ -98,6 +98,20 @@ __device__ __forceinline__ uint32_t dequant_pair_exact(uint32_t d, uint32_t s_lo
     return w;
 }
 
+// One 128-dim head through RMSNorm + rotate-half RoPE, one wave per head: lane l holds dims
+// l and l + 64 (each other's RoPE partners).  Rounding points of the reference
+// (src/moss_tts/_runtime/kernels.py:142-170): xn = bf16(bf16(x * r) * w); out_l =
+// bf16(bf16(xn_l * cos_l) + bf16(-xn_{l+64} * sin_l)), out_{l+64} = bf16(bf16(xn_{l+64} *
+// cos_{l+64}) + bf16(xn_l * sin_{l+64})), the negation being float negation.
+__device__ __forceinline__ void head_norm_rope(float a, float b, float w0, float w1, float c0, float c1, float s0,
+                                               float s1, float eps, uint16_t& o0, uint16_t& o1) {
+    const float r = rsqrtf(wave_sum(a * a + b * b) / 128.0f + eps);
+    const float an = round_bf16(round_bf16(a * r) * w0);
+    const float bn = round_bf16(round_bf16(b * r) * w1);
+    o0 = f32_to_bf16(round_bf16(an * c0) + round_bf16((-bn) * s0));
+    o1 = f32_to_bf16(round_bf16(bn * c1) + round_bf16(an * s1));
+}
+
 }  // namespace moss
 
 // ---------------------------------------------------------------- host-side plumbing

@@ -112,17 +112,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
     const uint16_t* wt = is_q ? qw : kw;
     const float a = bf16_bits(qkv[base + l]);       // dim l
     const float b = bf16_bits(qkv[base + l + 64]);  // dim l + 64
-    const float r = rsqrtf(wave_sum(a * a + b * b) / (float)D + eps);
-    const float an = round_bf16(round_bf16(a * r) * bf16_bits(wt[l]));
-    const float bn = round_bf16(round_bf16(b * r) * bf16_bits(wt[l + 64]));
     // positions are validated on the host; the clamp keeps every cache/table access in range
     const int64_t p = min(max(pos[t], (int64_t)0), (int64_t)(L - 1));
     const size_t crow = cos_by_position ? (size_t)p : (size_t)t;  // table row: by position or token
     const float c0 = bf16_bits(cos_t[crow * D + l]), c1 = bf16_bits(cos_t[crow * D + l + 64]);
     const float s0 = bf16_bits(sin_t[crow * D + l]), s1 = bf16_bits(sin_t[crow * D + l + 64]);
-    // d = l < 64: partner is bn, negated;  d = l + 64: partner is an
-    const uint16_t o0 = f32_to_bf16(round_bf16(an * c0) + round_bf16((-bn) * s0));
-    const uint16_t o1 = f32_to_bf16(round_bf16(bn * c1) + round_bf16(an * s1));
+    uint16_t o0, o1;
+    head_norm_rope(a, b, bf16_bits(wt[l]), bf16_bits(wt[l + 64]), c0, c1, s0, s1, eps, o0, o1);
     if (is_q) {
         uint16_t* dst = q_out + ((size_t)t * QH + h) * D;
         dst[l] = o0;

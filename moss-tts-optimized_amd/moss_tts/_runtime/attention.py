@@ -24,7 +24,8 @@ def splits(L: int) -> int:
 
 
 def workspace(L: int, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """(partial fp32 [32, S, 128], lse fp32 [32, S]) for a cache of ``L`` rows."""
+    """(partial fp32 [32, S, 128], lse fp32 [32, S]) for a cache of ``L`` rows; calls that
+    share a workspace must not overlap (one stream, or one graph)."""
     s = splits(L)
     return (torch.empty((QH, s, HD), device=device, dtype=torch.float32),
             torch.empty((QH, s), device=device, dtype=torch.float32))
@@ -33,7 +34,8 @@ def workspace(L: int, device) -> tuple[torch.Tensor, torch.Tensor]:
 def decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, position: torch.Tensor,
                      *, out: torch.Tensor | None = None, ws=None) -> torch.Tensor:
     """One decode token: ``q`` bf16 (32*128 values), ``keys``/``values`` bf16 ``[1, 8, L, 128]``
-    (one layer), ``position`` int64 ``[1]`` on the device.  Returns bf16 ``[1, 1, 4096]``."""
+    (one layer, L a multiple of 64), ``position`` int64 ``[1]`` on the device.  Returns bf16
+    ``[1, 1, 4096]``."""
     _cuda_contig("q", q, torch.bfloat16)
     dev = q.device
     _require(q.numel() == QH * HD, f"q must hold {QH}x{HD} values")
@@ -45,12 +47,49 @@ def decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, 
     _require(position.numel() == 1, "one int64 position required")
     _require(_aligned(keys, 16) and _aligned(values, 16), "KV buffers must be 16-byte aligned")
     L = keys.shape[2]
+    _require(L % 64 == 0 and L <= 32768, "the cache length must be a multiple of 64, at most 32768")
     partial, lse = ws if ws is not None else workspace(L, dev)
     _require(partial.numel() >= QH * splits(L) * HD and lse.numel() >= QH * splits(L), "workspace too small")
     if out is None:
         out = torch.empty((1, 1, QH * HD), device=dev, dtype=torch.bfloat16)
     native.call("moss_decode_attention", native.ptr(q), native.ptr(keys), native.ptr(values), native.ptr(position),
                 native.ptr(partial), native.ptr(lse), native.ptr(out), L, native.stream_of(q))
+    return out
+
+
+def decode_attention_qkv(qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, cos: torch.Tensor,
+                         sin: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, position: torch.Tensor,
+                         eps: float, *, out: torch.Tensor | None = None, ws=None) -> torch.Tensor:
+    """q/k head-norm + RoPE + KV-cache write + decode attention in one pass
+    (``src/moss_tts/_runtime/kernels.py:211-251``): ``qkv`` bf16 (6144 values: q | k | v),
+    head-norm weights bf16 [128], cos/sin bf16 ``[L, 128]`` tables indexed by the device
+    position; K/V row ``position`` of the cache is written.  Returns bf16 ``[1, 1, 4096]``,
+    bit-identical to ``qk_rope`` followed by ``decode_attention``."""
+    _cuda_contig("qkv", qkv, torch.bfloat16)
+    dev = qkv.device
+    _require(qkv.numel() == (QH + 2 * KH) * HD, "one q||k||v row of 6144 values required")
+    for name, t in (("keys", keys), ("values", values)):
+        _cuda_contig(name, t, torch.bfloat16, dev)
+    _require(keys.shape == values.shape and keys.ndim == 4 and tuple(keys.shape[:2]) == (1, KH)
+             and keys.shape[3] == HD, "matching [1, 8, L, 128] KV buffers required")
+    L = keys.shape[2]
+    _require(L % 64 == 0 and L <= 32768, "the cache length must be a multiple of 64, at most 32768")
+    for name, t in (("q_norm", q_norm), ("k_norm", k_norm)):
+        _cuda_contig(name, t, torch.bfloat16, dev)
+        _require(t.numel() == HD, f"{name} must hold {HD} values")
+    for name, t in (("cos", cos), ("sin", sin)):
+        _cuda_contig(name, t, torch.bfloat16, dev)
+        _require(t.numel() == L * HD, f"{name} must be an [L, {HD}] table")
+    _cuda_contig("position", position, torch.int64, dev)
+    _require(position.numel() == 1, "one int64 position required")
+    _require(_aligned(keys, 16) and _aligned(values, 16), "KV buffers must be 16-byte aligned")
+    partial, lse = ws if ws is not None else workspace(L, dev)
+    _require(partial.numel() >= QH * splits(L) * HD and lse.numel() >= QH * splits(L), "workspace too small")
+    if out is None:
+        out = torch.empty((1, 1, QH * HD), device=dev, dtype=torch.bfloat16)
+    native.call("moss_decode_attention_qkv", native.ptr(qkv), native.ptr(q_norm), native.ptr(k_norm),
+                native.ptr(cos), native.ptr(sin), native.ptr(keys), native.ptr(values), native.ptr(position),
+                native.ptr(partial), native.ptr(lse), native.ptr(out), L, float(eps), native.stream_of(qkv))
     return out
 
 

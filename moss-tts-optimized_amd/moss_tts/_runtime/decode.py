@@ -1,8 +1,9 @@
 """Batch-1 decode step of the Qwen3-8B backbone on the gfx950 kernels, captured as one graph.
 
 Per layer (the order of ``src/moss_tts/_runtime/llm.py:227-260`` with fused residuals):
-add-RMSNorm + q||k||v GEMV (one kernel) -> q/k head-norm + RoPE + KV write -> split-K GQA
-attention -> O GEMV -> add-RMSNorm + gate||up GEMV with SiLU*mul (one kernel) -> down GEMV.  The step starts with the
+add-RMSNorm + q||k||v GEMV (one kernel) -> q/k head-norm + RoPE + KV write + split GQA
+attention (one kernel) -> split merge -> O GEMV -> add-RMSNorm + gate||up GEMV with SiLU*mul
+(one kernel) -> down GEMV.  The step starts with the
 33-row embedding sum (``src/moss_tts/_runtime/kernels.py:7-26``) and ends with the final norm
 and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``),
 here INT4-G32 as well.  Static input buffers (ids, position) make the step graph-capturable;
@@ -15,7 +16,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import attention, pointwise, w4g32
+from . import attention, w4g32
 from .modules import QuantGateUpG32, QuantLinearG32
 from .w4g32 import _require
 
@@ -93,9 +94,8 @@ class DecodeStepG32:
             else:
                 residual, qkv = w4g32.norm_gemv(mlp, layer.input_norm, eps, layer.qkv.packed, residual=residual,
                                                 dequant=layer.qkv.dequant)
-            q = pointwise.qk_rope(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
-                                  self.values[i], self.position, eps, cos_by_position=True)
-            attn = attention.decode_attention(q, self.keys[i], self.values[i], self.position, ws=self.ws)
+            attn = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
+                                                  self.values[i], self.position, eps, ws=self.ws)
             o = layer.o(attn.view(1, HIDDEN))
             residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
                                                    residual=residual, dequant=layer.gate_up.dequant)

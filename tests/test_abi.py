@@ -60,7 +60,7 @@ def test_host_only_entry_points(lib):
     assert lib.moss_abi_version() == 1
     assert lib.moss_error_string(0)
     assert lib.moss_decode_attention_splits(2048) == 32
-    assert lib.moss_decode_attention_splits(96) == 2
+    assert lib.moss_decode_attention_splits(128) == 2
 
 
 def test_argument_errors_are_rejected_before_launch(lib):

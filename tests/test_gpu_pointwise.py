@@ -87,7 +87,8 @@ def test_silu_mul(dev, rows, n):
     _close(pointwise.silu_mul(x.to(dev)), p.silu_mul(x), f"silu_mul {rows}x{n}")
 
 
-@pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (96, 95)])
+@pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (128, 127),
+                                        (32768, 20000)])
 def test_decode_attention(dev, L, position):
     """Split-softmax GQA decode attention vs the oracle's exact fp32 softmax; bf16 output."""
     from moss_tts._runtime import attention
@@ -99,9 +100,46 @@ def test_decode_attention(dev, L, position):
     kc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
     vc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
     pos = torch.tensor([position], dtype=torch.int64)
-    out = attention.decode_attention(q.to(dev), kc.to(dev), vc.to(dev), pos.to(dev))
+    ws = attention.workspace(L, dev)
+    out = attention.decode_attention(q.to(dev), kc.to(dev), vc.to(dev), pos.to(dev), ws=ws)
     ref = oa.decode_attention(q, kc, vc, position).reshape(1, 1, 4096)
     _close(out, ref.bfloat16(), f"attention L={L} p={position}", exact_frac=0.95)
+    # a second call on the same workspace reproduces the first bit for bit
+    again = attention.decode_attention(q.to(dev), kc.to(dev), vc.to(dev), pos.to(dev), ws=ws)
+    assert torch.equal(out, again)
+
+
+def test_decode_attention_rejects_unaligned_length(dev):
+    from moss_tts._runtime import attention
+
+    q = torch.zeros((32, 128), device=dev, dtype=torch.bfloat16)
+    kc = torch.zeros((1, 8, 96, 128), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        attention.decode_attention(q, kc, kc.clone(), torch.zeros(1, device=dev, dtype=torch.int64))
+
+
+@pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (128, 5)])
+def test_fused_qkv_attention_equals_rope_then_attention(dev, L, position):
+    """q/k-norm + RoPE + KV write fused into the attention kernel reproduces moss_qk_norm_rope_kv
+    followed by moss_decode_attention bit for bit, output and both caches."""
+    from moss_tts._runtime import attention, pointwise
+
+    print(f"fused qkv attention L={L} p={position}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(L + position)
+    qkv = (torch.randn((1, 6144), device=dev, generator=g) * 2).bfloat16()
+    qn = (1 + 0.05 * torch.randn(128, device=dev, generator=g)).bfloat16()
+    kn = (1 + 0.05 * torch.randn(128, device=dev, generator=g)).bfloat16()
+    cos, sin = p.rope_tables(torch.arange(L))
+    cos, sin = cos.to(dev), sin.to(dev)
+    kc = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    vc = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    pos = torch.tensor([position], device=dev)
+    k1, v1, k2, v2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    q = pointwise.qk_rope(qkv, qn, kn, cos, sin, k1, v1, pos, 1e-6, cos_by_position=True)
+    ref = attention.decode_attention(q, k1, v1, pos)
+    out = attention.decode_attention_qkv(qkv, qn, kn, cos, sin, k2, v2, pos, 1e-6)
+    assert torch.equal(out, ref)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
 
 
 def test_decode_attention_ignores_rows_after_position(dev):
