@@ -304,8 +304,12 @@ __device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const 
     if (NORM == 0 && row0 >= n_out) return;  // wave-uniform
 
     constexpr int NR = PAIRED ? 2 * R : R;
+    // The activations are loaded before the weight rows: vector-memory completions are counted
+    // in order, so row 0 can then be computed while later rows are still arriving.
     NormLoad<(NORM > 0 ? KG : 1)> nl;
+    XSlice<KG> xs;
     if constexpr (NORM > 0) norm_load<NORM, KG>(nl, x, na);
+    else load_x<KG, !EXACT, FULL>(xs, x, lane, G);
     RowLoad<KG> rows[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -313,15 +317,12 @@ __device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const 
         const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
         load_row_nt<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
     }
-    XSlice<KG> xs;
     if constexpr (NORM > 0) {
         __shared__ __attribute__((aligned(16))) uint16_t xn[2048 * KG];
         __shared__ float red[4];
         norm_into_lds<NORM, KG>(nl, na, xn, red, 32 * G);
         if (row0 >= n_out) return;  // after the workgroup's barriers
         load_x<KG, !EXACT, FULL>(xs, xn, lane, G);
-    } else {
-        load_x<KG, !EXACT, FULL>(xs, x, lane, G);
     }
 
     const Magic m = make_magic();
@@ -379,6 +380,8 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
     if (row0 >= n_out) return;  // uniform across the workgroup
     const int g0 = 128 * slice;
 
+    XSlice<2> xs;
+    load_x<2, !EXACT, true>(xs, x + 32 * g0, lane, 128);  // first: see gemv_rows
     RowLoad<2> rows[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -386,8 +389,6 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
         const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
         load_row_slice<true>(rows[r], qw, sc, zp, n, lane, G, g0);
     }
-    XSlice<2> xs;
-    load_x<2, !EXACT, true>(xs, x + 32 * g0, lane, 128);
     const Magic m = make_magic();
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -571,7 +572,9 @@ int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, v
         if (mode == MOSS_DEQUANT_UNROUNDED) return launch_ksplit<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
         return (int)hipErrorInvalidValue;
     }
-    if (rows == 0) rows = (G <= 128) ? (PAIRED ? 2 : 4) : (G <= 256 ? 2 : 1);
+    // measured on MI355X (K = 4096): 2 rows per wave is best for the exact mode in both roles;
+    // the unrounded GEMV is as fast at 4 and the unrounded gate||up at 2
+    if (rows == 0) rows = (G <= 128) ? ((PAIRED || mode == MOSS_DEQUANT_EXACT) ? 2 : 4) : (G <= 256 ? 2 : 1);
     if (mode == MOSS_DEQUANT_EXACT)
         return launch_gemv_mode<PAIRED, true, NORM>(x, qw, sc, zp, y, G, n_out, rows, na, st);
     if (mode == MOSS_DEQUANT_UNROUNDED)
