@@ -103,20 +103,27 @@ int moss_w4g32_norm_gateup_silu(const void *x, const void *res, const void *norm
 /* ------------------------------------------------------------- prefill GEMM */
 /* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);
  * weights are dequantized bit-exactly (bf16_rne((q-z)*s)) into LDS and multiplied with
- * v_mfma_f32_32x32x16_bf16, fp32 accumulate.  The reference runs bf16 F.linear here
- * (src/moss_tts/_runtime/llm.py:29,84,130); its INT4 contract is dequant + F.linear
- * (src/moss_tts/calibration.py:185-188). */
+ * v_mfma_f32_32x32x16_bf16, fp32 accumulate.  When the output tiles alone cannot fill the GPU
+ * (small M) the K dimension is split over workgroups: that needs a caller-owned fp32 workspace
+ * of moss_gemm_workspace_bytes(M, K, N) bytes (16-byte aligned; y 8-byte aligned); with a
+ * NULL or smaller workspace the GEMM runs unsplit.  Partial sums are added in a fixed order.
+ * The reference runs bf16 F.linear here (src/moss_tts/_runtime/llm.py:29,84,130); its INT4
+ * contract is dequant + F.linear (src/moss_tts/calibration.py:185-188). */
 int moss_w4g32_gemm(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
-                    void *stream);
+                    void *workspace, long long workspace_bytes, void *stream);
+
+/* Workspace bytes the GEMMs (INT4 and FP8, M > 1) use for an M x K x N problem; 0 = none. */
+long long moss_gemm_workspace_bytes(int M, int K, int N);
 
 /* --------------------------------------------------- FP8 E4M3 weight-only */
 /* W e4m3 (OCP) [N, K] row-major bytes (16-byte aligned), scale fp32 [N] or NULL (= 1):
  * y bf16 [M, N] = bf16(scale[n] * sum_k f32(W[n,k]) * x[m,k]), fp32 accumulate.
  * M == 1: decode GEMV (K % 16 == 0, K <= 16384, rows_per_wave in {0 (auto), 1, 2, 4});
- * M > 1: MFMA GEMM with exact e4m3 -> bf16 weights (K % 64 == 0).  Arithmetic of
- * _fp8_silu_gemv, src/moss_tts/_runtime/fused_mlp.py:7-23, without the SiLU epilogue. */
+ * M > 1: MFMA GEMM with exact e4m3 -> bf16 weights (K % 64 == 0), optionally split over K
+ * with the workspace described at moss_w4g32_gemm.  Arithmetic of _fp8_silu_gemv,
+ * src/moss_tts/_runtime/fused_mlp.py:7-23, without the SiLU epilogue. */
 int moss_fp8_linear(const void *x, const void *w, const void *scale, void *y, int M, int K, int N,
-                    int rows_per_wave, void *stream);
+                    int rows_per_wave, void *workspace, long long workspace_bytes, void *stream);
 
 /* Fused gate||up FP8 decode GEMV: W e4m3 [2*N_half, K] (gate rows first), scale fp32
  * [2*N_half] or NULL, M must be 1; y bf16 [N_half] = bf16(bf16(silu(bf16(g*sg))) *

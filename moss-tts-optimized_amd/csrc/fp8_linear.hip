@@ -19,8 +19,8 @@
 
 namespace moss {
 
-int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* y, int M, int K, int N,
-                    hipStream_t stream);
+int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* y, int M, int K, int N, void* ws,
+                    long long ws_bytes, hipStream_t stream);
 
 namespace {
 
@@ -158,15 +158,15 @@ __global__ __launch_bounds__(256) void fp8_to_bf16_kernel(const uint32_t* __rest
 using namespace moss;
 
 MOSS_API int moss_fp8_linear(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
-                             int rows_per_wave, void* stream) {
+                             int rows_per_wave, void* workspace, long long workspace_bytes, void* stream) {
     MOSS_CHECK_ARG(x && w && y && M > 0 && N > 0 && K > 0);
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(w, 16) && MOSS_ALIGNED(y, 2));
     if (M == 1) {
         MOSS_CHECK_ARG(K % 16 == 0 && K <= 16384);
         return launch_gemv<false>(x, w, (const float*)scale, y, K, N, rows_per_wave, (hipStream_t)stream);
     }
-    MOSS_CHECK_ARG(K % 64 == 0);
-    return fp8_gemm_launch(x, w, (const float*)scale, y, M, K, N, (hipStream_t)stream);
+    MOSS_CHECK_ARG(K % 64 == 0 && workspace_bytes >= 0);
+    return fp8_gemm_launch(x, w, (const float*)scale, y, M, K, N, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 MOSS_API int moss_fp8_gateup_silu(const void* x, const void* w, const void* scale, void* y, int M, int K,

@@ -11,11 +11,17 @@
 // epilogue (src/moss_tts/_runtime/fused_mlp.py:20-21).  The fp8 MFMA forms are not used:
 // they would round the bf16 activations to e4m3 as well.
 //
-// Tile: BM x BN outputs per 256-thread workgroup (2 x 2 waves, each 2 x 2 MFMA tiles of
-// 32 x 32), K in steps of 64 (two quantization groups).  Per step each thread dequantizes
-// one 32-code group (or converts 32 e4m3 bytes) of one weight row and copies 32
-// activations; the next step's global loads are issued into registers before the current
-// step's MFMAs.
+// Tile: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
+// (BM/2) x (BN/2), K in steps of 64 (two quantization groups).  Pipeline: two LDS buffers and
+// two register stages; step st + 2 is loaded from global memory while step st is multiplied and
+// step st + 1 is converted into the other LDS buffer, so each load has two steps of MFMA work
+// to arrive, with one barrier per step.
+// Split-K (SPLIT): workgroup z of a tile covers K range [z K/S, (z+1) K/S) and stores fp32
+// partial sums; gemm_reduce adds them in z order (deterministic) and applies the epilogue.
+// It is used when the tiles alone cannot fill the 256 CUs (small M).
+// Tile order: logical tiles are n-major with the M tiles of one N tile adjacent, and the
+// workgroup id is remapped so that consecutive logical tiles run on the same XCD (workgroups
+// are dealt to the 8 XCDs round-robin), so a weight tile is fetched into one L2.
 #include "common.h"
 
 namespace moss {
@@ -27,40 +33,43 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kBK = 64;
 constexpr int kPad = 8;  // bf16 padding per LDS row: breaks the 128-byte bank period
 constexpr int kLds = kBK + kPad;
+constexpr int kXcds = 8;
 
 enum WeightFormat { kInt4G32 = 0, kFp8E4M3 = 1 };
 
+// Per-thread share of one K step: BM rows x 64 activations (BM / 32 uint4 per thread) and one
+// (row, 32-wide half) of the weight tile.
+template <int BM>
 struct StepRegs {
-    uint4 x[4];     // 32 activations of one X row
-    uint4 w[2];     // INT4: w[0] = 32 codes of one weight row; FP8: 32 e4m3 bytes
-    uint32_t s, z;  // INT4: its group's scale bits and zero point
+    uint4 x[BM / 32];
+    uint4 w[2];     // INT4: w[0] = 32 codes; FP8: 32 e4m3 bytes
+    uint32_t s, z;  // INT4: the group's scale bits and zero point
 };
 
 template <int BM, int BN, int FMT>
-__device__ __forceinline__ void load_step(StepRegs& r, const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
-                                          const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp, int M,
-                                          int N, int K, int G, int m0, int n0, int k0, int tid) {
-    const int row = tid >> 1, half = tid & 1;
-    // activations: thread -> (row, 32-wide half of the step); rows beyond M read as zero
+__device__ __forceinline__ void load_step(StepRegs<BM>& r, const uint16_t* __restrict__ X,
+                                          const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
+                                          const uint8_t* __restrict__ zp, int M, int N, int K, int G, int m0,
+                                          int n0, int k0, int tid) {
+    // activations: 256 / BM threads per row, each BM / 32 uint4; rows beyond M read as zero
+    constexpr int TPR = 256 / BM, CH = 8 / TPR;
+    {
+        const int row = tid / TPR, part = tid % TPR, m = m0 + row;
+        if (m < M) {
+            const uint4* p = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0) + CH * part;
 #pragma unroll
-    for (int rr = 0; rr < BM / 128; ++rr) {
-        const int m = m0 + row + 128 * rr;
-        if (rr == 0) {
-            if (m < M) {
-                const uint4* p = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0 + 32 * half);
+            for (int c = 0; c < CH; ++c) r.x[c] = p[c];
+        } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) r.x[c] = p[c];
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) r.x[c] = make_uint4(0u, 0u, 0u, 0u);
-            }
+            for (int c = 0; c < CH; ++c) r.x[c] = make_uint4(0u, 0u, 0u, 0u);
         }
     }
     // weights: thread -> (row, 32-wide half of the step)
-    const int n = n0 + row;
+    const int row = tid >> 1, half = tid & 1, n = n0 + row;
+    const bool ok = row < BN && n < N;
     if constexpr (FMT == kInt4G32) {
         const int g = (k0 >> 5) + half;
-        if (row < BN && n < N) {
+        if (ok) {
             r.w[0] = qw[(size_t)n * G + g];
             r.s = sc[(size_t)n * G + g];
             r.z = zero_of_group(zp + (size_t)n * (G >> 1), g, G);
@@ -70,9 +79,9 @@ __device__ __forceinline__ void load_step(StepRegs& r, const uint16_t* __restric
             r.z = 0u;
         }
     } else {
-        if (row < BN && n < N) {
-            const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(qw) + (size_t)n * K + k0 +
-                                                            32 * half);
+        if (ok) {
+            const uint4* p =
+                reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(qw) + (size_t)n * K + k0 + 32 * half);
             r.w[0] = p[0];
             r.w[1] = p[1];
         } else {
@@ -88,141 +97,237 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
 }
 
 template <int BM, int BN, int FMT>
-__device__ __forceinline__ void store_step(const StepRegs& r, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds], int tid) {
+__device__ __forceinline__ void store_step(const StepRegs<BM>& r, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds],
+                                           int tid) {
+    constexpr int TPR = 256 / BM, CH = 8 / TPR;
+    {
+        const int row = tid / TPR, part = tid % TPR;
+        uint4* a = reinterpret_cast<uint4*>(&As[row][0]) + CH * part;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) a[c] = r.x[c];
+    }
     const int row = tid >> 1, half = tid & 1;
-    uint4* a = reinterpret_cast<uint4*>(&As[row][32 * half]);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) a[c] = r.x[c];
+    if (row >= BN) return;
+    uint32_t out[16];
     if constexpr (FMT == kFp8E4M3) {
-        if (row < BN) {
-            const uint32_t words[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
-            uint32_t out[16];
+        const uint32_t words[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                out[2 * c] = fp8x2_to_bf16x2<false>(words[c]);
-                out[2 * c + 1] = fp8x2_to_bf16x2<true>(words[c]);
-            }
-            uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * half]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) b[c] = make_uint4(out[4 * c], out[4 * c + 1], out[4 * c + 2], out[4 * c + 3]);
+        for (int c = 0; c < 8; ++c) {
+            out[2 * c] = fp8x2_to_bf16x2<false>(words[c]);
+            out[2 * c + 1] = fp8x2_to_bf16x2<true>(words[c]);
         }
-        return;
-    } else if (row < BN) {
+    } else {
         uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
         asm volatile("" : "+v"(mask), "+v"(bias_bits));
         const uint32_t s_lo = r.s & 0xffffu, s_hi = s_lo << 16;
         const float bias = -(128.0f + (float)r.z) * bf16_bits((uint16_t)s_lo);
         const uint32_t words[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
-        uint32_t out[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 out[4 * j + i] = dequant_pair_exact(((words[j] >> (4 * i)) & mask) | bias_bits, s_lo, s_hi, bias);
-        uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * half]);
+    }
+    uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * half]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) b[c] = make_uint4(out[4 * c], out[4 * c + 1], out[4 * c + 2], out[4 * c + 3]);
+    for (int c = 0; c < 4; ++c) b[c] = make_uint4(out[4 * c], out[4 * c + 1], out[4 * c + 2], out[4 * c + 3]);
+}
+
+template <int BM, int BN>
+__device__ __forceinline__ void mfma_step(const uint16_t (*As)[kLds], const uint16_t (*Bs)[kLds],
+                                          f32x16_t (&acc)[BM / 64][BN / 64], int lane, int wm, int wn) {
+    constexpr int TM = BM / 64, TN = BN / 64;  // 32 x 32 MFMA tiles per wave
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+        const int kc = 16 * kk + 8 * (lane >> 5);
+        bf16x8_t a[TM], b[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            a[i] = *reinterpret_cast<const bf16x8_t*>(&As[(BM / 2) * wm + 32 * i + (lane & 31)][kc]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            b[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[(BN / 2) * wn + 32 * j + (lane & 31)][kc]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
 }
 
 // FMT == kFp8E4M3: qw is e4m3 [N, K] (row-major bytes), `row_scale` fp32 [N] or null.
-template <int BM, int BN, int FMT>
+// SPLIT: `part` is fp32 [S, M, N]; gridDim.y = S.
+template <int BM, int BN, int FMT, bool SPLIT>
 __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
                                                          const uint16_t* __restrict__ sc,
                                                          const uint8_t* __restrict__ zp, uint16_t* __restrict__ Y,
-                                                         int M, int N, int K, const float* __restrict__ row_scale) {
-    static_assert(BM == 128 && (BN == 128 || BN == 64), "tile");
-    constexpr int WN = BN / 2;             // wave tile columns (2 x 2 waves)
-    constexpr int TN = WN / 32;            // 32-wide MFMA tiles per wave along N
-    __shared__ __attribute__((aligned(16))) uint16_t As[BM][kLds];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[BN][kLds];
+                                                         float* __restrict__ part, int M, int N, int K,
+                                                         const float* __restrict__ row_scale) {
+    static_assert((BM == 64 || BM == 128) && (BN == 64 || BN == 128), "tile");
+    constexpr int TM = BM / 64, TN = BN / 64;
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][kLds];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int G = K >> 5, steps = K / kBK;
+    // XCD-aware logical tile (n-major, M tiles of one N tile adjacent)
+    const int mt = (M + BM - 1) / BM, tiles = gridDim.x;
+    int tile = blockIdx.x;
+    if (tiles % kXcds == 0) tile = (blockIdx.x % kXcds) * (tiles / kXcds) + blockIdx.x / kXcds;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+    const int G = K >> 5;
+    const int steps = K / kBK / gridDim.y;
+    const int kbase = blockIdx.y * steps * kBK;
 
-    f32x16_t acc[2][TN];
+    f32x16_t acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    StepRegs r;
-    load_step<BM, BN, FMT>(r, X, qw, sc, zp, M, N, K, G, m0, n0, 0, tid);
-    for (int st = 0; st < steps; ++st) {
-        store_step<BM, BN, FMT>(r, As, Bs, tid);
+    StepRegs<BM> r0, r1;
+    load_step<BM, BN, FMT>(r0, X, qw, sc, zp, M, N, K, G, m0, n0, kbase, tid);
+    if (steps > 1) load_step<BM, BN, FMT>(r1, X, qw, sc, zp, M, N, K, G, m0, n0, kbase + kBK, tid);
+    store_step<BM, BN, FMT>(r0, As[0], Bs[0], tid);
+    __syncthreads();
+    // two steps per trip so the register stages and LDS buffers are named statically; an odd
+    // last step (in buffer 0) is peeled off after the loop
+    int st = 0;
+    for (; st + 1 < steps; st += 2) {
+        if (st + 2 < steps) load_step<BM, BN, FMT>(r0, X, qw, sc, zp, M, N, K, G, m0, n0, kbase + (st + 2) * kBK, tid);
+        mfma_step<BM, BN>(As[0], Bs[0], acc, lane, wm, wn);
+        store_step<BM, BN, FMT>(r1, As[1], Bs[1], tid);
         __syncthreads();
-        if (st + 1 < steps) load_step<BM, BN, FMT>(r, X, qw, sc, zp, M, N, K, G, m0, n0, (st + 1) * kBK, tid);
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int kc = 16 * kk + 8 * (lane >> 5);
-            bf16x8_t a[2], b[TN];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[64 * wm + 32 * i + (lane & 31)][kc]);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                b[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[WN * wn + 32 * j + (lane & 31)][kc]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
+        if (st + 3 < steps) load_step<BM, BN, FMT>(r1, X, qw, sc, zp, M, N, K, G, m0, n0, kbase + (st + 3) * kBK, tid);
+        mfma_step<BM, BN>(As[1], Bs[1], acc, lane, wm, wn);
+        if (st + 2 < steps) store_step<BM, BN, FMT>(r0, As[0], Bs[0], tid);
         __syncthreads();
     }
+    if (st < steps) mfma_step<BM, BN>(As[0], Bs[0], acc, lane, wm, wn);
     // C layout of a 32 x 32 tile: lane l, element e -> row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int n = n0 + WN * wn + 32 * j + (lane & 31);
+            const int n = n0 + (BN / 2) * wn + 32 * j + (lane & 31);
             if (n >= N) continue;
             // FP8: the per-row scale multiplies the finished sum (src/moss_tts/_runtime/fused_mlp.py:20-21)
-            const float rs = (FMT == kFp8E4M3 && row_scale) ? row_scale[n] : 1.0f;
+            const float rs = (!SPLIT && FMT == kFp8E4M3 && row_scale) ? row_scale[n] : 1.0f;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (m < M) Y[(size_t)m * N + n] = f32_to_bf16(FMT == kFp8E4M3 ? acc[i][j][e] * rs : acc[i][j][e]);
+                const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (m >= M) continue;
+                if constexpr (SPLIT)
+                    part[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
+                else
+                    Y[(size_t)m * N + n] = f32_to_bf16(FMT == kFp8E4M3 ? acc[i][j][e] * rs : acc[i][j][e]);
             }
         }
 }
 
+// y[m, n] = bf16(scale[n] * sum_z part[z, m, n]), z ascending; 4 outputs per thread (N % 4 == 0).
+__global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ part, const float* __restrict__ row_scale,
+                                                   uint16_t* __restrict__ Y, int MN, int N, int S) {
+    const int i = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= MN) return;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < S; ++z) {
+        const float4 v = *reinterpret_cast<const float4*>(part + (size_t)z * MN + i);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    const int n = i % N;  // the 4 outputs share a row
+    float4 s = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (row_scale) s = make_float4(row_scale[n], row_scale[n + 1], row_scale[n + 2], row_scale[n + 3]);
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16(acc.x * s.x) | ((uint32_t)f32_to_bf16(acc.y * s.y) << 16);
+    o.y = (uint32_t)f32_to_bf16(acc.z * s.z) | ((uint32_t)f32_to_bf16(acc.w * s.w) << 16);
+    *reinterpret_cast<uint2*>(Y + i) = o;
+}
+
+struct Plan {
+    int bm, bn, split;
+};
+
+// Tile shape and K split: 64-row tiles for M <= 64; 128-wide N tiles when they already give
+// >= 256 workgroups; a K split (2..8) only for M <= 256 while the tiles give fewer than 256
+// workgroups (the fp32 partials cost 8 M N bytes per split).
+Plan plan_gemm(int M, int K, int N) {
+    Plan p;
+    p.bm = M <= 64 ? 64 : 128;
+    const long mt = (M + p.bm - 1) / p.bm;
+    p.bn = mt * ((N + 127) / 128) >= 256 ? 128 : 64;
+    const long tiles = mt * ((N + p.bn - 1) / p.bn);
+    const int steps = K / kBK;
+    p.split = 1;
+    if (N % 4 == 0 && M <= 256)
+        while (p.split < 8 && tiles * p.split < 256 && steps % (2 * p.split) == 0 && steps / (2 * p.split) >= 4)
+            p.split *= 2;
+    return p;
+}
+
+template <int BM, int BN, int FMT>
+void launch_tile(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* part,
+                 int M, int K, int N, const float* row_scale, hipStream_t st) {
+    const dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)), (unsigned)p.split);
+    if (p.split > 1)
+        hipLaunchKernelGGL((w4g32_gemm_kernel<BM, BN, FMT, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                           (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)part, M,
+                           N, K, row_scale);
+    else
+        hipLaunchKernelGGL((w4g32_gemm_kernel<BM, BN, FMT, false>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                           (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)part, M,
+                           N, K, row_scale);
+}
+
 template <int FMT>
 int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K, int N,
-                const float* row_scale, hipStream_t st) {
-    const int mt = (M + 127) / 128;
-    // wide tiles when they already give one workgroup per CU, narrow ones otherwise
-    if ((long)mt * ((N + 127) / 128) >= 256) {
-        hipLaunchKernelGGL((w4g32_gemm_kernel<128, 128, FMT>), dim3((N + 127) / 128, mt), dim3(256), 0, st,
-                           (const uint16_t*)x, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,
-                           (uint16_t*)y, M, N, K, row_scale);
-    } else {
-        hipLaunchKernelGGL((w4g32_gemm_kernel<128, 64, FMT>), dim3((N + 63) / 64, mt), dim3(256), 0, st,
-                           (const uint16_t*)x, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,
-                           (uint16_t*)y, M, N, K, row_scale);
+                const float* row_scale, void* ws, long long ws_bytes, hipStream_t st) {
+    Plan p = plan_gemm(M, K, N);
+    if (p.split > 1 &&
+        (!ws || ws_bytes < (long long)p.split * M * N * 4 || !MOSS_ALIGNED(ws, 16) || !MOSS_ALIGNED(y, 8)))
+        p.split = 1;
+    if (p.bm == 64 && p.bn == 64) launch_tile<64, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
+    else if (p.bm == 64) launch_tile<64, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
+    else if (p.bn == 64) launch_tile<128, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
+    else launch_tile<128, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
+    if (p.split > 1) {
+        const int mn = M * N;
+        hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, st, (const float*)ws,
+                           FMT == kFp8E4M3 ? row_scale : nullptr, (uint16_t*)y, mn, N, p.split);
     }
     return moss_launch_status();
 }
 
 }  // namespace
+
+// FP8 e4m3 rows [N, K] with optional fp32 row scales; arguments checked by the caller.
+int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* y, int M, int K, int N, void* ws,
+                    long long ws_bytes, hipStream_t stream) {
+    return launch_gemm<kFp8E4M3>(x, w, nullptr, nullptr, y, M, K, N, row_scale, ws, ws_bytes, stream);
+}
+
+long long gemm_workspace_bytes(int M, int K, int N) {
+    const Plan p = plan_gemm(M, K, N);
+    return p.split > 1 ? (long long)p.split * M * N * 4 : 0;
+}
+
 }  // namespace moss
 
 using namespace moss;
 
-MOSS_API int moss_w4g32_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
-                             int N, void* stream) {
-    MOSS_CHECK_ARG(x && qw && sc && zp && y && M > 0 && N > 0 && K > 0 && K % 64 == 0);
-    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
-    return launch_gemm<kInt4G32>(x, qw, sc, zp, y, M, K, N, nullptr, (hipStream_t)stream);
+MOSS_API long long moss_gemm_workspace_bytes(int M, int K, int N) {
+    if (M <= 0 || K <= 0 || N <= 0 || K % 64) return 0;
+    return gemm_workspace_bytes(M, K, N);
 }
 
-namespace moss {
-// FP8 e4m3 rows [N, K] with optional fp32 row scales; arguments checked by the caller.
-int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* y, int M, int K, int N,
-                    hipStream_t stream) {
-    return launch_gemm<kFp8E4M3>(x, w, nullptr, nullptr, y, M, K, N, row_scale, stream);
+MOSS_API int moss_w4g32_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
+                             int N, void* workspace, long long workspace_bytes, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && y && M > 0 && N > 0 && K > 0 && K % 64 == 0);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && workspace_bytes >= 0);
+    return launch_gemm<kInt4G32>(x, qw, sc, zp, y, M, K, N, nullptr, workspace, workspace_bytes,
+                                 (hipStream_t)stream);
 }
-}  // namespace moss

@@ -3,7 +3,7 @@
 ``fp8_silu_decode(x, weight, scale=None)`` keeps the reference's signature and meaning
 (``src/moss_tts/_runtime/fused_mlp.py:26-30``): ``weight`` is e4m3 ``[2n, K]`` (gate rows
 first), ``scale`` an optional fp32 ``[2n]``, output bf16 ``[..., n]`` from the first row of
-``x``... here exactly one row is required.  ``linear(x, weight, scale)`` is the plain
+``x`` (the reference reads only its first row; here exactly one row is required).  ``linear(x, weight, scale)`` is the plain
 projection for any number of rows (GEMV for one row, MFMA GEMM for more).  Weights may be
 passed as ``torch.float8_e4m3fn`` or as their ``uint8`` bit patterns.
 """
@@ -52,7 +52,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor | None = N
         _require(k % 64 == 0, "the prefill GEMM needs K % 64 == 0")
     s = _scale_arg(scale, n, w.device)
     y = torch.empty((*x.shape[:-1], n), dtype=torch.bfloat16, device=x.device)
-    native.call("moss_fp8_linear", native.ptr(x), native.ptr(w), s, native.ptr(y), m, k, n, rows_per_wave,
+    wp, wb, _keep = native.gemm_workspace(m, k, n, x.device) if m > 1 else (None, 0, None)
+    native.call("moss_fp8_linear", native.ptr(x), native.ptr(w), s, native.ptr(y), m, k, n, rows_per_wave, wp, wb,
                 native.stream_of(x))
     return y
 

@@ -34,7 +34,8 @@ SIGNATURES: dict[str, list] = {
     "moss_w4g32_quantize_minmax": [_P, _P, _P, _P, _I, _I, _P],
     "moss_w4g32_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_w4g32_gateup_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
-    "moss_w4g32_gemm": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "moss_w4g32_gemm": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
+    "moss_gemm_workspace_bytes": [_I, _I, _I],
     "moss_w4g32_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_w4g32_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
@@ -44,11 +45,11 @@ SIGNATURES: dict[str, list] = {
     "moss_decode_attention": [_P, _P, _P, _P, _P, _P, _P, _I, _P],
     "moss_decode_attention_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P],
     "moss_embedding_sum": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
-    "moss_fp8_linear": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "moss_fp8_linear": [_P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_fp8_gateup_silu": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_fp8_to_bf16": [_P, _P, ctypes.c_longlong, _P],
 }
-_RESTYPES = {"moss_error_string": ctypes.c_char_p}
+_RESTYPES = {"moss_error_string": ctypes.c_char_p, "moss_gemm_workspace_bytes": ctypes.c_longlong}
 
 
 class NativeLibraryMissing(RuntimeError):
@@ -80,6 +81,15 @@ def check(code: int, what: str) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args), name)
+
+
+def gemm_workspace(m: int, k: int, n: int, device) -> tuple:
+    """(pointer, bytes) of a fresh fp32 workspace for an M x K x N GEMM, or (None, 0)."""
+    nbytes = int(lib().moss_gemm_workspace_bytes(int(m), int(k), int(n)))
+    if nbytes == 0:
+        return None, 0, None
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+    return ctypes.c_void_p(ws.data_ptr()), nbytes, ws
 
 
 def stream_of(t: torch.Tensor) -> ctypes.c_void_p:

@@ -264,6 +264,7 @@ def gemm(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
     m = x.numel() // w.K
     _require(m > 0, "empty input")
     y = torch.empty((*x.shape[:-1], w.N), dtype=torch.bfloat16, device=x.device)
+    wp, wb, _keep = native.gemm_workspace(m, w.K, w.N, x.device)
     native.call("moss_w4g32_gemm", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
-                native.ptr(y), m, w.K, w.N, native.stream_of(x))
+                native.ptr(y), m, w.K, w.N, wp, wb, native.stream_of(x))
     return y

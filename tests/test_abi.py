@@ -16,7 +16,7 @@ def _declared() -> dict[str, int]:
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|const char\s*\*)\s*(moss_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|long long|const char\s*\*)\s*(moss_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
     return out
@@ -58,6 +58,9 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_host_only_entry_points(lib):
     assert lib.moss_abi_version() == 1
+    ws = lib.moss_gemm_workspace_bytes(64, 4096, 4096)                            # M=64: K split over workgroups
+    assert ws > 0 and ws % (64 * 4096 * 4) == 0 and ws // (64 * 4096 * 4) in (2, 4, 8)
+    assert lib.moss_gemm_workspace_bytes(512, 4096, 6144) == 0                    # prefill tiles fill the GPU
     assert lib.moss_error_string(0)
     assert lib.moss_decode_attention_splits(2048) == 32
     assert lib.moss_decode_attention_splits(128) == 2
@@ -74,9 +77,9 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4000, 4096, 0, 0, null) == 1          # K % 64
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 3, 0, null) == 1          # rows_per_wave
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 0, 7, null) == 1          # dequant mode
-    assert lib.moss_w4g32_gemm(odd, p, p, p, p, 64, 4096, 4096, null) == 1             # alignment
-    assert lib.moss_fp8_linear(p, p, null, p, 1, 4100, 64, 0, null) == 1                # K % 16
-    assert lib.moss_fp8_linear(p, p, null, p, 2, 4112, 64, 0, null) == 1                # GEMM K % 64
+    assert lib.moss_w4g32_gemm(odd, p, p, p, p, 64, 4096, 4096, null, 0, null) == 1    # alignment
+    assert lib.moss_fp8_linear(p, p, null, p, 1, 4100, 64, 0, null, 0, null) == 1      # K % 16
+    assert lib.moss_fp8_linear(p, p, null, p, 2, 4112, 64, 0, null, 0, null) == 1      # GEMM K % 64
     assert lib.moss_fp8_gateup_silu(p, p, null, p, 2, 4096, 64, 0, null) == 1           # M must be 1
     assert lib.moss_fp8_to_bf16(p, p, 6, null) == 1                                     # count % 4
     assert lib.moss_rmsnorm(p, null, p, null, p, 1, 8200, ctypes.c_float(1e-6), null) == 1   # n <= 8192
