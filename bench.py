@@ -207,13 +207,14 @@ def prefill_bench(torch, dev):
     return out
 
 
-def decode_step_bench(torch, n_layers: int, steps: int, dev):
+def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False):
     """The full batch-1 decode step (embedding -> n_layers -> 32 INT4 heads, KV cache of 2048
-    rows filled with N(0,1), current position 2047) captured as one graph; ms per step."""
+    rows filled with N(0,1), current position 2047) captured as one graph; ms per step.
+    ``w4a8``: the layer projections in the int8-activation arithmetic."""
     from moss_tts._runtime.decode import DecodeStepG32
 
-    _log(f"[bench] building the {n_layers}-layer decode step (random INT4-G32 weights, KV 2048)")
-    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
+    _log(f"[bench] building the {n_layers}-layer decode step (random INT4-G32 weights, KV 2048, w4a8={w4a8})")
+    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242, w4a8=w4a8)
     eng.capture()
     ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
     eng.step(ids, 2047)
@@ -227,10 +228,11 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     nbytes = eng.step_bytes(2047)
-    _log(f"[bench] decode step ({n_layers} layers): {ms:.3f} ms, {nbytes / ms / 1e6:.0f} GB/s")
+    _log(f"[bench] decode step ({n_layers} layers, w4a8={w4a8}): {ms:.3f} ms, {nbytes / ms / 1e6:.0f} GB/s")
     out = {"layers": n_layers, "ms_per_step": round(ms, 4), "bytes_per_step": nbytes,
            "GB/s": round(nbytes / ms / 1e6, 1), "frac_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-           "kv_rows": 2048, "position": 2047, "dequant": "exact", "target_ms": 4.0}
+           "kv_rows": 2048, "position": 2047, "target_ms": 4.0,
+           "arithmetic": "w4a8 (int8 activations, integer dot)" if w4a8 else "w4a16 (exact bf16 dequant)"}
     del eng
     torch.cuda.empty_cache()
     return out
@@ -266,7 +268,7 @@ def main() -> int:
 
     import torch
 
-    from moss_tts._runtime import native, pointwise, w4g32
+    from moss_tts._runtime import native, pointwise, w4a8, w4g32
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -354,6 +356,22 @@ def main() -> int:
     g_unr.replay()
     unr_s = _time_graph(torch, g_unr, max(1, args.steps // cycle)) / cycle
 
+    # the same MLP step in the W4A8 arithmetic: norm + int8 quantizer, gate||up with the fused
+    # output quantizer, down
+    def steps_w4a8(count: int):
+        def run():
+            for i in range(count):
+                gu, dn = copies[i % len(copies)]
+                _, _, act = w4a8.norm_quant(h, None, norm_w, 1e-6, normalized=False)
+                _, mid = w4a8.linear(None, gu, paired=True, fused=True, prequantized=act)
+                w4a8.linear(None, dn, prequantized=mid)
+        return run
+
+    g_w8 = _capture(torch, steps_w4a8(cycle))
+    g_w8.replay()
+    w8_s = _time_graph(torch, g_w8, max(1, args.steps // cycle)) / cycle
+    _log(f"[bench] W4A8 MLP step: {w8_s * 1e6:.2f} us ({MLP_BYTES / w8_s / 1e9:.0f} GB/s)")
+
     # dominant kernel alone: fused gate||up GEMV over the rotating copies
     xs = pointwise.rmsnorm(h, norm_w, 1e-6)
 
@@ -381,13 +399,15 @@ def main() -> int:
          f"down K=12288 N=4096: {dn_s * 1e6:.2f} us, {DOWN_BYTES / dn_s / 1e9:.0f} GB/s")
 
     n_copies = len(copies)
-    del copies, gemv_copies, g_cycle, g_unr, g_rem
+    del copies, gemv_copies, g_cycle, g_unr, g_rem, g_w8
     torch.cuda.empty_cache()
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
     prefill = prefill_bench(torch, dev) if not args.no_extras else None
-    decode = None
+    decode = decode_w4a8 = None
     if args.decode_steps > 0:
         decode = decode_step_bench(torch, args.decode_layers, args.decode_steps, dev)
+        if not args.no_extras:
+            decode_w4a8 = decode_step_bench(torch, args.decode_layers, args.decode_steps, dev, w4a8=True)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -442,10 +462,13 @@ def main() -> int:
             "gateup_unrounded": {"us_per_call": round(gu_unr_s * 1e6, 3),
                                  "GB/s": round(NORM_GATEUP_BYTES / gu_unr_s / 1e9, 1)},
             "mlp_step_unrounded": {"us_per_step": round(unr_s * 1e6, 3), "GB/s": round(MLP_BYTES / unr_s / 1e9, 1)},
+            "mlp_step_w4a8": {"us_per_step": round(w8_s * 1e6, 3), "GB/s": round(MLP_BYTES / w8_s / 1e9, 1),
+                              "arithmetic": "int8 activations per 32-group, integer dot, fp32 group combine"},
             "gemv_down_k12288_n4096": {"us_per_call": round(dn_s * 1e6, 3),
                                        "GB/s": round(DOWN_BYTES / dn_s / 1e9, 1)},
             "wall_s_timed_region": round(wall, 4),
             "decode_step": decode,
+            "decode_step_w4a8": decode_w4a8,
             "fp8": fp8_lines,
             "prefill_gemm": prefill,
         },

@@ -72,7 +72,7 @@ int moss_w4g32_quantize_minmax(const void *w, void *qw, void *sc, void *zp, int 
 
 /* y bf16 [N] = x bf16 [K] . dequant(W)^T, M must be 1, K % 64 == 0, K <= 16384.
  * rows_per_wave in {0 (auto), 1, 2, 4}.  Replaces the W4A8 projection
- * linear() of src/moss_tts/_runtime/dp4a_scaled.py:81-95 (and int4_dp4a.py:335-353). */
+ * linear() of src/moss_tts/_runtime/dp4a_scaled.py:81-95 (and int4_dp4a, int4_dp4a.py:56-74). */
 int moss_w4g32_gemv(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
                     int rows_per_wave, int dequant_mode, void *stream);
 
@@ -99,6 +99,41 @@ int moss_w4g32_norm_gemv(const void *x, const void *res, const void *norm_w, voi
 int moss_w4g32_norm_gateup_silu(const void *x, const void *res, const void *norm_w, void *sum_out, float eps,
                                 const void *qw, const void *sc, const void *zp, void *y, int K, int N_half,
                                 int rows_per_wave, int dequant_mode, void *stream);
+
+/* ------------------------------------------------- W4A8 G32 decode mode */
+/* The reference's serving arithmetic: activations quantized to int8 per group of 32, integer
+ * dot products against the INT4 codes, fp32 group combine.  Quantized activations ("qact",
+ * G = K/32 groups):
+ *   qx    int8  [K]  in dot4 order: bytes 8b..8b+7 hold x[8b + {0,4,1,5,2,6,3,7}]
+ *   sx    fp32  [G]  scale = max(RN(max|x_g| / 127), 1e-8)
+ *   qsum  int32 [G]  sum of the group's codes (the zero-point term)
+ * with q = rint(x * RN(1 / scale)), ties to even, |q| <= 127.
+ * bf16 x [K] (K % 32 == 0) -> qact.  Replaces _int8_activation_grouped,
+ * src/moss_tts/_runtime/int4_dp4a.py:21-30 (launched by dp4a_scaled.py:88-89). */
+int moss_int8_quantize_g32(const void *x, void *qx, void *sx, void *qsum, int K, void *stream);
+
+/* (add+)RMSNorm exactly as moss_rmsnorm, then the output quantized to qact (n % 32 == 0);
+ * y may be NULL (no bf16 output).  For rows > 1, row r's qact starts at qx + r*n,
+ * sx + r*n/32, qsum + r*n/32.  Replaces _norm_quant, src/moss_tts/_runtime/dp4a_fusions.py:24-40
+ * (the normalization half of dp4a_norm_projection.py:66-78). */
+int moss_rmsnorm_quant_g32(const void *x, const void *res, const void *w, void *sum_out, void *y, void *qx,
+                           void *sx, void *qsum, int rows, int n, float eps, void *stream);
+
+/* y bf16 [N] = bf16(sum_g f32(isum[n,g]) * (s[n,g] * sx[g])), isum[n,g] = sum_{k in g}
+ * (q[n,k] - z[n,g]) * qx[k] exact in int32, on rowpack weights; K % 64 == 0, K <= 16384,
+ * rows_per_wave in {0 (auto), 1, 2, 4}.  Replaces linear (paired=False),
+ * src/moss_tts/_runtime/dp4a_scaled.py:22-57,80-95 (and int4_dp4a.py:33-74). */
+int moss_w4a8_gemv(const void *qx, const void *sx, const void *qsum, const void *qw, const void *sc, const void *zp,
+                   void *y, int K, int N, int rows_per_wave, void *stream);
+
+/* Paired gate||up (W has 2*N_half rows, gate first): gate and up rounded to bf16, y bf16
+ * [N_half] = bf16(bf16(silu(gate)) * up).  With out_qx/out_sx/out_qsum (all set or all NULL;
+ * N_half % 32 == 0, rows_per_wave 0, 2 or 4) y is also quantized to qact for the next
+ * projection.  Replaces linear
+ * (paired=True, fused), src/moss_tts/_runtime/dp4a_scaled.py:60-78 (dp4a_gateup_quant.py:11-33). */
+int moss_w4a8_gateup_silu(const void *qx, const void *sx, const void *qsum, const void *qw, const void *sc,
+                          const void *zp, void *y, void *out_qx, void *out_sx, void *out_qsum, int K, int N_half,
+                          int rows_per_wave, void *stream);
 
 /* ------------------------------------------------------------- prefill GEMM */
 /* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);

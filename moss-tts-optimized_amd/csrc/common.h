@@ -75,6 +75,41 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Max and sum over the 4 lanes of each DPP quad; every lane of the quad receives the result.
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    return fmaxf(v, dpp_move<0x4E>(v));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_move<0xB1>(v);
+    return v + dpp_move<0x4E>(v);
+}
+
+// ---------------------------------------------------------------- grouped int8 activations
+// Per group of 32 values: scale = max(RN(max|x| / 127), 1e-8), inv = RN(1 / scale),
+// q = rint(x * inv) (ties to even), |q| <= 127.  Division here is IEEE (correctly rounded).
+__device__ __forceinline__ float g32_scale(float absmax) { return fmaxf(absmax / 127.0f, 1e-8f); }
+
+// Quantize 8 consecutive values into two words in dot4 order: bytes 0..7 hold
+// q[0], q[4], q[1], q[5], q[2], q[6], q[3], q[7] -- the order in which (w & 0x0F0F0F0F)
+// and ((w >> 4) & 0x0F0F0F0F) expand a row-packed INT4 code word.  Returns the code sum.
+__device__ __forceinline__ int quantize8_dot4(const float* v, float inv, uint32_t& lo, uint32_t& hi) {
+    int q[8], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        q[i] = (int)rintf(v[i] * inv);
+        sum += q[i];
+    }
+    lo = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[4] & 0xff) << 8 | (uint32_t)(q[1] & 0xff) << 16 |
+         (uint32_t)(q[5] & 0xff) << 24;
+    hi = (uint32_t)(q[2] & 0xff) | (uint32_t)(q[6] & 0xff) << 8 | (uint32_t)(q[3] & 0xff) << 16 |
+         (uint32_t)(q[7] & 0xff) << 24;
+    return sum;
+}
+
+// Byte offset, within its 8-value block, of value t in dot4 order.
+__device__ __forceinline__ int dot4_slot(int t) { return ((t & 3) << 1) | (t >> 2); }
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                            __builtin_bit_cast(bf16x2_t, b), c, false);

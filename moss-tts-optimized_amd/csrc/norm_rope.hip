@@ -29,12 +29,19 @@ __device__ __forceinline__ float block_sum(float v, float* lds) {
 // (n % 8 == 0, n <= 8 * 256 * kMaxChunks).
 constexpr int kMaxChunks = 4;
 
-template <bool RESIDUAL>
+// QUANT: also quantize y per group of 32 to int8 (dot4 order, see common.h) with fp32 group
+// scales and code sums, as the reference's fused norm + quantizer does
+// (src/moss_tts/_runtime/dp4a_fusions.py:24-40); y may then be null.  A group's 4 chunks
+// belong to the 4 lanes of one DPP quad.
+template <bool RESIDUAL, bool QUANT = false>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ res,
                                                              const uint16_t* __restrict__ w,
                                                              uint16_t* __restrict__ sum_out,
-                                                             uint16_t* __restrict__ y, int n, float eps) {
+                                                             uint16_t* __restrict__ y, int n, float eps,
+                                                             uint2* __restrict__ qx = nullptr,
+                                                             float* __restrict__ sx = nullptr,
+                                                             int* __restrict__ qsum = nullptr) {
     __shared__ float lds[kNormThreads / kWave];
     const size_t row = blockIdx.x;
     const int chunks = n / 8;
@@ -42,6 +49,14 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
     const uint4* rr = reinterpret_cast<const uint4*>(res + row * n);
     float v[kMaxChunks][8];
     float ss = 0.f;
+    // the weight loads go out first so they overlap the reduction
+    const uint4* wr = reinterpret_cast<const uint4*>(w);
+    uint4 wv4[kMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        const int ci = threadIdx.x + c * kNormThreads;
+        wv4[c] = ci < chunks ? wr[ci] : make_uint4(0u, 0u, 0u, 0u);
+    }
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
         const int ci = threadIdx.x + c * kNormThreads;
@@ -73,12 +88,14 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
         }
     }
     const float inv = rsqrtf(block_sum(ss, lds) / (float)n + eps);
-    const uint4* wr = reinterpret_cast<const uint4*>(w);
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
         const int ci = threadIdx.x + c * kNormThreads;
-        if (ci < chunks) {
-            const uint4 ww = wr[ci];
+        if (c * kNormThreads >= chunks) break;  // block-uniform
+        float yv[8];
+        const bool active = ci < chunks;
+        if (active) {
+            const uint4 ww = wv4[c];
             const uint32_t wv[4] = {ww.x, ww.y, ww.z, ww.w};
             uint32_t o[4];
 #pragma unroll
@@ -86,8 +103,29 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
                 const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
                 const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
                 o[p] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+                yv[2 * p] = bf16_lo(o[p]);
+                yv[2 * p + 1] = bf16_hi(o[p]);
             }
-            reinterpret_cast<uint4*>(y + row * n)[ci] = make_uint4(o[0], o[1], o[2], o[3]);
+            if (!QUANT || y) reinterpret_cast<uint4*>(y + row * n)[ci] = make_uint4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) yv[i] = 0.f;
+        }
+        if constexpr (QUANT) {
+            float m = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(yv[i]));
+            const float scale = g32_scale(quad_max(m));
+            uint32_t lo, hi;
+            const int part = quantize8_dot4(yv, 1.0f / scale, lo, hi);
+            const float total = quad_sum((float)part);  // |sum| <= 32 * 127: exact in fp32
+            if (active) {
+                qx[row * chunks + ci] = make_uint2(lo, hi);
+                if ((ci & 3) == 0) {
+                    sx[row * (n / 32) + ci / 4] = scale;
+                    qsum[row * (n / 32) + ci / 4] = (int)total;
+                }
+            }
         }
     }
 }
@@ -171,6 +209,25 @@ MOSS_API int moss_rmsnorm(const void* x, const void* res, const void* w, void* s
     else
         hipLaunchKernelGGL(rmsnorm_rows<false>, dim3(rows), dim3(kNormThreads), 0, st, (const uint16_t*)x,
                            (const uint16_t*)nullptr, (const uint16_t*)w, (uint16_t*)nullptr, (uint16_t*)y, n, eps);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_rmsnorm_quant_g32(const void* x, const void* res, const void* w, void* sum_out, void* y, void* qx,
+                                    void* sx, void* qsum, int rows, int n, float eps, void* stream) {
+    MOSS_CHECK_ARG(x && w && qx && sx && qsum && rows > 0 && n > 0 && n % 32 == 0 &&
+                   n <= 8 * kNormThreads * kMaxChunks);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(w, 16) && MOSS_ALIGNED(y, 16) && MOSS_ALIGNED(qx, 8) &&
+                   MOSS_ALIGNED(sx, 4) && MOSS_ALIGNED(qsum, 4));
+    MOSS_CHECK_ARG(!res || (sum_out && MOSS_ALIGNED(res, 16) && MOSS_ALIGNED(sum_out, 16)));
+    hipStream_t st = (hipStream_t)stream;
+    if (res)
+        hipLaunchKernelGGL((rmsnorm_rows<true, true>), dim3(rows), dim3(kNormThreads), 0, st, (const uint16_t*)x,
+                           (const uint16_t*)res, (const uint16_t*)w, (uint16_t*)sum_out, (uint16_t*)y, n, eps,
+                           (uint2*)qx, (float*)sx, (int*)qsum);
+    else
+        hipLaunchKernelGGL((rmsnorm_rows<false, true>), dim3(rows), dim3(kNormThreads), 0, st, (const uint16_t*)x,
+                           (const uint16_t*)nullptr, (const uint16_t*)w, (uint16_t*)nullptr, (uint16_t*)y, n, eps,
+                           (uint2*)qx, (float*)sx, (int*)qsum);
     return moss_launch_status();
 }
 

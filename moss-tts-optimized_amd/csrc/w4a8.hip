@@ -1,0 +1,246 @@
+// W4A8 decode mode: the reference's G32 serving arithmetic (int8 activations, integer dot
+// products, fp32 group combine) on the row-packed INT4-G32 weights.
+//
+// Activation quantizer (src/moss_tts/_runtime/int4_dp4a.py:21-30, also fused into the
+// reference's producers): per 32-value group, sc = max(RN(max|x| / 127), 1e-8),
+// inv = RN(1 / sc), q = rint(x * inv) (ties to even), all in fp32 with correctly rounded
+// division.  Integer sums (src/moss_tts/_runtime/dp4a_scaled.py:22-57):
+// isum[n, g] = sum_k (q_w - z) * q_x, exact in int32; y[n] = sum_g f32(isum) * (s_w * s_x)
+// in fp32, rounded to bf16; the paired form rounds gate and up to bf16 and applies the
+// SiLU*mul epilogue (dp4a_scaled.py:64-68).
+//
+// Byte order of the quantized activations ("dot4 order"): within each block of 8 values,
+// bytes 8b..8b+7 hold x[8b + {0, 4, 1, 5, 2, 6, 3, 7}].  That is the order in which
+// (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) expand a row-packed code word into bytes, so
+// each 8 weights cost one shift, two ands and two v_dot4_i32_i8 (unsigned codes 0..15 are
+// non-negative int8).
+#include "common.h"
+
+namespace moss {
+namespace {
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// One thread per group of 32: reads 64 bytes of bf16, writes 32 int8 in dot4 order, the
+// group scale and the group's code sum (for the zero-point term).
+__global__ __launch_bounds__(256) void int8_quantize_g32(const uint16_t* __restrict__ x, uint2* __restrict__ qx,
+                                                         float* __restrict__ sx, int* __restrict__ qsum, int G) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= G) return;
+    const uint4* p = reinterpret_cast<const uint4*>(x + 32 * g);
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint4 t = p[c];
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[8 * c + 2 * e] = bf16_lo(w[e]);
+            v[8 * c + 2 * e + 1] = bf16_hi(w[e]);
+        }
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+    const float sc = g32_scale(m);
+    const float inv = 1.0f / sc;
+    int sum = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        uint32_t lo, hi;
+        sum += quantize8_dot4(v + 8 * b, inv, lo, hi);
+        qx[4 * g + b] = make_uint2(lo, hi);
+    }
+    sx[g] = sc;
+    qsum[g] = sum;
+}
+
+__device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
+    const float g = round_bf16(gate);
+    const float u = round_bf16(up);
+    const float a = round_bf16(g / (1.0f + expf(-g)));
+    return f32_to_bf16(a * u);
+}
+
+// Row-per-wave GEMV: lane l owns groups l + 64 j; KG = ceil(G / 64).  QOUT (paired only):
+// 32 / R waves x R rows per workgroup cover one 32-row output group, which the workgroup
+// also quantizes (the down projection's activations), as the reference's fused gate/up does
+// (src/moss_tts/_runtime/dp4a_scaled.py:70-78).
+template <int KG, int R, bool PAIRED, bool QOUT>
+__global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
+    const uint32_t* __restrict__ qx, const float* __restrict__ sx, const int* __restrict__ qsum,
+    const uint4* __restrict__ qw, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    uint16_t* __restrict__ y, uint8_t* __restrict__ oq, float* __restrict__ osx, int* __restrict__ osum, int G,
+    int n_out) {
+    static_assert(!QOUT || (PAIRED && (R == 2 || R == 4)), "output quantization covers 32 paired rows");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
+    const int row0 = wave * R;
+    if (!QOUT && row0 >= n_out) return;  // wave-uniform; QOUT grids hold whole groups only
+    constexpr int NR = PAIRED ? 2 * R : R;
+    // activations first (completions are counted in order): 32 int8 per group, its scale and sum
+    uint4 xa[KG], xb[KG];
+    float xs[KG];
+    int xq[KG];
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        const int g = lane + kWave * j;
+        if (g < G) {
+            const uint4* p = reinterpret_cast<const uint4*>(qx + 8 * g);
+            xa[j] = p[0];
+            xb[j] = p[1];
+            xs[j] = sx[g];
+            xq[j] = qsum[g];
+        } else {
+            xa[j] = xb[j] = make_uint4(0u, 0u, 0u, 0u);
+            xs[j] = 0.f;
+            xq[j] = 0;
+        }
+    }
+    uint4 w[NR][KG];
+    uint32_t s[NR][KG], z[NR][KG];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int local = PAIRED ? (r % R) : r;
+        const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const int g = lane + kWave * j;
+            if (g < G) {
+                const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(qw + (size_t)n * G + g));
+                w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
+                s[r][j] = sc[(size_t)n * G + g];
+                z[r][j] = zero_of_group(zp + (size_t)n * (G >> 1), g, G);
+            } else {
+                w[r][j] = make_uint4(0u, 0u, 0u, 0u);
+                s[r][j] = 0u;
+                z[r][j] = 0u;
+            }
+        }
+    }
+    uint32_t mask = 0x0F0F0F0Fu;
+    asm volatile("" : "+v"(mask));
+    float out[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const uint32_t words[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
+            const uint32_t xw[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
+            int isum = -(int)z[r][j] * xq[j];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                isum = dot4(words[c] & mask, xw[2 * c], isum);
+                isum = dot4((words[c] >> 4) & mask, xw[2 * c + 1], isum);
+            }
+            part = fmaf((float)isum, bf16_bits((uint16_t)s[r][j]) * xs[j], part);
+        }
+        out[r] = wave_sum(part);
+    }
+    uint16_t val[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) val[r] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < n_out) y[row0 + r] = val[r];
+    }
+    if constexpr (QOUT) {
+        // rows 32 b .. 32 b + 31 of this workgroup form output group b
+        __shared__ float grp[32];
+        const int wl = threadIdx.x / kWave;
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) grp[R * wl + r] = bf16_bits(val[r]);
+        }
+        __syncthreads();
+        if (wl == 0) {
+            const int b = blockIdx.x;
+            const float v = lane < 32 ? grp[lane] : 0.f;
+            const float scale = g32_scale(wave_max(fabsf(v)));
+            const float q = rintf(v * (1.0f / scale));
+            const float total = wave_sum(q);  // |sum| <= 32 * 127: exact in fp32
+            if (lane < 32) oq[32 * b + 8 * (lane >> 3) + dot4_slot(lane & 7)] = (uint8_t)(int)q;
+            if (lane == 0) {
+                osx[b] = scale;
+                osum[b] = (int)total;
+            }
+        }
+    }
+}
+
+template <bool PAIRED, bool QOUT>
+int launch_w4a8(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc, const void* zp,
+                void* y, void* oq, void* osx, void* osum, int K, int n_out, int rows, hipStream_t st) {
+    const int G = K / 32, KG = (G + kWave - 1) / kWave;
+    if (rows == 0) rows = QOUT ? 2 : 1;
+    if (QOUT && rows == 1) return (int)hipErrorInvalidValue;
+    const int waves = (n_out + rows - 1) / rows;
+    const int wpb = QOUT ? 32 / rows : 4;
+    const dim3 grid((waves + wpb - 1) / wpb), block(kWave * wpb);
+#define MOSS_W4A8(KGV, RV)                                                                                        \
+    if (KG == KGV && rows == RV) {                                                                                \
+        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, QOUT && RV != 1>), grid, block, 0, st,              \
+                           (const uint32_t*)qx, (const float*)sx, (const int*)qsum, (const uint4*)qw,             \
+                           (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (uint8_t*)oq, (float*)osx,      \
+                           (int*)osum, G, n_out);                                                                 \
+        return moss_launch_status();                                                                              \
+    }
+#define MOSS_W4A8_R(KGV) MOSS_W4A8(KGV, 1) MOSS_W4A8(KGV, 2) MOSS_W4A8(KGV, 4)
+    MOSS_W4A8_R(1) MOSS_W4A8_R(2) MOSS_W4A8_R(3) MOSS_W4A8_R(4) MOSS_W4A8_R(5) MOSS_W4A8_R(6) MOSS_W4A8_R(7)
+    MOSS_W4A8_R(8)
+#undef MOSS_W4A8_R
+#undef MOSS_W4A8
+    return (int)hipErrorInvalidValue;
+}
+
+}  // namespace
+}  // namespace moss
+
+using namespace moss;
+
+MOSS_API int moss_int8_quantize_g32(const void* x, void* qx, void* sx, void* qsum, int K, void* stream) {
+    MOSS_CHECK_ARG(x && qx && sx && qsum && K > 0 && K % 32 == 0);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qx, 16) && MOSS_ALIGNED(sx, 4) && MOSS_ALIGNED(qsum, 4));
+    const int G = K / 32;
+    hipLaunchKernelGGL(int8_quantize_g32, dim3((G + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, (uint2*)qx, (float*)sx, (int*)qsum, G);
+    return moss_launch_status();
+}
+
+static int check_w4a8(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc, const void* zp,
+                      const void* y, int K, int rows) {
+    MOSS_CHECK_ARG(qx && sx && qsum && qw && sc && zp && y && K > 0 && K % 64 == 0 && K <= 16384);
+    MOSS_CHECK_ARG(rows == 0 || rows == 1 || rows == 2 || rows == 4);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(qx, 16) && MOSS_ALIGNED(qw, 16));
+    return 0;
+}
+
+MOSS_API int moss_w4a8_gemv(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc,
+                            const void* zp, void* y, int K, int N, int rows_per_wave, void* stream) {
+    if (int rc = check_w4a8(qx, sx, qsum, qw, sc, zp, y, K, rows_per_wave)) return rc;
+    MOSS_CHECK_ARG(N > 0);
+    return launch_w4a8<false, false>(qx, sx, qsum, qw, sc, zp, y, nullptr, nullptr, nullptr, K, N, rows_per_wave,
+                                     (hipStream_t)stream);
+}
+
+MOSS_API int moss_w4a8_gateup_silu(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc,
+                                   const void* zp, void* y, void* out_qx, void* out_sx, void* out_qsum, int K,
+                                   int N_half, int rows_per_wave, void* stream) {
+    if (int rc = check_w4a8(qx, sx, qsum, qw, sc, zp, y, K, rows_per_wave)) return rc;
+    MOSS_CHECK_ARG(N_half > 0);
+    const bool quant = out_qx != nullptr;
+    MOSS_CHECK_ARG(quant == (out_sx != nullptr) && quant == (out_qsum != nullptr));
+    if (!quant)
+        return launch_w4a8<true, false>(qx, sx, qsum, qw, sc, zp, y, nullptr, nullptr, nullptr, K, N_half,
+                                        rows_per_wave, (hipStream_t)stream);
+    MOSS_CHECK_ARG(N_half % 32 == 0 && rows_per_wave != 1);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(out_sx, 4) && MOSS_ALIGNED(out_qsum, 4));
+    return launch_w4a8<true, true>(qx, sx, qsum, qw, sc, zp, y, out_qx, out_sx, out_qsum, K, N_half,
+                                   rows_per_wave, (hipStream_t)stream);
+}

@@ -6,7 +6,12 @@ attention (one kernel) -> split merge -> O GEMV -> add-RMSNorm + gate||up GEMV w
 (one kernel) -> down GEMV.  The step starts with the
 33-row embedding sum (``src/moss_tts/_runtime/kernels.py:7-26``) and ends with the final norm
 and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``),
-here INT4-G32 as well.  Static input buffers (ids, position) make the step graph-capturable;
+here INT4-G32 as well.  With ``w4a8`` the four layer projections run the reference's serving
+arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
+``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer -> q||k||v ->
+attention -> int8 quantizer -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul and the
+output quantizer -> down (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
+Static input buffers (ids, position) make the step graph-capturable;
 ``step()`` copies new inputs into them and replays the graph, as ``FastLLM.step`` does
 (``src/moss_tts/_runtime/llm.py:327-338``).
 """
@@ -16,7 +21,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import attention, w4g32
+from . import attention, w4a8, w4g32
 from .modules import QuantGateUpG32, QuantLinearG32
 from .w4g32 import _require
 
@@ -57,7 +62,7 @@ class DecodeStepG32:
 
     def __init__(self, layers: list[DecoderLayerG32], final_norm: torch.Tensor, heads: QuantLinearG32,
                  text_embedding: torch.Tensor, audio_embedding: torch.Tensor, *, max_length: int,
-                 eps: float = 1e-6, theta: float = 1e6):
+                 eps: float = 1e-6, theta: float = 1e6, w4a8: bool = False):
         _require(len(layers) > 0, "at least one layer")
         dev = final_norm.device
         _require(dev.type == "cuda", "the decode step runs on a HIP device")
@@ -70,6 +75,7 @@ class DecodeStepG32:
         self.audio_embedding = audio_embedding
         self.max_length = max_length
         self.eps = eps
+        self.w4a8 = bool(w4a8)
         self.device = dev
         self.keys = [torch.zeros((1, KH, max_length, HD), device=dev, dtype=torch.bfloat16) for _ in layers]
         self.values = [torch.zeros((1, KH, max_length, HD), device=dev, dtype=torch.bfloat16) for _ in layers]
@@ -84,6 +90,8 @@ class DecodeStepG32:
     def forward(self) -> torch.Tensor:
         """One step from the static ``ids``/``position`` buffers -> logits bf16 ``[N_heads]``.
         Every (add+)RMSNorm runs inside the projection that consumes it (``norm_gemv``)."""
+        if self.w4a8:
+            return self._forward_w4a8()
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
@@ -100,6 +108,27 @@ class DecodeStepG32:
             residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
                                                    residual=residual, dequant=layer.gate_up.dequant)
             mlp = layer.down(act)
+        _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
+                                    dequant=self.heads.dequant)
+        return logits.view(-1)
+
+    def _forward_w4a8(self) -> torch.Tensor:
+        eps = self.eps
+        x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
+        residual = x
+        mlp = None
+        for i, layer in enumerate(self.layers):
+            if i == 0:
+                _, _, act = w4a8.norm_quant(x, None, layer.input_norm, eps, normalized=False)
+            else:
+                residual, _, act = w4a8.norm_quant(mlp, residual, layer.input_norm, eps, normalized=False)
+            qkv = w4a8.linear(None, layer.qkv.packed, prequantized=act)
+            attn = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
+                                                  self.values[i], self.position, eps, ws=self.ws)
+            o = w4a8.linear(attn.view(-1), layer.o.packed)
+            residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
+            _, hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, fused=True, prequantized=act)
+            mlp = w4a8.linear(None, layer.down.packed, prequantized=hidden).view(1, HIDDEN)
         _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
                                     dequant=self.heads.dequant)
         return logits.view(-1)
@@ -144,7 +173,7 @@ class DecodeStepG32:
     # ------------------------------------------------------------ installed model
     @classmethod
     @torch.no_grad()
-    def from_model(cls, model, *, max_length: int, dequant: int = w4g32.EXACT) -> "DecodeStepG32":
+    def from_model(cls, model, *, max_length: int, dequant: int = w4g32.EXACT, w4a8: bool = False) -> "DecodeStepG32":
         """The decode step of a MOSS-TTS model after ``install_gptq``: its quantized projections,
         norm weights and embeddings as they are (no copies); the 32 audio heads (rows
         ``[:1024]`` of ``lm_heads[1:]``, ``src/moss_tts/_runtime/llm.py:188-191``) concatenated
@@ -169,13 +198,13 @@ class DecodeStepG32:
         heads = QuantLinearG32(w4g32.quantize_minmax(heads_bf16.float().contiguous()), dequant=dequant)
         audio = torch.stack([e.weight for e in model.emb_ext]).contiguous()
         return cls(layers, lm.norm.weight, heads, lm.embed_tokens.weight.contiguous(), audio,
-                   max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6)
+                   max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6, w4a8=w4a8)
 
     # -------------------------------------------------------------- synthetic model
     @classmethod
     @torch.inference_mode()
     def random(cls, n_layers: int, *, max_length: int, device, seed: int = 0, text_vocab: int = 151936,
-               kv_fill: bool = True, dequant: int = w4g32.EXACT) -> "DecodeStepG32":
+               kv_fill: bool = True, dequant: int = w4g32.EXACT, w4a8: bool = False) -> "DecodeStepG32":
         """Random-init Qwen3-8B-shaped weights (N(0, 0.02), min-max INT4-G32 quantized on the
         device), norm weights 1 + N(0, 0.01), embeddings N(0, 1), KV caches N(0, 1)."""
         dev = torch.device(device)
@@ -196,7 +225,7 @@ class DecodeStepG32:
         heads = q(CODEBOOKS * AUDIO_VOCAB, HIDDEN)
         text = torch.randn((text_vocab, HIDDEN), generator=gen, device=dev).bfloat16()
         audio = torch.randn((CODEBOOKS, AUDIO_VOCAB, HIDDEN), generator=gen, device=dev).bfloat16()
-        eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length)
+        eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length, w4a8=w4a8)
         if kv_fill:
             for t in eng.keys + eng.values:
                 t.copy_(torch.randn(t.shape, generator=gen, device=dev))

@@ -48,6 +48,10 @@ SIGNATURES: dict[str, list] = {
     "moss_fp8_linear": [_P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_fp8_gateup_silu": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_fp8_to_bf16": [_P, _P, ctypes.c_longlong, _P],
+    "moss_int8_quantize_g32": [_P, _P, _P, _P, _I, _P],
+    "moss_rmsnorm_quant_g32": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "moss_w4a8_gemv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "moss_w4a8_gateup_silu": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
 }
 _RESTYPES = {"moss_error_string": ctypes.c_char_p, "moss_gemm_workspace_bytes": ctypes.c_longlong}
 

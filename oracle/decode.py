@@ -11,6 +11,7 @@ import torch
 
 from . import attention as oa
 from . import pointwise as op
+from . import w4a8 as o8
 from . import w4g32 as ow
 
 
@@ -36,5 +37,31 @@ def decode_step(layers, final_norm, heads_w, text, audio, ids, position, keys, v
         n = y.shape[1] // 2
         a = ow.silu_mul_rounded(y[:, :n], y[:, n:])
         mlp = ow.linear(a, L["down"]).bfloat16()
+    _, h = op.add_rmsnorm(mlp, residual, final_norm, eps)
+    return ow.linear(h, heads_w).bfloat16().view(-1)
+
+
+def decode_step_w4a8(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):
+    """The same step with the four layer projections in the W4A8 arithmetic
+    (``oracle.w4a8``; order ``src/moss_tts/_runtime/llm.py:29-56,71-92``): ``layers`` dicts hold
+    ``(q, z, s)`` code triples for ``qkv``, ``o``, ``gate_up``, ``down``; the heads stay
+    dequant-then-matmul on ``heads_w``."""
+    p = int(position)
+    x = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
+    residual = x
+    h = op.rmsnorm(x, layers[0]["input_norm"], eps)
+    mlp = None
+    for i, L in enumerate(layers):
+        if i > 0:
+            residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
+        qkv = o8.w4a8_linear(h.view(-1), *L["qkv"])[0].view(1, -1)
+        q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],
+                               torch.tensor([p]), eps)
+        attn = oa.decode_attention(q, keys[i], values[i], p).bfloat16().view(-1)
+        o = o8.w4a8_linear(attn, *L["o"])[0].view(1, -1)
+        residual, h = op.add_rmsnorm(o, residual, L["post_norm"], eps)
+        n = L["gate_up"][0].shape[0] // 2
+        a = o8.w4a8_gateup_silu(h.view(-1), *L["gate_up"], n)[0]
+        mlp = o8.w4a8_linear(a, *L["down"])[0].view(1, -1)
     _, h = op.add_rmsnorm(mlp, residual, final_norm, eps)
     return ow.linear(h, heads_w).bfloat16().view(-1)

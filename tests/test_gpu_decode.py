@@ -65,3 +65,37 @@ def test_decode_graph_replay_matches_eager(dev):
         replay.append(eng.step(ids, p).clone())
         torch.cuda.synchronize()
     assert torch.equal(eager[0], replay[0]) and torch.equal(eager[1], replay[1])
+
+
+def _codes_cpu(m):
+    q, z = o.rowunpack(m.qw.cpu(), m.zeros.cpu())
+    return q, z, m.scales.cpu()
+
+
+def test_decode_step_w4a8_two_layers(dev):
+    """The W4A8 mode of the step vs the oracle composition in the same arithmetic
+    (int8 activations at every projection input); same end-to-end bar as the bf16 mode."""
+    from moss_tts._runtime.decode import DecodeStepG32
+
+    print("decode step w4a8: 2 layers, L=128", flush=True)
+    L, position = 128, 77
+    eng = DecodeStepG32.random(2, max_length=L, device=dev, seed=9, text_vocab=512, w4a8=True)
+    keys = [k.cpu().clone() for k in eng.keys]
+    values = [v.cpu().clone() for v in eng.values]
+    ids = torch.tensor([[23] + list(range(40, 72))], dtype=torch.int64)
+    logits = eng.step(ids, position).float().cpu()
+    layers = [dict(qkv=_codes_cpu(l.qkv.packed), o=_codes_cpu(l.o.packed), gate_up=_codes_cpu(l.gate_up.packed),
+                   down=_codes_cpu(l.down.packed), input_norm=l.input_norm.cpu(), post_norm=l.post_norm.cpu(),
+                   q_norm=l.q_norm.cpu(), k_norm=l.k_norm.cpu()) for l in eng.layers]
+    ref = od.decode_step_w4a8(layers, eng.final_norm.cpu(), _dequant_cpu(eng.heads), eng.text_embedding.cpu(),
+                              eng.audio_embedding.cpu(), ids, position, keys, values, eng.cos.cpu(),
+                              eng.sin.cpu()).float()
+    rel = float((logits - ref).norm() / ref.norm())
+    print(f"w4a8 relative L2 error of logits: {rel:.3e}", flush=True)
+    assert rel < 2e-2
+    # graph replay reproduces eager execution bit for bit
+    eager = eng.step(ids, position).clone()
+    eng.capture()
+    replay = eng.step(ids, position).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, replay)
