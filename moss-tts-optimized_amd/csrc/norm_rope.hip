@@ -69,9 +69,8 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
                 const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
-                    const uint32_t lo = f32_to_bf16(bf16_lo(aw[p]) + bf16_lo(bw[p]));
-                    const uint32_t hi = f32_to_bf16(bf16_hi(aw[p]) + bf16_hi(bw[p]));
-                    sw[p] = lo | (hi << 16);
+                    sw[p] = pack_bf16x2(bf16_lo(aw[p]) + bf16_lo(bw[p]),
+                                bf16_hi(aw[p]) + bf16_hi(bw[p]));
                 }
                 reinterpret_cast<uint4*>(sum_out + row * n)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
             } else {
@@ -102,7 +101,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
             for (int p = 0; p < 4; ++p) {
                 const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
                 const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
-                o[p] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+                o[p] = pack_bf16x2(a, b);
                 yv[2 * p] = bf16_lo(o[p]);
                 yv[2 * p + 1] = bf16_hi(o[p]);
             }
@@ -189,7 +188,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows(const uint32_t* __restrict_
         const float uv = p ? bf16_hi(u) : bf16_lo(u);
         r[p] = round_bf16(gv / (1.0f + expf(-gv))) * uv;
     }
-    y[row * half + c] = (uint32_t)f32_to_bf16(r[0]) | ((uint32_t)f32_to_bf16(r[1]) << 16);
+    y[row * half + c] = pack_bf16x2(r[0], r[1]);
 }
 
 }  // namespace

@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256) void dequant_bf16(const uint32_t* __restrict__
     for (int p = 0; p < 4; ++p) {
         const float a = (float)((int)rowpack_code(word, 2 * p) - z) * s;
         const float b = (float)((int)rowpack_code(word, 2 * p + 1) - z) * s;
-        o[p] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+        o[p] = pack_bf16x2(a, b);
     }
     reinterpret_cast<uint4*>(out)[i] = make_uint4(o[0], o[1], o[2], o[3]);
 }

@@ -243,8 +243,8 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ par
     float4 s = make_float4(1.f, 1.f, 1.f, 1.f);
     if (row_scale) s = make_float4(row_scale[n], row_scale[n + 1], row_scale[n + 2], row_scale[n + 3]);
     uint2 o;
-    o.x = (uint32_t)f32_to_bf16(acc.x * s.x) | ((uint32_t)f32_to_bf16(acc.y * s.y) << 16);
-    o.y = (uint32_t)f32_to_bf16(acc.z * s.z) | ((uint32_t)f32_to_bf16(acc.w * s.w) << 16);
+    o.x = pack_bf16x2(acc.x * s.x, acc.y * s.y);
+    o.y = pack_bf16x2(acc.z * s.z, acc.w * s.w);
     *reinterpret_cast<uint2*>(Y + i) = o;
 }
 

@@ -256,9 +256,8 @@ __device__ __forceinline__ void norm_into_lds(const NormLoad<CH>& nl, const Norm
             const uint32_t bw[4] = {nl.r[c].x, nl.r[c].y, nl.r[c].z, nl.r[c].w};
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                const uint32_t lo = f32_to_bf16(bf16_lo(sw[p]) + bf16_lo(bw[p]));
-                const uint32_t hi = f32_to_bf16(bf16_hi(sw[p]) + bf16_hi(bw[p]));
-                sw[p] = lo | (hi << 16);
+                sw[p] = pack_bf16x2(bf16_lo(sw[p]) + bf16_lo(bw[p]),
+                            bf16_hi(sw[p]) + bf16_hi(bw[p]));
             }
             if (blockIdx.x == 0)
                 reinterpret_cast<uint4*>(na.sum_out)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
@@ -284,7 +283,7 @@ __device__ __forceinline__ void norm_into_lds(const NormLoad<CH>& nl, const Norm
         for (int p = 0; p < 4; ++p) {
             const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
             const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
-            o[p] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+            o[p] = pack_bf16x2(a, b);
         }
         reinterpret_cast<uint4*>(xn)[ci] = make_uint4(o[0], o[1], o[2], o[3]);
     }
