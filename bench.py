@@ -95,7 +95,7 @@ def _traffic():
     try:
         with open(path) as f:
             data = json.load(f)
-        return data.get("gateup_silu_k4096_n24576", {}).get("hbm_bytes_per_launch")
+        return data.get("norm_gateup_silu_k4096_n24576", {}).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
 

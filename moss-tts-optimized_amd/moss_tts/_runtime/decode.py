@@ -9,8 +9,8 @@ and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188
 here INT4-G32 as well.  With ``w4a8`` the four layer projections run the reference's serving
 arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
 ``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer -> q||k||v ->
-attention -> int8 quantizer -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul and the
-output quantizer -> down (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
+attention -> int8 quantizer -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul ->
+int8 quantizer -> down (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
 Static input buffers (ids, position) make the step graph-capturable;
 ``step()`` copies new inputs into them and replays the graph, as ``FastLLM.step`` does
 (``src/moss_tts/_runtime/llm.py:327-338``).
@@ -127,8 +127,10 @@ class DecodeStepG32:
                                                   self.values[i], self.position, eps, ws=self.ws)
             o = w4a8.linear(attn.view(-1), layer.o.packed)
             residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
-            _, hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, fused=True, prequantized=act)
-            mlp = w4a8.linear(None, layer.down.packed, prequantized=hidden).view(1, HIDDEN)
+            # the unfused gate/up (one row per wave) plus the standalone quantizer is faster here
+            # than the fused output quantizer, whose 32-row workgroups hold fewer rows in flight
+            hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
+            mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
         _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
                                     dequant=self.heads.dequant)
         return logits.view(-1)
