@@ -35,11 +35,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // Round a float through bf16 and back (the "x.to(bf16).to(f32)" step).
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits(f32_to_bf16(f)); }
 
-// Zero point of group g in a row-packed zp row (blocks of 128 groups: for block c with
-// r = min(128, G - 128c) groups, byte 64c + b holds z[128c + b] low and z[128c + r/2 + b] high).
-__device__ __forceinline__ uint32_t zero_of_group(const uint8_t* __restrict__ zrow, int g, int G) {
+// Where group g's zero point sits in a row-packed zp row (blocks of 128 groups: for block c with
+// r = min(128, G - 128c) groups, byte 64c + b holds z[128c + b] low and z[128c + r/2 + b] high):
+// byte index and bit shift.  Branch-free, so a byte load through it is not followed by a wait at
+// the load site; callers that prefetch keep the raw byte and shift until the value is used.
+__device__ __forceinline__ void zero_loc(int g, int G, int& byte, uint32_t& shift) {
     const int c0 = g & ~127, r = min(128, G - c0), off = g - c0, hr = r >> 1;
-    return off < hr ? (uint32_t)(zrow[(c0 >> 1) + off] & 15u) : (uint32_t)(zrow[(c0 >> 1) + off - hr] >> 4);
+    const int hi = off >= hr;
+    byte = (c0 >> 1) + off - hi * hr;
+    shift = (uint32_t)hi << 2;
+}
+
+__device__ __forceinline__ uint32_t zero_of_group(const uint8_t* __restrict__ zrow, int g, int G) {
+    int b;
+    uint32_t sh;
+    zero_loc(g, G, b, sh);
+    return ((uint32_t)zrow[b] >> sh) & 15u;
 }
 
 // ---------------------------------------------------------------- cross-lane sums

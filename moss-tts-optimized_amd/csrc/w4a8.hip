@@ -102,7 +102,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
         }
     }
     uint4 w[NR][KG];
-    uint32_t s[NR][KG], z[NR][KG];
+    uint32_t s[NR][KG], z[NR][KG], zsh[NR][KG];  // z: the raw byte holding the zero point at bit zsh
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         const int local = PAIRED ? (r % R) : r;
@@ -114,11 +114,14 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
                 const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(qw + (size_t)n * G + g));
                 w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
                 s[r][j] = sc[(size_t)n * G + g];
-                z[r][j] = zero_of_group(zp + (size_t)n * (G >> 1), g, G);
+                int zb;
+                zero_loc(g, G, zb, zsh[r][j]);
+                z[r][j] = zp[(size_t)n * (G >> 1) + zb];
             } else {
                 w[r][j] = make_uint4(0u, 0u, 0u, 0u);
                 s[r][j] = 0u;
                 z[r][j] = 0u;
+                zsh[r][j] = 0u;
             }
         }
     }
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
         for (int j = 0; j < KG; ++j) {
             const uint32_t words[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
             const uint32_t xw[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
-            int isum = -(int)z[r][j] * xq[j];
+            int isum = -(int)((z[r][j] >> zsh[r][j]) & 15u) * xq[j];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 isum = dot4(words[c] & mask, xw[2 * c], isum);

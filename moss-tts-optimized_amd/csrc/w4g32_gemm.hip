@@ -13,9 +13,9 @@
 //
 // Tile: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
 // (BM/2) x (BN/2), K in steps of 64 (two quantization groups).  Pipeline: two LDS buffers and
-// two register stages; step st + 2 is loaded from global memory while step st is multiplied and
-// step st + 1 is converted into the other LDS buffer, so each load has two steps of MFMA work
-// to arrive, with one barrier per step.
+// kStages register stages; while step st is multiplied from one LDS buffer and step st + 1 is
+// converted into the other, the global loads of step st + kStages are issued, so every load
+// has kStages - 1 steps of MFMA work to arrive (one barrier per step).
 // Split-K (SPLIT): workgroup z of a tile covers K range [z K/S, (z+1) K/S) and stores fp32
 // partial sums; gemm_reduce adds them in z order (deterministic) and applies the epilogue.
 // It is used when the tiles alone cannot fill the 256 CUs (small M).
@@ -34,61 +34,57 @@ constexpr int kBK = 64;
 constexpr int kPad = 8;  // bf16 padding per LDS row: breaks the 128-byte bank period
 constexpr int kLds = kBK + kPad;
 constexpr int kXcds = 8;
+constexpr int kStages = 4;  // register stages of the global-load pipeline
 
 enum WeightFormat { kInt4G32 = 0, kFp8E4M3 = 1 };
 
-// Per-thread share of one K step: BM rows x 64 activations (BM / 32 uint4 per thread) and one
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Per-thread share of one K step: BM rows x 64 activations (BM / 32 x 16 B per thread) and one
 // (row, 32-wide half) of the weight tile.
 template <int BM>
 struct StepRegs {
-    uint4 x[BM / 32];
-    uint4 w[2];     // INT4: w[0] = 32 codes; FP8: 32 e4m3 bytes
-    uint32_t s, z;  // INT4: the group's scale bits and zero point
+    u32x4_t x[BM / 32];
+    u32x4_t w[2];        // INT4: w[0] = 32 codes; FP8: 32 e4m3 bytes
+    uint32_t s, z, zsh;  // INT4: the group's scale bits, and the byte holding its zero point at bit zsh
 };
 
+// Out-of-range rows and columns load the last valid row / column instead (addresses are clamped):
+// rows of X and columns of W are independent in the product, and those outputs are never stored.
+// With BN = 64 the threads beyond the 64 weight rows load row (row mod 64) again and discard it.
 template <int BM, int BN, int FMT>
 __device__ __forceinline__ void load_step(StepRegs<BM>& r, const uint16_t* __restrict__ X,
                                           const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
                                           const uint8_t* __restrict__ zp, int M, int N, int K, int G, int m0,
                                           int n0, int k0, int tid) {
-    // activations: 256 / BM threads per row, each BM / 32 uint4; rows beyond M read as zero
+    // activations: 256 / BM threads per row, each BM / 32 x 16 B
     constexpr int TPR = 256 / BM, CH = 8 / TPR;
     {
-        const int row = tid / TPR, part = tid % TPR, m = m0 + row;
-        if (m < M) {
-            const uint4* p = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0) + CH * part;
+        const int row = tid / TPR, part = tid % TPR, m = min(m0 + row, M - 1);
+        const uint4* p = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0) + CH * part;
 #pragma unroll
-            for (int c = 0; c < CH; ++c) r.x[c] = p[c];
-        } else {
-#pragma unroll
-            for (int c = 0; c < CH; ++c) r.x[c] = make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int c = 0; c < CH; ++c) r.x[c] = __builtin_bit_cast(u32x4_t, p[c]);
     }
-    // weights: thread -> (row, 32-wide half of the step)
-    const int row = tid >> 1, half = tid & 1, n = n0 + row;
-    const bool ok = row < BN && n < N;
+    const int row = (tid >> 1) & (BN - 1), half = tid & 1, n = min(n0 + row, N - 1);
     if constexpr (FMT == kInt4G32) {
         const int g = (k0 >> 5) + half;
-        if (ok) {
-            r.w[0] = qw[(size_t)n * G + g];
-            r.s = sc[(size_t)n * G + g];
-            r.z = zero_of_group(zp + (size_t)n * (G >> 1), g, G);
-        } else {
-            r.w[0] = make_uint4(0u, 0u, 0u, 0u);
-            r.s = 0u;
-            r.z = 0u;
-        }
+        int zb;
+        zero_loc(g, G, zb, r.zsh);
+        r.w[0] = __builtin_bit_cast(u32x4_t, qw[(size_t)n * G + g]);
+        r.s = sc[(size_t)n * G + g];
+        r.z = zp[(size_t)n * (G >> 1) + zb];  // raw byte: the nibble is taken where it is used
     } else {
-        if (ok) {
-            const uint4* p =
-                reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(qw) + (size_t)n * K + k0 + 32 * half);
-            r.w[0] = p[0];
-            r.w[1] = p[1];
-        } else {
-            r.w[0] = r.w[1] = make_uint4(0u, 0u, 0u, 0u);
-        }
+        const uint4* p =
+            reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(qw) + (size_t)n * K + k0 + 32 * half);
+        r.w[0] = __builtin_bit_cast(u32x4_t, p[0]);
+        r.w[1] = __builtin_bit_cast(u32x4_t, p[1]);
     }
 }
+
+// Keeps the scheduler from moving instructions across this point: the loads of a pipeline stage
+// stay where they are issued instead of being sunk next to their first use (which would shrink
+// the prefetch distance to nothing); the compiler still places the waits before each use.
+__device__ __forceinline__ void pin() { __builtin_amdgcn_sched_barrier(0); }
 
 // Two e4m3 codes (bytes 2p, 2p+1 of a word pair) -> bf16 pair; exact: every e4m3 value is a bf16 value.
 template <bool HI>
@@ -102,12 +98,13 @@ __device__ __forceinline__ void store_step(const StepRegs<BM>& r, uint16_t (*As)
     constexpr int TPR = 256 / BM, CH = 8 / TPR;
     {
         const int row = tid / TPR, part = tid % TPR;
-        uint4* a = reinterpret_cast<uint4*>(&As[row][0]) + CH * part;
+        u32x4_t* a = reinterpret_cast<u32x4_t*>(&As[row][0]) + CH * part;
 #pragma unroll
         for (int c = 0; c < CH; ++c) a[c] = r.x[c];
     }
-    const int row = tid >> 1, half = tid & 1;
-    if (row >= BN) return;
+    // with BN = 64 the upper 128 threads hold a second copy of rows 0..63 (see load_step) and
+    // write the same values again: no branch, so no load is moved into one
+    const int row = (tid >> 1) & (BN - 1), half = tid & 1;
     uint32_t out[16];
     if constexpr (FMT == kFp8E4M3) {
         const uint32_t words[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
@@ -120,7 +117,7 @@ __device__ __forceinline__ void store_step(const StepRegs<BM>& r, uint16_t (*As)
         uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
         asm volatile("" : "+v"(mask), "+v"(bias_bits));
         const uint32_t s_lo = r.s & 0xffffu, s_hi = s_lo << 16;
-        const float bias = -(128.0f + (float)r.z) * bf16_bits((uint16_t)s_lo);
+        const float bias = -(128.0f + (float)((r.z >> r.zsh) & 15u)) * bf16_bits((uint16_t)s_lo);
         const uint32_t words[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -156,8 +153,9 @@ __device__ __forceinline__ void mfma_step(const uint16_t (*As)[kLds], const uint
 }
 
 // FMT == kFp8E4M3: qw is e4m3 [N, K] (row-major bytes), `row_scale` fp32 [N] or null.
-// SPLIT: `part` is fp32 [S, M, N]; gridDim.y = S.
-template <int BM, int BN, int FMT, bool SPLIT>
+// SPLIT: `part` is fp32 [S, M, N]; gridDim.y = S.  TAIL: the K steps of one workgroup need not
+// be a multiple of kStages.
+template <int BM, int BN, int FMT, bool SPLIT, bool TAIL>
 __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
                                                          const uint16_t* __restrict__ sc,
                                                          const uint8_t* __restrict__ zp, uint16_t* __restrict__ Y,
@@ -186,25 +184,42 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    StepRegs<BM> r0, r1;
-    load_step<BM, BN, FMT>(r0, X, qw, sc, zp, M, N, K, G, m0, n0, kbase, tid);
-    if (steps > 1) load_step<BM, BN, FMT>(r1, X, qw, sc, zp, M, N, K, G, m0, n0, kbase + kBK, tid);
-    store_step<BM, BN, FMT>(r0, As[0], Bs[0], tid);
+    // register stage i % kStages holds step i; kStages is even, so step i's LDS buffer is i % 2.
+    // Every sub-step issues one stage of loads (steps past the end load the last step again),
+    // so the stage consumed next has (kStages - 1) stages of loads issued after it.
+    static_assert(kStages % 2 == 0, "stages");
+    StepRegs<BM> r[kStages];
+#pragma unroll
+    for (int i = 0; i < kStages; ++i)
+        load_step<BM, BN, FMT>(r[i], X, qw, sc, zp, M, N, K, G, m0, n0, kbase + min(i, steps - 1) * kBK, tid);
+    pin();
+    store_step<BM, BN, FMT>(r[0], As[0], Bs[0], tid);
     __syncthreads();
-    // two steps per trip so the register stages and LDS buffers are named statically; an odd
-    // last step (in buffer 0) is peeled off after the loop
+    // whole trips of kStages steps (at the very last step the store writes a copy of that step
+    // into the idle buffer, which is never read), then, with TAIL, the remaining steps with guards
     int st = 0;
-    for (; st + 1 < steps; st += 2) {
-        if (st + 2 < steps) load_step<BM, BN, FMT>(r0, X, qw, sc, zp, M, N, K, G, m0, n0, kbase + (st + 2) * kBK, tid);
-        mfma_step<BM, BN>(As[0], Bs[0], acc, lane, wm, wn);
-        store_step<BM, BN, FMT>(r1, As[1], Bs[1], tid);
-        __syncthreads();
-        if (st + 3 < steps) load_step<BM, BN, FMT>(r1, X, qw, sc, zp, M, N, K, G, m0, n0, kbase + (st + 3) * kBK, tid);
-        mfma_step<BM, BN>(As[1], Bs[1], acc, lane, wm, wn);
-        if (st + 2 < steps) store_step<BM, BN, FMT>(r0, As[0], Bs[0], tid);
-        __syncthreads();
+    for (; st + kStages <= steps; st += kStages) {
+#pragma unroll
+        for (int i = 0; i < kStages; ++i) {
+            load_step<BM, BN, FMT>(r[i], X, qw, sc, zp, M, N, K, G, m0, n0,
+                                   kbase + min(st + i + kStages, steps - 1) * kBK, tid);
+            pin();
+            mfma_step<BM, BN>(As[i % 2], Bs[i % 2], acc, lane, wm, wn);
+            store_step<BM, BN, FMT>(r[(i + 1) % kStages], As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
+            __syncthreads();
+        }
     }
-    if (st < steps) mfma_step<BM, BN>(As[0], Bs[0], acc, lane, wm, wn);
+#pragma unroll
+    for (int i = 0; i < kStages - 1; ++i) {
+        const int s = st + i;
+        if (TAIL && s < steps) {  // uniform
+            load_step<BM, BN, FMT>(r[i], X, qw, sc, zp, M, N, K, G, m0, n0, kbase + (steps - 1) * kBK, tid);
+            pin();
+            mfma_step<BM, BN>(As[i % 2], Bs[i % 2], acc, lane, wm, wn);
+            if (s + 1 < steps) store_step<BM, BN, FMT>(r[(i + 1) % kStages], As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
+            __syncthreads();
+        }
+    }
     // C layout of a 32 x 32 tile: lane l, element e -> row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -269,18 +284,27 @@ Plan plan_gemm(int M, int K, int N) {
     return p;
 }
 
-template <int BM, int BN, int FMT>
-void launch_tile(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* part,
-                 int M, int K, int N, const float* row_scale, hipStream_t st) {
+template <int BM, int BN, int FMT, bool TAIL>
+void launch_tile2(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* part,
+                  int M, int K, int N, const float* row_scale, hipStream_t st) {
     const dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)), (unsigned)p.split);
     if (p.split > 1)
-        hipLaunchKernelGGL((w4g32_gemm_kernel<BM, BN, FMT, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
+        hipLaunchKernelGGL((w4g32_gemm_kernel<BM, BN, FMT, true, TAIL>), grid, dim3(256), 0, st, (const uint16_t*)x,
                            (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)part, M,
                            N, K, row_scale);
     else
-        hipLaunchKernelGGL((w4g32_gemm_kernel<BM, BN, FMT, false>), grid, dim3(256), 0, st, (const uint16_t*)x,
+        hipLaunchKernelGGL((w4g32_gemm_kernel<BM, BN, FMT, false, TAIL>), grid, dim3(256), 0, st, (const uint16_t*)x,
                            (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)part, M,
                            N, K, row_scale);
+}
+
+template <int BM, int BN, int FMT>
+void launch_tile(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* part,
+                 int M, int K, int N, const float* row_scale, hipStream_t st) {
+    if ((K / kBK / p.split) % kStages == 0)
+        launch_tile2<BM, BN, FMT, false>(p, x, qw, sc, zp, y, part, M, K, N, row_scale, st);
+    else
+        launch_tile2<BM, BN, FMT, true>(p, x, qw, sc, zp, y, part, M, K, N, row_scale, st);
 }
 
 template <int FMT>
