@@ -41,43 +41,75 @@ enum WeightFormat { kInt4G32 = 0, kFp8E4M3 = 1 };
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Per-thread share of one K step: BM rows x 64 activations (BM / 32 x 16 B per thread) and one
-// (row, 32-wide half) of the weight tile.
-template <int BM>
+// piece of the BN x 64 weight tile.  The weight tile is 2 BN (row, 32-wide half) units; with
+// BN = 64 two threads share a unit (TPU = 2), each taking half of it.
+template <int BM, int BN>
 struct StepRegs {
+    static constexpr int TPU = 256 / (2 * BN), WPT = 4 / TPU;  // threads per unit; INT4 code words per thread
     u32x4_t x[BM / 32];
-    u32x4_t w[2];        // INT4: w[0] = 32 codes; FP8: 32 e4m3 bytes
-    uint32_t s, z, zsh;  // INT4: the group's scale bits, and the byte holding its zero point at bit zsh
+    uint32_t w[2 * WPT];  // INT4: WPT words of codes (8 codes each); FP8: 2 WPT words of e4m3 bytes
+    uint32_t s, z, zsh;   // INT4: the group's scale bits, and the byte holding its zero point at bit zsh
 };
 
-// Out-of-range rows and columns load the last valid row / column instead (addresses are clamped):
-// rows of X and columns of W are independent in the product, and those outputs are never stored.
-// With BN = 64 the threads beyond the 64 weight rows load row (row mod 64) again and discard it.
+// Per-thread addressing, fixed for a workgroup: the thread's activation row and weight row.
+template <int BM, int BN>
+struct StepAddr {
+    const uint16_t* x;  // X row start + this thread's column offset
+    size_t wrow;        // weight row n (clamped)
+    int half, sub;      // which 32-wide half of the step, which part of it
+};
+
+// Out-of-range rows and columns load the last valid row / column instead (addresses are clamped
+// here): rows of X and columns of W are independent in the product, and those outputs are never
+// stored.  Every thread then issues the same loads.
+template <int BM, int BN>
+__device__ __forceinline__ StepAddr<BM, BN> step_addr(const uint16_t* __restrict__ X, int M, int N, int K, int m0,
+                                                      int n0, int tid) {
+    constexpr int TPR = 256 / BM, CH = BM / 32, TPU = StepRegs<BM, BN>::TPU;
+    StepAddr<BM, BN> a;
+    const int row = tid / TPR, part = tid % TPR;
+    a.x = X + (size_t)min(m0 + row, M - 1) * K + 8 * CH * part;
+    const int unit = tid / TPU;
+    a.wrow = (size_t)min(n0 + (unit >> 1), N - 1);
+    a.half = unit & 1;
+    a.sub = tid % TPU;
+    return a;
+}
+
 template <int BM, int BN, int FMT>
-__device__ __forceinline__ void load_step(StepRegs<BM>& r, const uint16_t* __restrict__ X,
+__device__ __forceinline__ void load_step(StepRegs<BM, BN>& r, const StepAddr<BM, BN>& a,
                                           const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
-                                          const uint8_t* __restrict__ zp, int M, int N, int K, int G, int m0,
-                                          int n0, int k0, int tid) {
-    // activations: 256 / BM threads per row, each BM / 32 x 16 B
-    constexpr int TPR = 256 / BM, CH = 8 / TPR;
+                                          const uint8_t* __restrict__ zp, int K, int G, int k0) {
+    constexpr int CH = BM / 32, WPT = StepRegs<BM, BN>::WPT;
     {
-        const int row = tid / TPR, part = tid % TPR, m = min(m0 + row, M - 1);
-        const uint4* p = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0) + CH * part;
+        const uint4* p = reinterpret_cast<const uint4*>(a.x + k0);
 #pragma unroll
         for (int c = 0; c < CH; ++c) r.x[c] = __builtin_bit_cast(u32x4_t, p[c]);
     }
-    const int row = (tid >> 1) & (BN - 1), half = tid & 1, n = min(n0 + row, N - 1);
     if constexpr (FMT == kInt4G32) {
-        const int g = (k0 >> 5) + half;
+        const int g = (k0 >> 5) + a.half;
         int zb;
         zero_loc(g, G, zb, r.zsh);
-        r.w[0] = __builtin_bit_cast(u32x4_t, qw[(size_t)n * G + g]);
-        r.s = sc[(size_t)n * G + g];
-        r.z = zp[(size_t)n * (G >> 1) + zb];  // raw byte: the nibble is taken where it is used
+        const uint32_t* codes = reinterpret_cast<const uint32_t*>(qw + a.wrow * G + g) + WPT * a.sub;
+        if constexpr (WPT == 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(codes);
+            r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(codes);
+            r.w[0] = v.x; r.w[1] = v.y;
+        }
+        r.s = sc[a.wrow * G + g];
+        r.z = zp[a.wrow * (G >> 1) + zb];  // raw byte: the nibble is taken where it is used
     } else {
-        const uint4* p =
-            reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(qw) + (size_t)n * K + k0 + 32 * half);
-        r.w[0] = __builtin_bit_cast(u32x4_t, p[0]);
-        r.w[1] = __builtin_bit_cast(u32x4_t, p[1]);
+        // 32 e4m3 bytes per unit: 8 words, 2 WPT of them per thread
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(qw) + a.wrow * K + k0 +
+                                                              32 * a.half) + 2 * WPT * a.sub;
+        const uint4 v0 = reinterpret_cast<const uint4*>(p)[0];
+        r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+        if constexpr (WPT == 4) {
+            const uint4 v1 = reinterpret_cast<const uint4*>(p)[1];
+            r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
+        }
     }
 }
 
@@ -93,41 +125,38 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
 }
 
 template <int BM, int BN, int FMT>
-__device__ __forceinline__ void store_step(const StepRegs<BM>& r, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds],
-                                           int tid) {
-    constexpr int TPR = 256 / BM, CH = 8 / TPR;
+__device__ __forceinline__ void store_step(const StepRegs<BM, BN>& r, const StepAddr<BM, BN>& ad,
+                                           uint16_t (*As)[kLds], uint16_t (*Bs)[kLds], int tid) {
+    constexpr int TPR = 256 / BM, CH = BM / 32, TPU = StepRegs<BM, BN>::TPU, WPT = StepRegs<BM, BN>::WPT;
     {
         const int row = tid / TPR, part = tid % TPR;
         u32x4_t* a = reinterpret_cast<u32x4_t*>(&As[row][0]) + CH * part;
 #pragma unroll
         for (int c = 0; c < CH; ++c) a[c] = r.x[c];
     }
-    // with BN = 64 the upper 128 threads hold a second copy of rows 0..63 (see load_step) and
-    // write the same values again: no branch, so no load is moved into one
-    const int row = (tid >> 1) & (BN - 1), half = tid & 1;
-    uint32_t out[16];
+    const int row = (tid / TPU) >> 1;
+    constexpr int NOUT = 4 * WPT;  // bf16 pairs per thread (32 / TPU weights)
+    uint32_t out[NOUT];
     if constexpr (FMT == kFp8E4M3) {
-        const uint32_t words[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            out[2 * c] = fp8x2_to_bf16x2<false>(words[c]);
-            out[2 * c + 1] = fp8x2_to_bf16x2<true>(words[c]);
+        for (int c = 0; c < 2 * WPT; ++c) {
+            out[2 * c] = fp8x2_to_bf16x2<false>(r.w[c]);
+            out[2 * c + 1] = fp8x2_to_bf16x2<true>(r.w[c]);
         }
     } else {
         uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
         asm volatile("" : "+v"(mask), "+v"(bias_bits));
         const uint32_t s_lo = r.s & 0xffffu, s_hi = s_lo << 16;
         const float bias = -(128.0f + (float)((r.z >> r.zsh) & 15u)) * bf16_bits((uint16_t)s_lo);
-        const uint32_t words[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < WPT; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                out[4 * j + i] = dequant_pair_exact(((words[j] >> (4 * i)) & mask) | bias_bits, s_lo, s_hi, bias);
+                out[4 * j + i] = dequant_pair_exact(((r.w[j] >> (4 * i)) & mask) | bias_bits, s_lo, s_hi, bias);
     }
-    uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * half]);
+    uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * ad.half + (32 / TPU) * ad.sub]);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) b[c] = make_uint4(out[4 * c], out[4 * c + 1], out[4 * c + 2], out[4 * c + 3]);
+    for (int c = 0; c < NOUT / 4; ++c) b[c] = make_uint4(out[4 * c], out[4 * c + 1], out[4 * c + 2], out[4 * c + 3]);
 }
 
 template <int BM, int BN>
@@ -188,12 +217,12 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
     // Every sub-step issues one stage of loads (steps past the end load the last step again),
     // so the stage consumed next has (kStages - 1) stages of loads issued after it.
     static_assert(kStages % 2 == 0, "stages");
-    StepRegs<BM> r[kStages];
+    const StepAddr<BM, BN> ad = step_addr<BM, BN>(X, M, N, K, m0, n0, tid);
+    StepRegs<BM, BN> r[kStages];
 #pragma unroll
-    for (int i = 0; i < kStages; ++i)
-        load_step<BM, BN, FMT>(r[i], X, qw, sc, zp, M, N, K, G, m0, n0, kbase + min(i, steps - 1) * kBK, tid);
+    for (int i = 0; i < kStages; ++i) load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + min(i, steps - 1) * kBK);
     pin();
-    store_step<BM, BN, FMT>(r[0], As[0], Bs[0], tid);
+    store_step<BM, BN, FMT>(r[0], ad, As[0], Bs[0], tid);
     __syncthreads();
     // whole trips of kStages steps (at the very last step the store writes a copy of that step
     // into the idle buffer, which is never read), then, with TAIL, the remaining steps with guards
@@ -201,11 +230,10 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
     for (; st + kStages <= steps; st += kStages) {
 #pragma unroll
         for (int i = 0; i < kStages; ++i) {
-            load_step<BM, BN, FMT>(r[i], X, qw, sc, zp, M, N, K, G, m0, n0,
-                                   kbase + min(st + i + kStages, steps - 1) * kBK, tid);
+            load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + min(st + i + kStages, steps - 1) * kBK);
             pin();
             mfma_step<BM, BN>(As[i % 2], Bs[i % 2], acc, lane, wm, wn);
-            store_step<BM, BN, FMT>(r[(i + 1) % kStages], As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
+            store_step<BM, BN, FMT>(r[(i + 1) % kStages], ad, As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
             __syncthreads();
         }
     }
@@ -213,10 +241,10 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
     for (int i = 0; i < kStages - 1; ++i) {
         const int s = st + i;
         if (TAIL && s < steps) {  // uniform
-            load_step<BM, BN, FMT>(r[i], X, qw, sc, zp, M, N, K, G, m0, n0, kbase + (steps - 1) * kBK, tid);
+            load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + (steps - 1) * kBK);
             pin();
             mfma_step<BM, BN>(As[i % 2], Bs[i % 2], acc, lane, wm, wn);
-            if (s + 1 < steps) store_step<BM, BN, FMT>(r[(i + 1) % kStages], As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
+            if (s + 1 < steps) store_step<BM, BN, FMT>(r[(i + 1) % kStages], ad, As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
             __syncthreads();
         }
     }
