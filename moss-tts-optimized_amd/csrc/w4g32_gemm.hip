@@ -296,8 +296,9 @@ struct Plan {
 };
 
 // Tile shape and K split: 64-row tiles for M <= 64; 128-wide N tiles when they already give
-// >= 256 workgroups; a K split (2..8) only for M <= 256 while the tiles give fewer than 256
-// workgroups (the fp32 partials cost 8 M N bytes per split).
+// >= 256 workgroups; a K split (2..8) for M <= 256 while the tiles give fewer than 256
+// workgroups, and a split of 2 up to M = 1024 when the tiles give at most 256 (the fp32
+// partials cost 8 M N bytes per split).
 Plan plan_gemm(int M, int K, int N) {
     Plan p;
     p.bm = M <= 64 ? 64 : 128;
@@ -306,9 +307,12 @@ Plan plan_gemm(int M, int K, int N) {
     const long tiles = mt * ((N + p.bn - 1) / p.bn);
     const int steps = K / kBK;
     p.split = 1;
-    if (N % 4 == 0 && M <= 256)
+    if (N % 4 == 0 && M <= 256) {
         while (p.split < 8 && tiles * p.split < 256 && steps % (2 * p.split) == 0 && steps / (2 * p.split) >= 4)
             p.split *= 2;
+    } else if (N % 4 == 0 && M <= 1024 && tiles <= 256 && steps % 4 == 0 && steps / 4 >= 4) {
+        p.split = 2;  // one workgroup per CU would leave half of each CU's wave slots empty
+    }
     return p;
 }
 
