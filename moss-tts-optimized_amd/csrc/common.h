@@ -148,6 +148,28 @@ __device__ __forceinline__ uint32_t dequant_pair_exact(uint32_t d, uint32_t s_lo
     return w;
 }
 
+// The same for the four code pairs of one row-packed word (d_i = pair i in magic form): the eight
+// v_dot2 come first, so each v_cvt_pk reads results written at least 3 instructions earlier and
+// the block needs no s_nop.
+__device__ __forceinline__ void dequant_word_exact(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t s_lo,
+                                                   uint32_t s_hi, float bias, uint32_t (&o)[4]) {
+    float t0, t1, t2, t3;
+    asm("v_dot2_f32_bf16 %0, %8, %12, %14\n\t"
+        "v_dot2_f32_bf16 %4, %8, %13, %14\n\t"
+        "v_dot2_f32_bf16 %1, %9, %12, %14\n\t"
+        "v_dot2_f32_bf16 %5, %9, %13, %14\n\t"
+        "v_dot2_f32_bf16 %2, %10, %12, %14\n\t"
+        "v_dot2_f32_bf16 %6, %10, %13, %14\n\t"
+        "v_dot2_f32_bf16 %3, %11, %12, %14\n\t"
+        "v_dot2_f32_bf16 %7, %11, %13, %14\n\t"
+        "v_cvt_pk_bf16_f32 %0, %0, %4\n\t"
+        "v_cvt_pk_bf16_f32 %1, %1, %5\n\t"
+        "v_cvt_pk_bf16_f32 %2, %2, %6\n\t"
+        "v_cvt_pk_bf16_f32 %3, %3, %7"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(d0), "v"(d1), "v"(d2), "v"(d3), "v"(s_lo), "v"(s_hi), "v"(bias));
+}
+
 // One 128-dim head through RMSNorm + rotate-half RoPE, one wave per head: lane l holds dims
 // l and l + 64 (each other's RoPE partners).  Rounding points of the reference
 // (src/moss_tts/_runtime/kernels.py:142-170): xn = bf16(bf16(x * r) * w); out_l =

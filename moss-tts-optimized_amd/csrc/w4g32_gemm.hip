@@ -149,10 +149,14 @@ __device__ __forceinline__ void store_step(const StepRegs<BM, BN>& r, const Step
         const uint32_t s_lo = r.s & 0xffffu, s_hi = s_lo << 16;
         const float bias = -(128.0f + (float)((r.z >> r.zsh) & 15u)) * bf16_bits((uint16_t)s_lo);
 #pragma unroll
-        for (int j = 0; j < WPT; ++j)
+        for (int j = 0; j < WPT; ++j) {
+            uint32_t o[4];
+            dequant_word_exact((r.w[j] & mask) | bias_bits, ((r.w[j] >> 4) & mask) | bias_bits,
+                               ((r.w[j] >> 8) & mask) | bias_bits, ((r.w[j] >> 12) & mask) | bias_bits, s_lo, s_hi,
+                               bias, o);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                out[4 * j + i] = dequant_pair_exact(((r.w[j] >> (4 * i)) & mask) | bias_bits, s_lo, s_hi, bias);
+            for (int i = 0; i < 4; ++i) out[4 * j + i] = o[i];
+        }
     }
     uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * ad.half + (32 / TPU) * ad.sub]);
 #pragma unroll

@@ -133,14 +133,15 @@ __device__ __forceinline__ float row_partial_unrounded(const XSlice<KG>& xs, con
 }
 
 // Exact form: every weight is the bit-exact bf16 dequant bf16_rne((q - z) * s) before it
-// meets x (dequant_pair_exact), then a dot2 with the matching x pair accumulates in fp32.
+// meets x (dequant_word_exact, four pairs at a time), then a dot2 with the matching x pair
+// accumulates in fp32.
 __device__ __forceinline__ float word_dot_exact(uint32_t w, const uint32_t* xv, float acc, Magic m, uint32_t s_lo,
                                                 uint32_t s_hi, float bias) {
+    uint32_t wq[4];
+    dequant_word_exact(((w >> 0) & m.mask) | m.bias, ((w >> 4) & m.mask) | m.bias, ((w >> 8) & m.mask) | m.bias,
+                       ((w >> 12) & m.mask) | m.bias, s_lo, s_hi, bias, wq);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t d = ((w >> (4 * i)) & m.mask) | m.bias;
-        acc = dot2_bf16(dequant_pair_exact(d, s_lo, s_hi, bias), xv[i], acc);
-    }
+    for (int i = 0; i < 4; ++i) acc = dot2_bf16(wq[i], xv[i], acc);
     return acc;
 }
 
