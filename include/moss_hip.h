@@ -226,6 +226,25 @@ int moss_decode_attention_qkv(const void *qkv, const void *q_norm_w, const void 
 int moss_embedding_sum(const void *ids, const void *text, const void *audio, void *out, int T, int H, int Vt, int V,
                        int Q, void *stream);
 
+/* --------------------------------------------------------------- sampling */
+/* Per row of bf16 logits (rows x stride, the first `vocab` <= 2048 entries used): temperature <= 0
+ * gives the argmax (first maximal index); otherwise the top_k (1..64) largest of logits/temperature
+ * in fp32, descending (ties: lower index first), their softmax, entries whose preceding cumulative
+ * probability exceeds top_p removed, and one index drawn in proportion to the rest with a Philox4x32-10
+ * uniform (counter = (*position, row, salt), key = seed).  out int64 [rows].
+ * Replaces sample_topk, src/moss_tts/_runtime/llm.py:10-19 (torch.topk + softmax + multinomial). */
+int moss_sample_topk(const void *logits, int rows, int stride, int vocab, float temperature, int top_k, float top_p,
+                     unsigned long long seed, const void *position, int salt, void *out, void *stream);
+
+/* next_ids int64 [1 + channels] from the sampled text index (int64 [1], into text_ids int64 [2]) and
+ * audio indices (int64 [channels]): the text token becomes delay_slot_id while *delay_length >= 0 and
+ * audio_end_id at *delay_length == 32; audio code c is kept when c < *audio_length and
+ * (*delay_length < 0 or c >= *delay_length), else pad_code.  Replaces the token logic of _decode,
+ * src/moss_tts/_runtime/llm.py:280-287. */
+int moss_compose_next_ids(const void *text_index, const void *audio_index, const void *text_ids,
+                          const void *audio_length, const void *delay_length, long long delay_slot_id,
+                          long long audio_end_id, int channels, long long pad_code, void *next_ids, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

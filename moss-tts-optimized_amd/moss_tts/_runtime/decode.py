@@ -11,9 +11,13 @@ arithmetic instead (int8 activations per group of 32, integer dot products, fp32
 ``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer -> q||k||v ->
 attention -> int8 quantizer -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul ->
 int8 quantizer -> down (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
-Static input buffers (ids, position) make the step graph-capturable;
-``step()`` copies new inputs into them and replays the graph, as ``FastLLM.step`` does
-(``src/moss_tts/_runtime/llm.py:327-338``).
+The heads matrix holds the 32 audio heads (``audio_stride`` rows each, the first 1024 sampled)
+followed by the 2 text-head rows (gen slot, delay slot; ``llm.py:190-191``); the step ends with the
+reference's sampling and token logic (``llm.py:278-287``): ``sample_topk`` on the text and audio
+logits and the delay-pattern composition of the next 33 ids.
+Static input buffers (ids, position, audio/delay lengths) make the step graph-capturable;
+``decode()`` copies new inputs into them and replays the graph, as ``FastLLM.step`` does
+(``src/moss_tts/_runtime/llm.py:327-338``); ``step()`` returns the logits of the same graph.
 """
 from __future__ import annotations
 
@@ -21,12 +25,15 @@ from dataclasses import dataclass
 
 import torch
 
-from . import attention, w4a8, w4g32
+from . import attention, sampling, w4a8, w4g32
 from .modules import QuantGateUpG32, QuantLinearG32
 from .w4g32 import _require
 
 HIDDEN, INTER, QH, KH, HD = 4096, 12288, 32, 8, 128
 CODEBOOKS, AUDIO_VOCAB = 32, 1025
+SAMPLED_CODES = 1024                      # audio codes a head can emit (1024 is the pad code)
+# MossTTSDelay token ids (the reference model config's defaults)
+GEN_SLOT_ID, DELAY_SLOT_ID, AUDIO_START_ID, AUDIO_END_ID = 151656, 151662, 151652, 151653
 
 
 @dataclass
@@ -62,12 +69,16 @@ class DecodeStepG32:
 
     def __init__(self, layers: list[DecoderLayerG32], final_norm: torch.Tensor, heads: QuantLinearG32,
                  text_embedding: torch.Tensor, audio_embedding: torch.Tensor, *, max_length: int,
-                 eps: float = 1e-6, theta: float = 1e6, w4a8: bool = False):
+                 eps: float = 1e-6, theta: float = 1e6, w4a8: bool = False, audio_stride: int = AUDIO_VOCAB,
+                 greedy: bool = False, seed: int = 0, text_ids=(GEN_SLOT_ID, DELAY_SLOT_ID),
+                 audio_end_id: int = AUDIO_END_ID):
         _require(len(layers) > 0, "at least one layer")
         dev = final_norm.device
         _require(dev.type == "cuda", "the decode step runs on a HIP device")
         _require(max_length > 0 and max_length % 64 == 0, "max_length must be a positive multiple of 64")
         _require(heads.in_features == HIDDEN, "heads must read the 4096-wide hidden state")
+        _require(audio_stride >= SAMPLED_CODES and heads.out_features == CODEBOOKS * audio_stride + 2,
+                 "heads must hold 32 audio heads of audio_stride rows, then the 2 text-head rows")
         self.layers = layers
         self.final_norm = final_norm
         self.heads = heads
@@ -83,6 +94,17 @@ class DecodeStepG32:
         self.ids = torch.zeros((1, CODEBOOKS + 1), device=dev, dtype=torch.int64)
         self.position = torch.zeros(1, device=dev, dtype=torch.int64)
         self.ws = attention.workspace(max_length, dev)
+        self.audio_stride = audio_stride
+        self.greedy = bool(greedy)
+        self.seed = int(seed)
+        self.audio_end_id = int(audio_end_id)
+        self.text_ids_host = tuple(int(t) for t in text_ids)
+        self.text_ids = torch.tensor(list(self.text_ids_host), device=dev, dtype=torch.int64)
+        self.audio_length = torch.full((1,), CODEBOOKS, device=dev, dtype=torch.int64)
+        self.delay_length = torch.full((1,), -1, device=dev, dtype=torch.int64)
+        self.text_index = torch.zeros(1, device=dev, dtype=torch.int64)
+        self.audio_index = torch.zeros(CODEBOOKS, device=dev, dtype=torch.int64)
+        self.next_ids = torch.zeros(CODEBOOKS + 1, device=dev, dtype=torch.int64)
         self.graph = None
         self.logits = None
 
@@ -110,7 +132,22 @@ class DecodeStepG32:
             mlp = layer.down(act)
         _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
                                     dequant=self.heads.dequant)
+        self._sample(logits.view(-1))
         return logits.view(-1)
+
+    def _sample(self, logits: torch.Tensor) -> None:
+        """Text and audio sampling and the next-id composition into ``next_ids`` (``llm.py:278-287``):
+        text top-2 at temperature 1.5, audio top-25 / top-p 0.8 at temperature 1.7, or argmax when
+        greedy."""
+        n_audio = CODEBOOKS * self.audio_stride
+        sampling.sample_topk(logits[n_audio:n_audio + 2], 0.0 if self.greedy else 1.5, 2, 1.0, seed=self.seed,
+                             position=self.position, salt=1, out=self.text_index)
+        sampling.sample_topk(logits[:n_audio].view(CODEBOOKS, self.audio_stride), 0.0 if self.greedy else 1.7, 25,
+                             0.8, seed=self.seed, position=self.position, salt=0, vocab=SAMPLED_CODES,
+                             out=self.audio_index)
+        sampling.compose_next_ids(self.text_index, self.audio_index, self.text_ids, self.audio_length,
+                                  self.delay_length, delay_slot_id=int(self.text_ids_host[1]),
+                                  audio_end_id=self.audio_end_id, out=self.next_ids)
 
     def _forward_w4a8(self) -> torch.Tensor:
         eps = self.eps
@@ -133,6 +170,7 @@ class DecodeStepG32:
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
         _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
                                     dequant=self.heads.dequant)
+        self._sample(logits.view(-1))
         return logits.view(-1)
 
     @torch.inference_mode()
@@ -161,6 +199,18 @@ class DecodeStepG32:
             return self.forward()
         self.graph.replay()
         return self.logits
+
+    @torch.inference_mode()
+    def decode(self, ids: torch.Tensor, position: int, audio_length: int = CODEBOOKS,
+               delay_length: int = -1) -> torch.Tensor:
+        """One step with the reference's ``FastLLM.step`` contract (``llm.py:327-338``): int64 ids
+        ``[1, 33]`` in, the next ids ``[1, 1, 33]`` out (sampled on the device)."""
+        if not 0 <= position < self.max_length:
+            raise ValueError("KV capacity exceeded")
+        self.audio_length.fill_(audio_length)
+        self.delay_length.fill_(delay_length)
+        self.step(ids, position)
+        return self.next_ids.clone().view(1, 1, CODEBOOKS + 1)
 
     @property
     def weight_bytes(self) -> int:
@@ -196,17 +246,26 @@ class DecodeStepG32:
         theta = getattr(lc, "rope_theta", None) if lc is not None else None
         if theta is None and lc is not None:
             theta = (getattr(lc, "rope_parameters", None) or {}).get("rope_theta")
-        heads_bf16 = torch.cat([h.weight[:AUDIO_VOCAB - 1] for h in model.lm_heads[1:]], 0)
+        cfg_ids = (getattr(cfg, "audio_assistant_gen_slot_token_id", GEN_SLOT_ID),
+                   getattr(cfg, "audio_assistant_delay_slot_token_id", DELAY_SLOT_ID))
+        text_head = model.lm_heads[0].weight
+        if not all(0 <= int(t) < text_head.shape[0] for t in cfg_ids):
+            raise ValueError("the gen-slot / delay-slot token ids are outside the text head")
+        text_rows = text_head[torch.tensor([int(t) for t in cfg_ids], device=text_head.device)]
+        heads_bf16 = torch.cat([h.weight[:SAMPLED_CODES] for h in model.lm_heads[1:]] + [text_rows], 0)
         heads = QuantLinearG32(w4g32.quantize_minmax(heads_bf16.float().contiguous()), dequant=dequant)
         audio = torch.stack([e.weight for e in model.emb_ext]).contiguous()
         return cls(layers, lm.norm.weight, heads, lm.embed_tokens.weight.contiguous(), audio,
-                   max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6, w4a8=w4a8)
+                   max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6, w4a8=w4a8,
+                   audio_stride=SAMPLED_CODES, text_ids=cfg_ids,
+                   audio_end_id=getattr(cfg, "audio_end_token_id", AUDIO_END_ID))
 
     # -------------------------------------------------------------- synthetic model
     @classmethod
     @torch.inference_mode()
     def random(cls, n_layers: int, *, max_length: int, device, seed: int = 0, text_vocab: int = 151936,
-               kv_fill: bool = True, dequant: int = w4g32.EXACT, w4a8: bool = False) -> "DecodeStepG32":
+               kv_fill: bool = True, dequant: int = w4g32.EXACT, w4a8: bool = False, greedy: bool = False,
+               sample_seed: int = 0) -> "DecodeStepG32":
         """Random-init Qwen3-8B-shaped weights (N(0, 0.02), min-max INT4-G32 quantized on the
         device), norm weights 1 + N(0, 0.01), embeddings N(0, 1), KV caches N(0, 1)."""
         dev = torch.device(device)
@@ -224,10 +283,11 @@ class DecodeStepG32:
         layers = [DecoderLayerG32(q((QH + 2 * KH) * HD, HIDDEN), q(HIDDEN, QH * HD),
                                   q(2 * INTER, HIDDEN, QuantGateUpG32), q(HIDDEN, INTER),
                                   norm(HIDDEN), norm(HIDDEN), norm(HD), norm(HD)) for _ in range(n_layers)]
-        heads = q(CODEBOOKS * AUDIO_VOCAB, HIDDEN)
+        heads = q(CODEBOOKS * AUDIO_VOCAB + 2, HIDDEN)  # 32 audio heads of 1025 rows, then the 2 text rows
         text = torch.randn((text_vocab, HIDDEN), generator=gen, device=dev).bfloat16()
         audio = torch.randn((CODEBOOKS, AUDIO_VOCAB, HIDDEN), generator=gen, device=dev).bfloat16()
-        eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length, w4a8=w4a8)
+        eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length, w4a8=w4a8, greedy=greedy,
+                  seed=sample_seed)
         if kv_fill:
             for t in eng.keys + eng.values:
                 t.copy_(torch.randn(t.shape, generator=gen, device=dev))

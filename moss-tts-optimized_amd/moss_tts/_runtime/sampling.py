@@ -1,0 +1,62 @@
+"""Decode-step sampling on the gfx950 library.
+
+``sample_topk(logits, temperature=1.7, top_k=25, top_p=0.8)`` keeps the reference's signature and
+meaning (``src/moss_tts/_runtime/llm.py:10-19``); the random draw comes from a counter-based
+Philox4x32-10 keyed by ``seed`` and indexed by the device-side ``position`` and the row, so a
+captured decode graph samples fresh values at every position.  ``compose_next_ids`` is the token
+logic of the reference's ``_decode`` (``llm.py:280-287``).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import native
+from .w4g32 import _cuda_contig, _require
+
+MAX_TOP_K = 64
+MAX_VOCAB = 2048
+
+
+def sample_topk(logits: torch.Tensor, temperature: float = 1.7, top_k: int = 25, top_p: float = 0.8, *,
+                seed: int = 0, position: torch.Tensor | None = None, salt: int = 0, vocab: int | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 logits ``[rows, stride]`` (or ``[stride]``) -> int64 indices ``[rows]`` into the first
+    ``vocab`` entries of each row."""
+    _cuda_contig("logits", logits, torch.bfloat16)
+    rows = 1 if logits.dim() == 1 else logits.shape[0]
+    stride = logits.shape[-1]
+    vocab = stride if vocab is None else int(vocab)
+    _require(0 < vocab <= min(stride, MAX_VOCAB), f"vocab must be in [1, min(stride, {MAX_VOCAB})]")
+    if temperature > 0:
+        _require(1 <= top_k <= min(MAX_TOP_K, vocab), f"top_k must be in [1, min({MAX_TOP_K}, vocab)]")
+    if position is None:
+        position = torch.zeros(1, dtype=torch.int64, device=logits.device)
+    _cuda_contig("position", position, torch.int64, logits.device)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    else:
+        _cuda_contig("out", out, torch.int64, logits.device)
+        _require(out.numel() == rows, f"out must hold {rows} indices")
+    native.call("moss_sample_topk", native.ptr(logits), rows, stride, vocab, float(temperature), int(top_k),
+                float(top_p), int(seed) & 0xFFFFFFFFFFFFFFFF, native.ptr(position), int(salt), native.ptr(out),
+                native.stream_of(logits))
+    return out
+
+
+def compose_next_ids(text_index: torch.Tensor, audio_index: torch.Tensor, text_ids: torch.Tensor,
+                     audio_length: torch.Tensor, delay_length: torch.Tensor, *, delay_slot_id: int,
+                     audio_end_id: int, pad_code: int = 1024, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int64 ``[1 + channels]``: the next text token and audio codes (``llm.py:280-287``)."""
+    dev = audio_index.device
+    for name, t in (("text_index", text_index), ("audio_index", audio_index), ("text_ids", text_ids),
+                    ("audio_length", audio_length), ("delay_length", delay_length)):
+        _cuda_contig(name, t, torch.int64, dev)
+    _require(text_ids.numel() == 2, "text_ids holds the gen-slot and delay-slot ids")
+    channels = audio_index.numel()
+    _require(0 < channels <= 64, "at most 64 channels")
+    if out is None:
+        out = torch.empty(1 + channels, dtype=torch.int64, device=dev)
+    native.call("moss_compose_next_ids", native.ptr(text_index), native.ptr(audio_index), native.ptr(text_ids),
+                native.ptr(audio_length), native.ptr(delay_length), int(delay_slot_id), int(audio_end_id),
+                channels, int(pad_code), native.ptr(out), native.stream_of(audio_index))
+    return out

@@ -37,6 +37,9 @@ class GptqEngine:
     def step(self, ids, position: int):
         return self.decode.step(ids, position)
 
+    def next_ids(self, ids, position: int, audio_length: int, delay_length: int):
+        return self.decode.decode(ids, position, audio_length, delay_length)
+
 
 class MossTTS:
     """One HIP device, one active request, all 32 acoustic codebooks."""
@@ -124,10 +127,17 @@ class MossTTS:
 
     def step(self, ids, position: int):
         """One batch-1 decode step: ``ids`` int64 ``[1, 33]`` (text token, 32 codebook codes) at
-        cache row ``position`` -> audio logits bf16 ``[32 * 1024]`` (a view of the graph's
-        output buffer, valid until the next step)."""
+        cache row ``position`` -> head logits bf16 (32 audio heads, then the 2 text-head rows; a
+        view of the graph's output buffer, valid until the next step)."""
         with self._request():
             return self._engine.step(ids, position)
+
+    def next_ids(self, ids, position: int, audio_length: int = 32, delay_length: int = -1):
+        """The same step with the reference's sampling and delay-pattern logic
+        (``FastLLM.step``, ``src/moss_tts/_runtime/llm.py:327-338``): the next ids int64
+        ``[1, 1, 33]``."""
+        with self._request():
+            return self._engine.next_ids(ids, position, audio_length, delay_length)
 
     @property
     def engine(self):

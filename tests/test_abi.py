@@ -90,3 +90,9 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, null, p, 4096, 64, 0, null) == 1   # partial outputs
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, p, p, 4096, 48, 0, null) == 1      # N_half % 32
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, p, p, 4096, 64, 1, null) == 1      # fused rows 2|4
+    f = ctypes.c_float
+    assert lib.moss_sample_topk(p, 32, 1025, 1024, f(1.7), 0, f(0.8), 0, p, 0, p, null) == 1      # top_k >= 1
+    assert lib.moss_sample_topk(p, 32, 1025, 1024, f(1.7), 65, f(0.8), 0, p, 0, p, null) == 1     # top_k <= 64
+    assert lib.moss_sample_topk(p, 1, 4096, 4096, f(0.0), 1, f(0.8), 0, p, 0, p, null) == 1      # vocab <= 2048
+    assert lib.moss_sample_topk(p, 1, 100, 200, f(0.0), 1, f(0.8), 0, p, 0, p, null) == 1        # stride >= vocab
+    assert lib.moss_compose_next_ids(p, p, p, p, p, 0, 0, 0, 1024, p, null) == 1                  # channels

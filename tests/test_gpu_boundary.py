@@ -42,7 +42,9 @@ def _model(dev, seed=0):
                                              [torch.nn.Linear(4096, 1025, bias=False).bfloat16() for _ in range(32)])
         for h in model.lm_heads:
             torch.nn.init.normal_(h.weight, 0.0, 0.02)
-    model.config = SimpleNamespace(language_config=cfg)
+    # the text head of this small model has 512 rows: special token ids inside it
+    model.config = SimpleNamespace(language_config=cfg, audio_assistant_gen_slot_token_id=100,
+                                   audio_assistant_delay_slot_token_id=101, audio_end_token_id=102)
     return model
 
 
@@ -113,7 +115,13 @@ def test_from_pretrained_install_and_decode(dev, tmp_path):
                          keys0, values0, eng.cos.cpu(), eng.sin.cpu()).float()
     rel = float((logits - ref).norm() / ref.norm())
     print(f"boundary decode: relative L2 {rel:.3e}", flush=True)
-    assert logits.shape == (32 * 1024,) and rel < 2e-2
+    assert logits.shape == (32 * 1024 + 2,) and rel < 2e-2
+    # the reference's step contract: sampled next ids, here greedy-free (temperature sampling)
+    nxt = tts.next_ids(ids, position, 32, -1)
+    assert nxt.shape == (1, 1, 33) and int(nxt[0, 0, 0]) in (100, 101)
+    assert bool(((nxt[0, 0, 1:] >= 0) & (nxt[0, 0, 1:] < 1024)).all())
+    nxt = tts.next_ids(ids, position, 32, 32)                                   # delay 32: audio end token
+    assert int(nxt[0, 0, 0]) == 102 and bool((nxt[0, 0, 1:] == 1024).all())
 
     with pytest.raises(RuntimeError, match="before graph capture"):
         install_gptq(tts.engine, tmp_path)

@@ -1,0 +1,141 @@
+"""GPU parity: decode-step sampling (``moss_sample_topk``, ``moss_compose_next_ids``) vs the oracle.
+
+Bars: argmax, top-k selection and the composed ids are exact; a sampled index equals the oracle's
+draw with the same Philox uniform, except where the oracle's target ``u * sum(kept)`` lies within
+1e-5 (relative) of a cumulative-probability boundary, where the neighbouring kept index is accepted
+(the kernel's expf and summation order differ from numpy's in the last bits).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling as os_
+
+pytestmark = pytest.mark.gpu
+
+
+def _logits(rows, stride, seed, scale=3.0, ties=False):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, stride, generator=g) * scale).bfloat16()
+    if ties:
+        x[:, 10] = x[:, 500] = x.max() + 1
+    return x
+
+
+def _check_draw(got, row_logits, temperature, top_k, top_p, u, what):
+    ref, probs, idx = os_.sample_row(row_logits, temperature, top_k, top_p, u)
+    if got == ref:
+        return
+    kept = probs > 0
+    assert kept[list(idx).index(got)], f"{what}: drew a removed index"
+    cdf = np.cumsum(probs.astype(np.float64))
+    target = float(u) * float(probs.sum(dtype=np.float64))
+    gap = np.min(np.abs(cdf[kept] - target))
+    assert gap <= 1e-5 * max(target, 1e-30), f"{what}: {got} vs {ref}, target {target} not at a boundary"
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_greedy_is_first_argmax(dev, ties):
+    from moss_tts._runtime import sampling
+
+    x = _logits(32, 1025, 1, ties=ties)
+    got = sampling.sample_topk(x.to(dev), 0.0, 25, 0.8, vocab=1024).cpu().numpy()
+    ref = np.argmax(x[:, :1024].float().numpy(), axis=1)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p,rows,stride,vocab", [(1.7, 25, 0.8, 32, 1025, 1024),
+                                                                       (1.5, 2, 1.0, 1, 2, 2),
+                                                                       (1.0, 64, 0.95, 4, 2048, 2048),
+                                                                       (0.7, 1, 0.5, 8, 300, 300)])
+def test_sampling_matches_oracle_draws(dev, temperature, top_k, top_p, rows, stride, vocab):
+    from moss_tts._runtime import sampling
+
+    print(f"sample_topk T={temperature} k={top_k} p={top_p} rows={rows} vocab={vocab}", flush=True)
+    x = _logits(rows, stride, 2)
+    xd = x.to(dev)
+    for position in (0, 7, 2047, 2**33 + 5):
+        pos = torch.tensor([position], dtype=torch.int64, device=dev)
+        for seed in (0, 12345678901234):
+            got = sampling.sample_topk(xd, temperature, top_k, top_p, seed=seed, position=pos, salt=3,
+                                       vocab=vocab).cpu().numpy()
+            for r in range(rows):
+                u = os_.uniform(seed, position, r, 3)
+                _check_draw(int(got[r]), x[r, :vocab].float().numpy(), temperature, top_k, top_p, u,
+                            f"pos {position} seed {seed} row {r}")
+
+
+def test_sampling_frequencies(dev):
+    """Across 2000 positions one row's draws follow the kept probabilities (chi-square bound)."""
+    from moss_tts._runtime import sampling
+
+    x = _logits(1, 64, 3, scale=1.0)
+    _, probs, idx = os_.sample_row(x[0].float().numpy(), 1.0, 8, 0.9, 0.0)
+    p = probs / probs.sum()
+    n = 2000
+    counts = np.zeros(len(p))
+    xd = x.to(dev)
+    pos = torch.zeros(1, dtype=torch.int64, device=dev)
+    outs = []
+    for t in range(n):
+        pos.fill_(t)
+        outs.append(sampling.sample_topk(xd, 1.0, 8, 0.9, seed=99, position=pos))
+    for o in torch.cat(outs).cpu().numpy():
+        counts[list(idx).index(int(o))] += 1
+    keep = p > 0
+    assert counts[~keep].sum() == 0
+    chi2 = (((counts - n * p)[keep] ** 2) / (n * p[keep])).sum()
+    assert chi2 < 30.0
+
+
+@pytest.mark.parametrize("audio_length,delay_length,text_index", [(32, -1, 0), (5, -1, 1), (32, 0, 0), (32, 7, 1),
+                                                                  (32, 32, 0), (3, 1, 1)])
+def test_compose_next_ids(dev, audio_length, delay_length, text_index):
+    from moss_tts._runtime import sampling
+
+    audio = torch.arange(100, 132, dtype=torch.int64, device=dev)
+    text_ids = torch.tensor([151656, 151662], dtype=torch.int64, device=dev)
+    out = sampling.compose_next_ids(torch.tensor([text_index], device=dev), audio, text_ids,
+                                    torch.tensor([audio_length], device=dev), torch.tensor([delay_length], device=dev),
+                                    delay_slot_id=151662, audio_end_id=151653).cpu().numpy()
+    ref = os_.compose_next_ids(text_index, np.arange(100, 132), [151656, 151662], audio_length, delay_length,
+                               151662, 151653)
+    assert np.array_equal(out, ref)
+
+
+@pytest.mark.parametrize("greedy", [True, False])
+def test_decode_step_next_ids(dev, greedy):
+    """The captured step's next ids equal the oracle's sampling of that step's own logits."""
+    from moss_tts._runtime.decode import CODEBOOKS, DecodeStepG32
+
+    print(f"decode next ids greedy={greedy}", flush=True)
+    eng = DecodeStepG32.random(1, max_length=128, device=dev, seed=5, text_vocab=256, greedy=greedy, sample_seed=42)
+    eng.capture()
+    ids = torch.tensor([[17] + [3] * 32], dtype=torch.int64)
+    for position, audio_length, delay_length in ((5, 32, -1), (9, 12, -1), (20, 32, 4)):
+        nxt = eng.decode(ids, position, audio_length, delay_length).view(-1).cpu().numpy()
+        logits = eng.logits.float().cpu().numpy()
+        stride, n_audio = eng.audio_stride, CODEBOOKS * eng.audio_stride
+        audio = logits[:n_audio].reshape(CODEBOOKS, stride)[:, :1024]
+        text = logits[n_audio:n_audio + 2]
+        if greedy:
+            t_idx = int(np.argmax(text))
+            a_idx = np.argmax(audio, axis=1)
+        else:
+            t_idx = os_.sample_row(text, 1.5, 2, 1.0, os_.uniform(42, position, 0, 1))[0]
+            a_idx = np.array([os_.sample_row(audio[c], 1.7, 25, 0.8, os_.uniform(42, position, c, 0))[0]
+                              for c in range(CODEBOOKS)])
+        ref = os_.compose_next_ids(t_idx, a_idx, eng.text_ids_host, audio_length, delay_length,
+                                   eng.text_ids_host[1], eng.audio_end_id)
+        if greedy:
+            assert np.array_equal(nxt, ref)
+        else:
+            # the text token and masked channels are exact; sampled codes obey the draw bar
+            assert nxt[0] == ref[0]
+            for c in range(CODEBOOKS):
+                valid = c < audio_length and (delay_length < 0 or c >= delay_length)
+                if not valid:
+                    assert nxt[1 + c] == 1024
+                else:
+                    _check_draw(int(nxt[1 + c]), audio[c], 1.7, 25, 0.8, os_.uniform(42, position, c, 0),
+                                f"pos {position} channel {c}")
