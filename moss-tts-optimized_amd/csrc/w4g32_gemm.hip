@@ -13,9 +13,9 @@
 //
 // Tile: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
 // (BM/2) x (BN/2), K in steps of 64 (two quantization groups).  Pipeline: two LDS buffers and
-// kStages register stages; while step st is multiplied from one LDS buffer and step st + 1 is
-// converted into the other, the global loads of step st + kStages are issued, so every load
-// has kStages - 1 steps of MFMA work to arrive (one barrier per step).
+// S register stages (stages_for); while step st is multiplied from one LDS buffer and step st + 1
+// is converted into the other, the global loads of step st + S are issued, so every load has
+// S - 1 steps of MFMA work to arrive (one barrier per step).
 // Split-K (SPLIT): workgroup z of a tile covers K range [z K/S, (z+1) K/S) and stores fp32
 // partial sums; gemm_reduce adds them in z order (deterministic) and applies the epilogue.
 // It is used when the tiles alone cannot fill the 256 CUs (small M).
@@ -34,7 +34,10 @@ constexpr int kBK = 64;
 constexpr int kPad = 8;  // bf16 padding per LDS row: breaks the 128-byte bank period
 constexpr int kLds = kBK + kPad;
 constexpr int kXcds = 8;
-constexpr int kStages = 4;  // register stages of the global-load pipeline
+// Register stages of the global-load pipeline: 4, or 2 for the 128 x 128 tile, whose 64
+// accumulators leave room for two stages at two waves per SIMD.
+template <int BM, int BN>
+constexpr int stages_for() { return BM == 128 && BN == 128 ? 2 : 4; }
 
 enum WeightFormat { kInt4G32 = 0, kFp8E4M3 = 1 };
 
@@ -187,7 +190,7 @@ __device__ __forceinline__ void mfma_step(const uint16_t (*As)[kLds], const uint
 
 // FMT == kFp8E4M3: qw is e4m3 [N, K] (row-major bytes), `row_scale` fp32 [N] or null.
 // SPLIT: `part` is fp32 [S, M, N]; gridDim.y = S.  TAIL: the K steps of one workgroup need not
-// be a multiple of kStages.
+// be a multiple of the stage count.
 template <int BM, int BN, int FMT, bool SPLIT, bool TAIL>
 __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
                                                          const uint16_t* __restrict__ sc,
@@ -217,38 +220,39 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    // register stage i % kStages holds step i; kStages is even, so step i's LDS buffer is i % 2.
+    constexpr int kStages_ = stages_for<BM, BN>();
+    // register stage i % kStages_ holds step i; kStages_ is even, so step i's LDS buffer is i % 2.
     // Every sub-step issues one stage of loads (steps past the end load the last step again),
-    // so the stage consumed next has (kStages - 1) stages of loads issued after it.
-    static_assert(kStages % 2 == 0, "stages");
+    // so the stage consumed next has (kStages_ - 1) stages of loads issued after it.
+    static_assert(kStages_ % 2 == 0, "stages");
     const StepAddr<BM, BN> ad = step_addr<BM, BN>(X, M, N, K, m0, n0, tid);
-    StepRegs<BM, BN> r[kStages];
+    StepRegs<BM, BN> r[kStages_];
 #pragma unroll
-    for (int i = 0; i < kStages; ++i) load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + min(i, steps - 1) * kBK);
+    for (int i = 0; i < kStages_; ++i) load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + min(i, steps - 1) * kBK);
     pin();
     store_step<BM, BN, FMT>(r[0], ad, As[0], Bs[0], tid);
     __syncthreads();
-    // whole trips of kStages steps (at the very last step the store writes a copy of that step
+    // whole trips of kStages_ steps (at the very last step the store writes a copy of that step
     // into the idle buffer, which is never read), then, with TAIL, the remaining steps with guards
     int st = 0;
-    for (; st + kStages <= steps; st += kStages) {
+    for (; st + kStages_ <= steps; st += kStages_) {
 #pragma unroll
-        for (int i = 0; i < kStages; ++i) {
-            load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + min(st + i + kStages, steps - 1) * kBK);
+        for (int i = 0; i < kStages_; ++i) {
+            load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + min(st + i + kStages_, steps - 1) * kBK);
             pin();
             mfma_step<BM, BN>(As[i % 2], Bs[i % 2], acc, lane, wm, wn);
-            store_step<BM, BN, FMT>(r[(i + 1) % kStages], ad, As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
+            store_step<BM, BN, FMT>(r[(i + 1) % kStages_], ad, As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
             __syncthreads();
         }
     }
 #pragma unroll
-    for (int i = 0; i < kStages - 1; ++i) {
+    for (int i = 0; i < kStages_ - 1; ++i) {
         const int s = st + i;
         if (TAIL && s < steps) {  // uniform
             load_step<BM, BN, FMT>(r[i], ad, qw, sc, zp, K, G, kbase + (steps - 1) * kBK);
             pin();
             mfma_step<BM, BN>(As[i % 2], Bs[i % 2], acc, lane, wm, wn);
-            if (s + 1 < steps) store_step<BM, BN, FMT>(r[(i + 1) % kStages], ad, As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
+            if (s + 1 < steps) store_step<BM, BN, FMT>(r[(i + 1) % kStages_], ad, As[(i + 1) % 2], Bs[(i + 1) % 2], tid);
             __syncthreads();
         }
     }
@@ -337,7 +341,7 @@ void launch_tile2(const Plan& p, const void* x, const void* qw, const void* sc, 
 template <int BM, int BN, int FMT>
 void launch_tile(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* part,
                  int M, int K, int N, const float* row_scale, hipStream_t st) {
-    if ((K / kBK / p.split) % kStages == 0)
+    if ((K / kBK / p.split) % stages_for<BM, BN>() == 0)
         launch_tile2<BM, BN, FMT, false>(p, x, qw, sc, zp, y, part, M, K, N, row_scale, st);
     else
         launch_tile2<BM, BN, FMT, true>(p, x, qw, sc, zp, y, part, M, K, N, row_scale, st);
