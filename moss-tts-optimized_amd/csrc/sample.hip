@@ -44,6 +44,13 @@ __device__ __forceinline__ unsigned long long order_key(float v, int i) {
     return ((unsigned long long)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
 }
 
+__device__ __forceinline__ float key_value(unsigned long long k) {
+    const uint32_t u = (uint32_t)(k >> 32);
+    return __uint_as_float((u >> 31) ? (u ^ 0x80000000u) : ~u);
+}
+
+__device__ __forceinline__ int key_index(unsigned long long k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
+
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -53,72 +60,119 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
     return k;
 }
 
-// One wave per row; lane l holds logits l + 64 j.
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// Number of lanes whose key is larger than this lane's.
+__device__ __forceinline__ int wave_rank(unsigned long long v) {
+    int r = 0;
+#pragma unroll
+    for (int l = 0; l < kWave; ++l) r += readlane_u64(v, l) > v;
+    return r;
+}
+
+// One wave per row; lane l holds logits l + 64 j as unique keys (value, then lower index first).
+// Selection: T = the k-th largest of the 64 per-lane maxima; at least k keys are >= T, so the top k
+// are among the keys >= T.  Those candidates are compacted into LDS; when at most 64 remain (the
+// usual case: about 31 for k = 25 over 1024 values) each lane ranks one against the others,
+// otherwise k rounds of wave argmax run over the candidates.
 __global__ __launch_bounds__(64) void sample_topk_rows(const uint16_t* __restrict__ logits, int stride, int vocab,
                                                        float temperature, int top_k, float top_p, uint2 key,
                                                        const int64_t* __restrict__ position, uint32_t salt,
                                                        int64_t* __restrict__ out) {
+    __shared__ unsigned long long cand[kWave * kMaxPerLane];
     __shared__ float val[kMaxTopK];
     __shared__ int idx[kMaxTopK];
     __shared__ float prob[kMaxTopK];
     const int row = blockIdx.x, lane = threadIdx.x;
     const uint16_t* lr = logits + (size_t)row * stride;
     const bool greedy = !(temperature > 0.f);
-    float v[kMaxPerLane];
+    const int k = greedy ? 1 : top_k;
+    uint16_t raw[kMaxPerLane];
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) raw[j] = lr[min(lane + kWave * j, vocab - 1)];  // no branch around loads
+    unsigned long long keys[kMaxPerLane];
+    unsigned long long lane_max = 0;
 #pragma unroll
     for (int j = 0; j < kMaxPerLane; ++j) {
         const int i = lane + kWave * j;
         // greedy: the raw logits (argmax is unchanged by a positive scale); else logits / T in fp32
-        v[j] = i < vocab ? (greedy ? bf16_bits(lr[i]) : bf16_bits(lr[i]) / temperature) : -__builtin_inff();
+        const float x = greedy ? bf16_bits(raw[j]) : bf16_bits(raw[j]) / temperature;
+        keys[j] = i < vocab ? order_key(x, i) : 0ull;  // every valid key is nonzero
+        lane_max = keys[j] > lane_max ? keys[j] : lane_max;
     }
-    const int k = greedy ? 1 : top_k;
-    uint32_t taken = 0;
-    for (int r = 0; r < k; ++r) {
-        unsigned long long best = 0;
+    // k <= min(vocab, 64) lanes hold a nonzero maximum, all distinct, so rank k - 1 exists
+    const int max_rank = wave_rank(lane_max);  // every lane takes part in the readlanes
+    const unsigned long long at_k = __ballot(lane_max != 0 && max_rank == k - 1);
+    const unsigned long long thresh = at_k ? readlane_u64(lane_max, __ffsll((long long)at_k) - 1) : 1ull;
+    int count = 0;
 #pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j) {
-            const int i = lane + kWave * j;
-            if (i < vocab && !((taken >> j) & 1u)) {
-                const unsigned long long kk = order_key(v[j], i);
-                best = kk > best ? kk : best;
-            }
+    for (int j = 0; j < kMaxPerLane; ++j) count += keys[j] >= thresh;
+    int incl = count;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int o = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += o;
+    }
+    const int total = __shfl(incl, kWave - 1, kWave);
+    int slot = incl - count;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j)
+        if (keys[j] >= thresh) cand[slot++] = keys[j];
+    __syncthreads();
+    if (total <= kWave) {
+        const unsigned long long mine = lane < total ? cand[lane] : 0ull;
+        const int r = wave_rank(mine);
+        if (mine != 0 && r < k) {
+            val[r] = key_value(mine);
+            idx[r] = key_index(mine);
         }
-        best = wave_max_u64(best);  // every lane holds the winner
-        const int bi = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
-        if ((bi & (kWave - 1)) == lane) {  // the owning lane marks it and publishes it
-            float sel = 0.f;
+    } else {
+        unsigned long long ck[kMaxPerLane];
 #pragma unroll
-            for (int j = 0; j < kMaxPerLane; ++j)
-                if (j == bi / kWave) sel = v[j];
-            taken |= 1u << (bi / kWave);
-            val[r] = sel;
-            idx[r] = bi;
+        for (int t = 0; t < kMaxPerLane; ++t) {
+            const int q = lane + kWave * t;
+            ck[t] = q < total ? cand[q] : 0ull;
+        }
+        for (int r = 0; r < k; ++r) {
+            unsigned long long best = 0;
+#pragma unroll
+            for (int t = 0; t < kMaxPerLane; ++t) best = ck[t] > best ? ck[t] : best;
+            best = wave_max_u64(best);  // keys are unique: exactly one entry equals it
+#pragma unroll
+            for (int t = 0; t < kMaxPerLane; ++t) ck[t] = ck[t] == best ? 0ull : ck[t];
+            if (lane == 0) {
+                val[r] = key_value(best);
+                idx[r] = key_index(best);
+            }
         }
     }
     __syncthreads();
-    if (lane != 0) return;
     if (greedy) {
-        out[row] = idx[0];
+        if (lane == 0) out[row] = idx[0];
         return;
     }
     // softmax over the k values (descending, so val[0] is the maximum), then the top-p cut
+    if (lane < k) prob[lane] = expf(val[lane] - val[0]);
+    __syncthreads();
+    if (lane != 0) return;
     float sum = 0.f;
-    for (int r = 0; r < k; ++r) {
-        prob[r] = expf(val[r] - val[0]);
-        sum += prob[r];
-    }
-    float cum = 0.f, total = 0.f;
+    for (int r = 0; r < k; ++r) sum += prob[r];
+    float cum = 0.f, total_p = 0.f;
     for (int r = 0; r < k; ++r) {
         float q = prob[r] / sum;
         cum += q;
         if (cum - q > top_p) q = 0.f;
         prob[r] = q;
-        total += q;
+        total_p += q;
     }
     const int64_t pos = *position;
     const uint4 rnd = philox4x32_10(make_uint4((uint32_t)pos, (uint32_t)((uint64_t)pos >> 32), (uint32_t)row, salt), key);
     const float u = (float)(rnd.x >> 8) * (1.0f / 16777216.0f);
-    const float target = u * total;
+    const float target = u * total_p;
     float acc = 0.f;
     int pick = 0;
     for (int r = 0; r < k; ++r) {

@@ -65,6 +65,61 @@ def test_sampling_matches_oracle_draws(dev, temperature, top_k, top_p, rows, str
                             f"pos {position} seed {seed} row {r}")
 
 
+def _candidate_count(row_logits: np.ndarray, temperature: float, top_k: int) -> int:
+    """How many keys the kernel's threshold keeps: those >= the k-th largest per-lane maximum
+    (lane l holds indices l + 64 j).  Tells which selection branch a case exercises."""
+    v = (row_logits.astype(np.float32) / np.float32(temperature)).astype(np.float64)
+    order = np.lexsort((np.arange(v.size), -v))          # rank 0 = largest key
+    rank = np.empty(v.size, dtype=np.int64)
+    rank[order] = np.arange(v.size)
+    lane_best = [rank[lane::64].min() for lane in range(min(64, v.size))]
+    thresh = sorted(lane_best)[top_k - 1]
+    return int((rank <= thresh).sum())
+
+
+def _pattern(name: str, rows: int, stride: int):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(rows, stride, generator=g)
+    if name == "lanes":           # the largest values all sit in lanes 0..4: more than 64 candidates
+        for lane in range(5):
+            x[:, lane::64] += 20.0
+    elif name == "equal":         # one value everywhere: the order is the index order
+        x[:] = 1.25
+    elif name == "neg_inf":       # all but 30 entries masked
+        keep = x.clone()
+        x[:] = -float("inf")
+        x[:, 3::37] = keep[:, 3::37]
+    return x.bfloat16()
+
+
+@pytest.mark.parametrize("name,top_k,top_p,vocab,branch", [("lanes", 25, 0.8, 1024, "rounds"),
+                                                          ("lanes", 64, 0.95, 1024, "rounds"),
+                                                          ("equal", 25, 0.8, 1024, "rank"),
+                                                          ("neg_inf", 25, 0.9, 1024, "rank"),
+                                                          ("random", 40, 1.0, 40, "rank")])
+def test_sampling_selection_branches(dev, name, top_k, top_p, vocab, branch):
+    """Both selection branches (rank among <= 64 candidates; rounds of argmax over more) draw the
+    oracle's index; the branch taken is predicted on the CPU from the same threshold."""
+    from moss_tts._runtime import sampling
+
+    print(f"sample_topk pattern={name} k={top_k} vocab={vocab}", flush=True)
+    rows, stride, temperature = 4, 1025, 1.7
+    x = _pattern(name, rows, stride)
+    for r in range(rows):
+        c = _candidate_count(x[r, :vocab].float().numpy(), temperature, top_k)
+        assert (c > 64) == (branch == "rounds"), (name, r, c)
+    xd = x.to(dev)
+    for position in (0, 7, 2047):
+        pos = torch.tensor([position], dtype=torch.int64, device=dev)
+        got = sampling.sample_topk(xd, temperature, top_k, top_p, seed=77, position=pos, salt=0,
+                                   vocab=vocab).cpu().numpy()
+        for r in range(rows):
+            _check_draw(int(got[r]), x[r, :vocab].float().numpy(), temperature, top_k, top_p,
+                        os_.uniform(77, position, r, 0), f"{name} pos {position} row {r}")
+    greedy = sampling.sample_topk(xd, 0.0, 25, 0.8, vocab=vocab).cpu().numpy()
+    assert np.array_equal(greedy, np.argmax(x[:, :vocab].float().numpy(), axis=1))
+
+
 def test_sampling_frequencies(dev):
     """Across 2000 positions one row's draws follow the kept probabilities (chi-square bound)."""
     from moss_tts._runtime import sampling
