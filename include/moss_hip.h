@@ -245,6 +245,17 @@ int moss_compose_next_ids(const void *text_index, const void *audio_index, const
                           const void *audio_length, const void *delay_length, long long delay_slot_id,
                           long long audio_end_id, int channels, long long pad_code, void *next_ids, void *stream);
 
+/* One in-audio step of the host loop on the device, so several decode steps can run in one graph:
+ * ids int64 [width] <- next_ids [width] (and history[step * width ...] when history is not null);
+ * *position += 1; *audio_length += 1 when next_ids[0] is audio_start_id, gen_slot_id or delay_slot_id;
+ * *delay_length becomes 0 at the first delay_slot_id and then grows by 1 each step; status int64 [4]
+ * (optional) = (text token, audio length, delay, position) after the update.  next_ids != ids.
+ * Replaces the host update of src/moss_tts/_runtime/streaming.py:107-112 and the _advance kernel of
+ * src/moss_tts/_runtime/first_audio_graph.py:14-29. */
+int moss_advance_step(const void *next_ids, void *ids, void *position, void *audio_length, void *delay_length,
+                      void *history, void *status, int step, int width, long long audio_start_id,
+                      long long gen_slot_id, long long delay_slot_id, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -206,6 +206,46 @@ __global__ __launch_bounds__(64) void compose_next_ids_kernel(const int64_t* __r
     }
 }
 
+// One in-audio step of the host loop, on the device (src/moss_tts/_runtime/streaming.py:107-112;
+// inside the first 32 steps after the audio start it is the advance kernel of
+// src/moss_tts/_runtime/first_audio_graph.py:14-29): the next ids become the step's input ids
+// (and row `step` of the history), the position advances by one, the audio length grows when the
+// text token is the audio start, gen-slot or delay-slot id, and the delay counter starts at the
+// first delay-slot token and then counts every step.  status = (text token, audio length, delay,
+// position) after the update.
+__global__ __launch_bounds__(64) void advance_step_kernel(const int64_t* __restrict__ next_ids,
+                                                          int64_t* __restrict__ ids, int64_t* __restrict__ position,
+                                                          int64_t* __restrict__ audio_length,
+                                                          int64_t* __restrict__ delay_length,
+                                                          int64_t* __restrict__ history, int64_t* __restrict__ status,
+                                                          int step, int width, int64_t audio_start_id,
+                                                          int64_t gen_slot_id, int64_t delay_slot_id) {
+    const int i = threadIdx.x;
+    if (i < width) {
+        const int64_t v = next_ids[i];
+        ids[i] = v;
+        if (history) history[(size_t)step * width + i] = v;
+    }
+    if (i == 0) {
+        const int64_t text = next_ids[0];
+        const int64_t pos = *position + 1;
+        int64_t len = *audio_length;
+        if (text == audio_start_id || text == gen_slot_id || text == delay_slot_id) ++len;
+        int64_t delay = *delay_length;
+        if (delay < 0 && text == delay_slot_id) delay = 0;
+        if (delay >= 0) ++delay;
+        *position = pos;
+        *audio_length = len;
+        *delay_length = delay;
+        if (status) {
+            status[0] = text;
+            status[1] = len;
+            status[2] = delay;
+            status[3] = pos;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace moss
 
@@ -235,5 +275,18 @@ MOSS_API int moss_compose_next_ids(const void* text_index, const void* audio_ind
                        (const int64_t*)text_index, (const int64_t*)audio_index, (const int64_t*)text_ids,
                        (const int64_t*)audio_length, (const int64_t*)delay_length, (int64_t)delay_slot_id,
                        (int64_t)audio_end_id, channels, (int64_t)pad_code, (int64_t*)next_ids);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_advance_step(const void* next_ids, void* ids, void* position, void* audio_length, void* delay_length,
+                               void* history, void* status, int step, int width, long long audio_start_id,
+                               long long gen_slot_id, long long delay_slot_id, void* stream) {
+    MOSS_CHECK_ARG(next_ids && ids && position && audio_length && delay_length);
+    MOSS_CHECK_ARG(width > 0 && width <= kWave && step >= 0);
+    MOSS_CHECK_ARG(next_ids != ids);
+    hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(kWave), 0, (hipStream_t)stream, (const int64_t*)next_ids,
+                       (int64_t*)ids, (int64_t*)position, (int64_t*)audio_length, (int64_t*)delay_length,
+                       (int64_t*)history, (int64_t*)status, step, width, (int64_t)audio_start_id,
+                       (int64_t)gen_slot_id, (int64_t)delay_slot_id);
     return moss_launch_status();
 }

@@ -71,7 +71,7 @@ class DecodeStepG32:
                  text_embedding: torch.Tensor, audio_embedding: torch.Tensor, *, max_length: int,
                  eps: float = 1e-6, theta: float = 1e6, w4a8: bool = False, audio_stride: int = AUDIO_VOCAB,
                  greedy: bool = False, seed: int = 0, text_ids=(GEN_SLOT_ID, DELAY_SLOT_ID),
-                 audio_end_id: int = AUDIO_END_ID):
+                 audio_end_id: int = AUDIO_END_ID, audio_start_id: int = AUDIO_START_ID):
         _require(len(layers) > 0, "at least one layer")
         dev = final_norm.device
         _require(dev.type == "cuda", "the decode step runs on a HIP device")
@@ -98,6 +98,7 @@ class DecodeStepG32:
         self.greedy = bool(greedy)
         self.seed = int(seed)
         self.audio_end_id = int(audio_end_id)
+        self.audio_start_id = int(audio_start_id)
         self.text_ids_host = tuple(int(t) for t in text_ids)
         self.text_ids = torch.tensor(list(self.text_ids_host), device=dev, dtype=torch.int64)
         self.audio_length = torch.full((1,), CODEBOOKS, device=dev, dtype=torch.int64)
@@ -258,7 +259,8 @@ class DecodeStepG32:
         return cls(layers, lm.norm.weight, heads, lm.embed_tokens.weight.contiguous(), audio,
                    max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6, w4a8=w4a8,
                    audio_stride=SAMPLED_CODES, text_ids=cfg_ids,
-                   audio_end_id=getattr(cfg, "audio_end_token_id", AUDIO_END_ID))
+                   audio_end_id=getattr(cfg, "audio_end_token_id", AUDIO_END_ID),
+                   audio_start_id=getattr(cfg, "audio_start_token_id", AUDIO_START_ID))
 
     # -------------------------------------------------------------- synthetic model
     @classmethod
@@ -292,3 +294,83 @@ class DecodeStepG32:
             for t in eng.keys + eng.values:
                 t.copy_(torch.randn(t.shape, generator=gen, device=dev))
         return eng
+
+
+class FirstAudioGraph:
+    """``steps`` consecutive decode steps in one graph, for the steps right after the audio start
+    (``src/moss_tts/_runtime/first_audio_graph.py:32-104``): each step samples its next ids on the
+    device and ``advance_step`` turns them into the next step's inputs (position, audio length and
+    delay counter as the host loop would, ``streaming.py:107-112``), recording them in ``history``.
+    One graph serves every start position (attention work follows the device-side position), so
+    there is no capacity list; ``run`` needs ``position + steps <= max_length``.  It shares the
+    engine's KV cache and input buffers: it must not overlap another step of the same engine.
+    ``warmup`` runs the body once at position 0, writing KV rows ``[0, steps)`` as the reference's
+    warm-up does."""
+
+    def __init__(self, engine: DecodeStepG32, steps: int = CODEBOOKS):
+        _require(isinstance(engine, DecodeStepG32), "engine must be a DecodeStepG32")
+        _require(0 < steps <= engine.max_length, "steps must be in [1, max_length]")
+        self.engine = engine
+        self.steps = int(steps)
+        dev = engine.device
+        self.history = torch.empty((self.steps, CODEBOOKS + 1), device=dev, dtype=torch.int64)
+        self.status = torch.empty(4, device=dev, dtype=torch.int64)
+        self.graph = None
+
+    def _body(self) -> None:
+        e = self.engine
+        for step in range(self.steps):
+            e.forward()
+            sampling.advance_step(e.next_ids, e.ids.view(-1), e.position, e.audio_length, e.delay_length, step=step,
+                                  history=self.history, status=self.status, audio_start_id=e.audio_start_id,
+                                  gen_slot_id=e.text_ids_host[0], delay_slot_id=e.text_ids_host[1])
+
+    def _initialize(self, ids: torch.Tensor, position: int, delay: int) -> None:
+        e = self.engine
+        e.ids.copy_(ids.reshape(1, CODEBOOKS + 1))
+        e.position.fill_(position)
+        e.audio_length.fill_(1)
+        e.delay_length.fill_(delay)
+
+    @torch.inference_mode()
+    def warmup(self) -> None:
+        if self.graph is not None:
+            raise RuntimeError("First-audio graph already captured")
+        e = self.engine
+        saved = [t.clone() for t in (e.ids, e.position, e.audio_length, e.delay_length)]
+        first = torch.full((1, CODEBOOKS + 1), SAMPLED_CODES, device=e.device, dtype=torch.int64)
+        first[0, 0] = e.audio_start_id
+        try:
+            side = torch.cuda.Stream(e.device)
+            side.wait_stream(torch.cuda.current_stream(e.device))
+            with torch.cuda.stream(side):
+                self._initialize(first, 0, -1)
+                self._body()
+            torch.cuda.current_stream(e.device).wait_stream(side)
+            self._initialize(first, 0, -1)
+            torch.cuda.synchronize(e.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._body()
+            torch.cuda.synchronize(e.device)
+            self.graph = graph
+        finally:
+            for dst, src in zip((e.ids, e.position, e.audio_length, e.delay_length), saved):
+                dst.copy_(src)
+
+    @torch.inference_mode()
+    def run(self, ids: torch.Tensor, position: int, *, delay: int = -1) -> tuple[torch.Tensor, torch.Tensor]:
+        """The ``steps`` next-id rows ``[steps, 33]`` and the final (text token, audio length,
+        delay, position), both device tensors overwritten by the next run."""
+        if self.graph is None:
+            raise RuntimeError("Warm the first-audio graph before use")
+        e = self.engine
+        if not 0 <= position or position + self.steps > e.max_length:
+            raise ValueError("Initial interval exceeds captured context capacity")
+        if tuple(ids.shape) != (1, 1, CODEBOOKS + 1) or ids.dtype != torch.long or ids.device != e.device:
+            raise ValueError("Expected a CUDA int64 audio-start row with all 32 channels")
+        if delay not in (-1, 0):
+            raise ValueError("Only fresh audio or an immediate-delay validation probe is supported")
+        self._initialize(ids, position, delay)
+        self.graph.replay()
+        return self.history, self.status

@@ -4,7 +4,9 @@
 meaning (``src/moss_tts/_runtime/llm.py:10-19``); the random draw comes from a counter-based
 Philox4x32-10 keyed by ``seed`` and indexed by the device-side ``position`` and the row, so a
 captured decode graph samples fresh values at every position.  ``compose_next_ids`` is the token
-logic of the reference's ``_decode`` (``llm.py:280-287``).
+logic of the reference's ``_decode`` (``llm.py:280-287``).  ``advance_step`` is the host loop's
+per-step update (``src/moss_tts/_runtime/streaming.py:107-112``) on the device, so several decode
+steps can be captured in one graph (``src/moss_tts/_runtime/first_audio_graph.py:14-29``).
 """
 from __future__ import annotations
 
@@ -60,3 +62,33 @@ def compose_next_ids(text_index: torch.Tensor, audio_index: torch.Tensor, text_i
                 native.ptr(audio_length), native.ptr(delay_length), int(delay_slot_id), int(audio_end_id),
                 channels, int(pad_code), native.ptr(out), native.stream_of(audio_index))
     return out
+
+
+def advance_step(next_ids: torch.Tensor, ids: torch.Tensor, position: torch.Tensor, audio_length: torch.Tensor,
+                 delay_length: torch.Tensor, *, step: int = 0, history: torch.Tensor | None = None,
+                 status: torch.Tensor | None = None, audio_start_id: int, gen_slot_id: int,
+                 delay_slot_id: int) -> None:
+    """In place: ``ids <- next_ids`` (and ``history[step]``), position + 1, the audio length and delay
+    counter advanced by the text token ``next_ids[0]``; ``status = (text, length, delay, position)``."""
+    dev = next_ids.device
+    for name, t in (("next_ids", next_ids), ("ids", ids), ("position", position), ("audio_length", audio_length),
+                    ("delay_length", delay_length)):
+        _cuda_contig(name, t, torch.int64, dev)
+    width = next_ids.numel()
+    _require(0 < width <= 64 and ids.numel() == width, "ids and next_ids must hold the same 1..64 ids")
+    _require(next_ids.data_ptr() != ids.data_ptr(), "next_ids and ids must be distinct buffers")
+    for name, t in (("position", position), ("audio_length", audio_length), ("delay_length", delay_length)):
+        _require(t.numel() == 1, f"{name} holds one value")
+    if history is not None:
+        _cuda_contig("history", history, torch.int64, dev)
+        _require(history.dim() == 2 and history.shape[1] == width and 0 <= step < history.shape[0],
+                 "history must be [steps, width] with 0 <= step < steps")
+    else:
+        _require(step >= 0, "step must be non-negative")
+    if status is not None:
+        _cuda_contig("status", status, torch.int64, dev)
+        _require(status.numel() == 4, "status holds 4 values")
+    native.call("moss_advance_step", native.ptr(next_ids), native.ptr(ids), native.ptr(position),
+                native.ptr(audio_length), native.ptr(delay_length), native.ptr(history) if history is not None else None,
+                native.ptr(status) if status is not None else None, int(step), width, int(audio_start_id),
+                int(gen_slot_id), int(delay_slot_id), native.stream_of(next_ids))

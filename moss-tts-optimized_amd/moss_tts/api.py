@@ -26,6 +26,7 @@ class GptqEngine:
         self.model = model
         self.max_length = max_length
         self.decode = DecodeStepG32.from_model(model, max_length=max_length)
+        self.first_audio = None
 
     @property
     def graph(self):
@@ -39,6 +40,25 @@ class GptqEngine:
 
     def next_ids(self, ids, position: int, audio_length: int, delay_length: int):
         return self.decode.decode(ids, position, audio_length, delay_length)
+
+    def enable_first_audio_graph(self, steps: int = 32) -> dict:
+        """Capture the steps right after the audio start as one graph
+        (``src/moss_tts/_runtime/first_audio_graph.py:93-110``); one graph serves every position."""
+        from ._runtime.decode import FirstAudioGraph
+
+        if self.first_audio is not None:
+            raise RuntimeError("Install initial-audio graphs once, before accepting requests")
+        if self.decode.graph is None:
+            raise ValueError("Initial-audio graphs require a warmed decode step")
+        graph = FirstAudioGraph(self.decode, steps)
+        graph.warmup()
+        self.first_audio = graph
+        return {"codebooks": 32, "steps": graph.steps}
+
+    def run_first_audio(self, ids, position: int, delay: int = -1):
+        if self.first_audio is None:
+            raise RuntimeError("Warm the first-audio graph before use")
+        return self.first_audio.run(ids, position, delay=delay)
 
 
 class MossTTS:
@@ -138,6 +158,14 @@ class MossTTS:
         ``[1, 1, 33]``."""
         with self._request():
             return self._engine.next_ids(ids, position, audio_length, delay_length)
+
+    def first_audio(self, ids, position: int, delay: int = -1):
+        """The steps after the audio start in one graph replay (``FirstAudioGraph.run``): ``ids`` is
+        the audio-start row int64 ``[1, 1, 33]``; returns the next-id rows ``[steps, 33]`` and the
+        final (text token, audio length, delay, position).  Needs
+        ``engine.enable_first_audio_graph()`` first."""
+        with self._request():
+            return self._engine.run_first_audio(ids, position, delay)
 
     @property
     def engine(self):

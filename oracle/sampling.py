@@ -11,6 +11,8 @@ Reference anchors
   kept index whose cumulative probability exceeds ``u * sum(kept)``; ties in value keep the lower
   index first.
 * The next-id composition -- ``src/moss_tts/_runtime/llm.py:280-287``.
+* The per-step state update of the in-audio loop -- ``src/moss_tts/_runtime/streaming.py:107-112``
+  (inside the first 32 steps after the audio start: ``first_audio_graph.py:14-29``).
 * Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers: as easy as 1, 2, 3",
   SC 2011): the counter-based generator the kernels draw ``u`` from, with counter
   ``(position low, position high, row, salt)`` and key ``(seed low, seed high)``.
@@ -19,7 +21,11 @@ Pinning (tests/test_oracle_sampling.py): Philox against the published known-answ
 Random123 distribution; the top-k set and order against ``torch.topk`` on distinct values and the
 argmax against ``torch.argmax``; the probabilities against ``torch.softmax``; the u-inversion against
 ``torch.multinomial`` frequencies and against the exact probabilities (chi-square bound); the
-composition against a direct loop restating the reference's two ``torch.where`` lines.
+composition against a direct loop restating the reference's two ``torch.where`` lines; the state
+update by its closed forms over token sequences (the delay counter equals the steps since the first
+delay-slot token, inclusive; the audio length counts the start / gen-slot / delay-slot tokens) and,
+composed with the composition, by the audio end appearing exactly 32 steps after the first delay
+slot.
 """
 from __future__ import annotations
 
@@ -114,3 +120,22 @@ def compose_next_ids(text_index: int, audio_index, text_ids, audio_length: int, 
     c = np.arange(audio.size)
     valid = (c < audio_length) & ((delay_length < 0) | (c >= delay_length))
     return np.concatenate([[tok], np.where(valid, audio, pad_code)]).astype(np.int64)
+
+
+def advance_state(next_ids, position: int, audio_length: int, delay_length: int, *, audio_start_id: int,
+                  gen_slot_id: int, delay_slot_id: int):
+    """``streaming.py:107-112`` for one in-audio step: the next ids become the input ids, the
+    position advances, the audio length grows on the start / gen-slot / delay-slot tokens, the delay
+    counter starts at the first delay-slot token and then counts every step.  Returns
+    (ids, position, audio_length, delay_length, status)."""
+    ids = np.asarray(next_ids, dtype=np.int64).copy()
+    text = int(ids[0])
+    if text in (audio_start_id, gen_slot_id, delay_slot_id):
+        audio_length += 1
+    if delay_length < 0 and text == delay_slot_id:
+        delay_length = 0
+    if delay_length >= 0:
+        delay_length += 1
+    position += 1
+    return ids, position, audio_length, delay_length, np.array([text, audio_length, delay_length, position],
+                                                               dtype=np.int64)

@@ -122,6 +122,19 @@ def test_from_pretrained_install_and_decode(dev, tmp_path):
     assert bool(((nxt[0, 0, 1:] >= 0) & (nxt[0, 0, 1:] < 1024)).all())
     nxt = tts.next_ids(ids, position, 32, 32)                                   # delay 32: audio end token
     assert int(nxt[0, 0, 0]) == 102 and bool((nxt[0, 0, 1:] == 1024).all())
+    # the 32 steps after the audio start in one graph
+    with pytest.raises(RuntimeError, match="Warm"):
+        tts.first_audio(nxt, position)
+    assert tts.engine.enable_first_audio_graph() == {"codebooks": 32, "steps": 32}
+    with pytest.raises(RuntimeError, match="once"):
+        tts.engine.enable_first_audio_graph()
+    start = torch.full((1, 1, 33), 1024, dtype=torch.int64, device=dev)
+    start[0, 0, 0] = eng.audio_start_id
+    history, status = tts.first_audio(start, position)
+    history, status = history.cpu(), status.cpu()
+    assert history.shape == (32, 33) and set(history[:, 0].tolist()) <= {100, 101}
+    assert int(status[1]) == 33 and int(status[3]) == position + 32
+    assert bool((history[0, 2:] == 1024).all())                                # audio length 1: channel 0 only
 
     with pytest.raises(RuntimeError, match="before graph capture"):
         install_gptq(tts.engine, tmp_path)

@@ -194,3 +194,71 @@ def test_decode_step_next_ids(dev, greedy):
                 else:
                     _check_draw(int(nxt[1 + c]), audio[c], 1.7, 25, 0.8, os_.uniform(42, position, c, 0),
                                 f"pos {position} channel {c}")
+
+
+START, GEN, DELAY = 151652, 151656, 151662
+
+
+@pytest.mark.parametrize("text,delay,with_outputs", [(GEN, -1, True), (DELAY, -1, True), (DELAY, 4, False),
+                                                     (GEN, 7, True), (START, -1, True), (42, -1, True),
+                                                     (42, 0, False)])
+def test_advance_step_matches_oracle(dev, text, delay, with_outputs):
+    from moss_tts._runtime import sampling
+
+    nxt = torch.tensor([text] + list(range(500, 532)), dtype=torch.int64, device=dev)
+    ids = torch.zeros(33, dtype=torch.int64, device=dev)
+    pos = torch.tensor([77], dtype=torch.int64, device=dev)
+    length = torch.tensor([5], dtype=torch.int64, device=dev)
+    dl = torch.tensor([delay], dtype=torch.int64, device=dev)
+    history = torch.full((4, 33), -9, dtype=torch.int64, device=dev) if with_outputs else None
+    status = torch.full((4,), -9, dtype=torch.int64, device=dev) if with_outputs else None
+    sampling.advance_step(nxt, ids, pos, length, dl, step=2, history=history, status=status, audio_start_id=START,
+                          gen_slot_id=GEN, delay_slot_id=DELAY)
+    r_ids, r_pos, r_len, r_delay, r_status = os_.advance_state(nxt.cpu().numpy(), 77, 5, delay, audio_start_id=START,
+                                                               gen_slot_id=GEN, delay_slot_id=DELAY)
+    assert np.array_equal(ids.cpu().numpy(), r_ids)
+    assert (int(pos), int(length), int(dl)) == (r_pos, r_len, r_delay)
+    if with_outputs:
+        h = history.cpu().numpy()
+        assert np.array_equal(h[2], r_ids) and (h[[0, 1, 3]] == -9).all()
+        assert np.array_equal(status.cpu().numpy(), r_status)
+
+
+@pytest.mark.parametrize("delay", [-1, 0])
+def test_first_audio_graph_equals_sequential_steps(dev, delay):
+    """32 steps in one graph (device-side advance) give the same next ids, step for step, and the
+    same final state as 32 single decode steps with the host-side update."""
+    from moss_tts._runtime.decode import CODEBOOKS, DecodeStepG32, FirstAudioGraph
+
+    print(f"first-audio graph delay={delay}", flush=True)
+    eng = DecodeStepG32.random(1, max_length=128, device=dev, seed=9, text_vocab=256, sample_seed=7)
+    eng.capture()
+    burst = FirstAudioGraph(eng, steps=CODEBOOKS)
+    first = torch.full((1, 1, 33), 1024, dtype=torch.int64, device=dev)
+    first[0, 0, 0] = eng.audio_start_id
+    with pytest.raises(RuntimeError, match="Warm"):
+        burst.run(first, 40)
+    burst.warmup()
+    with pytest.raises(ValueError, match="capacity"):
+        burst.run(first, 128 - CODEBOOKS + 1)
+    with pytest.raises(ValueError, match="audio-start row"):
+        burst.run(first.view(1, 33), 40)
+    with pytest.raises(ValueError, match="fresh audio"):
+        burst.run(first, 40, delay=3)
+    start = 40
+    hist, status = burst.run(first, start, delay=delay)
+    hist = hist.cpu().numpy().copy()
+    status = status.cpu().numpy().copy()
+    gen, dslot = eng.text_ids_host
+    ids, pos, length, d = first, start, 1, delay
+    for t in range(CODEBOOKS):
+        nxt = eng.decode(ids.view(1, 33), pos, audio_length=length, delay_length=d)
+        row = nxt.view(-1).cpu().numpy()
+        assert np.array_equal(row, hist[t]), f"step {t}"
+        _, pos, length, d, st = os_.advance_state(row, pos, length, d, audio_start_id=eng.audio_start_id,
+                                                  gen_slot_id=gen, delay_slot_id=dslot)
+        ids = nxt
+    assert np.array_equal(status, st)
+    assert set(hist[:, 0]) <= {gen, dslot}
+    if delay == 0:   # the probe starts the delay counter: every composed text token is the delay slot
+        assert (hist[:, 0] == dslot).all() and int(status[2]) == CODEBOOKS

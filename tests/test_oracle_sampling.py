@@ -87,3 +87,44 @@ def test_compose_matches_the_reference_where_lines(audio_length, delay_length):
     ref = torch.cat([tok.view(1), torch.where(valid, audio, 1024)]).numpy()
     got = s.compose_next_ids(1, audio.numpy(), text_ids.numpy(), audio_length, delay_length, 151662, 151653)
     assert np.array_equal(got, ref)
+
+
+START, GEN, DELAY, END = 151652, 151656, 151662, 151653
+
+
+@pytest.mark.parametrize("first_delay", [None, 0, 5, 20])
+def test_advance_state_closed_forms(first_delay):
+    """Over a run of in-audio steps: the delay counter after step t is t - t0 + 1 once the first
+    delay-slot token appeared at t0 (else -1), the audio length counts the start / gen / delay
+    tokens, and the position counts steps."""
+    pos, length, delay = 100, 1, -1
+    for t in range(40):
+        tok = DELAY if first_delay is not None and t >= first_delay else GEN
+        ids = np.array([tok] + [7] * 32)
+        _, pos, length, delay, status = s.advance_state(ids, pos, length, delay, audio_start_id=START,
+                                                        gen_slot_id=GEN, delay_slot_id=DELAY)
+        assert pos == 101 + t and length == 2 + t
+        assert delay == (t - first_delay + 1 if first_delay is not None and t >= first_delay else -1)
+        assert list(status) == [tok, length, delay, pos]
+    # other text tokens (an ordinary text id) leave the audio length alone
+    _, _, length2, delay2, _ = s.advance_state(np.array([42] * 33), 0, 3, -1, audio_start_id=START, gen_slot_id=GEN,
+                                               delay_slot_id=DELAY)
+    assert (length2, delay2) == (3, -1)
+
+
+def test_advance_then_compose_ends_audio_after_32_delay_steps():
+    """Composition and state update together: once the text head first picks the delay slot, the
+    composed text token is the delay slot until, 32 steps later, the audio end."""
+    text_ids = np.array([GEN, DELAY])
+    pos, length, delay = 0, 1, -1
+    first = 3
+    emitted = []
+    for t in range(40):
+        text_index = 1 if t == first else 0       # the head asks for the delay slot once, at step 3
+        nxt = s.compose_next_ids(text_index, np.arange(32), text_ids, length, delay, DELAY, END)
+        emitted.append(int(nxt[0]))
+        _, pos, length, delay, _ = s.advance_state(nxt, pos, length, delay, audio_start_id=START, gen_slot_id=GEN,
+                                                   delay_slot_id=DELAY)
+    assert emitted[:first] == [GEN] * first
+    assert emitted[first:first + 32] == [DELAY] * 32
+    assert emitted[first + 32] == END
