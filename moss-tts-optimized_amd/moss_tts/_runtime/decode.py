@@ -110,11 +110,18 @@ class DecodeStepG32:
         self.logits = None
 
     # ------------------------------------------------------------------ forward
-    def forward(self) -> torch.Tensor:
+    def forward(self, head_count: int = CODEBOOKS) -> torch.Tensor:
         """One step from the static ``ids``/``position`` buffers -> logits bf16 ``[N_heads]``.
-        Every (add+)RMSNorm runs inside the projection that consumes it (``norm_gemv``)."""
+        Every (add+)RMSNorm runs inside the projection that consumes it (``norm_gemv``).
+        ``head_count`` < 32 computes and samples only the first ``head_count`` audio heads: valid
+        while ``audio_length <= head_count``, when the composition masks every later channel
+        (``src/moss_tts/_runtime/llm.py:272-279``, ``audio_head_buckets.py``).  The reference fills
+        the skipped heads with zeros and samples all 32 rows to keep torch's RNG sequence; here each
+        row's Philox draw is independent of the others, so the skipped rows are left unwritten and
+        unsampled and the emitted ids are those of the full step."""
+        _require(head_count in (8, 16, 24, CODEBOOKS), "head_count must be 8, 16, 24 or 32")
         if self.w4a8:
-            return self._forward_w4a8()
+            return self._forward_w4a8(head_count)
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
@@ -131,26 +138,42 @@ class DecodeStepG32:
             residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
                                                    residual=residual, dequant=layer.gate_up.dequant)
             mlp = layer.down(act)
-        _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
-                                    dequant=self.heads.dequant)
-        self._sample(logits.view(-1))
-        return logits.view(-1)
+        logits = self._heads(mlp, residual, head_count)
+        self._sample(logits, head_count)
+        return logits
 
-    def _sample(self, logits: torch.Tensor) -> None:
+    def _heads(self, mlp: torch.Tensor, residual: torch.Tensor, head_count: int) -> torch.Tensor:
+        """Final add-RMSNorm + the INT4 heads: all rows, or the first ``head_count`` audio heads
+        and the 2 text rows written into one full-size logits buffer."""
+        eps, heads = self.eps, self.heads
+        if head_count == CODEBOOKS:
+            _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, heads.packed, residual=residual,
+                                        dequant=heads.dequant)
+            return logits.view(-1)
+        n_audio = CODEBOOKS * self.audio_stride
+        logits = torch.empty(heads.out_features, device=self.device, dtype=torch.bfloat16)
+        rows = head_count * self.audio_stride
+        w4g32.norm_gemv(mlp, self.final_norm, eps, heads.packed.rows(0, rows), residual=residual,
+                        dequant=heads.dequant, out=logits[:rows])
+        w4g32.norm_gemv(mlp, self.final_norm, eps, heads.packed.rows(n_audio, n_audio + 2), residual=residual,
+                        dequant=heads.dequant, out=logits[n_audio:])
+        return logits
+
+    def _sample(self, logits: torch.Tensor, head_count: int = CODEBOOKS) -> None:
         """Text and audio sampling and the next-id composition into ``next_ids`` (``llm.py:278-287``):
         text top-2 at temperature 1.5, audio top-25 / top-p 0.8 at temperature 1.7, or argmax when
         greedy."""
         n_audio = CODEBOOKS * self.audio_stride
         sampling.sample_topk(logits[n_audio:n_audio + 2], 0.0 if self.greedy else 1.5, 2, 1.0, seed=self.seed,
                              position=self.position, salt=1, out=self.text_index)
-        sampling.sample_topk(logits[:n_audio].view(CODEBOOKS, self.audio_stride), 0.0 if self.greedy else 1.7, 25,
-                             0.8, seed=self.seed, position=self.position, salt=0, vocab=SAMPLED_CODES,
-                             out=self.audio_index)
+        sampling.sample_topk(logits[:head_count * self.audio_stride].view(head_count, self.audio_stride),
+                             0.0 if self.greedy else 1.7, 25, 0.8, seed=self.seed, position=self.position, salt=0,
+                             vocab=SAMPLED_CODES, out=self.audio_index[:head_count])
         sampling.compose_next_ids(self.text_index, self.audio_index, self.text_ids, self.audio_length,
                                   self.delay_length, delay_slot_id=int(self.text_ids_host[1]),
                                   audio_end_id=self.audio_end_id, out=self.next_ids)
 
-    def _forward_w4a8(self) -> torch.Tensor:
+    def _forward_w4a8(self, head_count: int = CODEBOOKS) -> torch.Tensor:
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
@@ -169,10 +192,9 @@ class DecodeStepG32:
             # than the fused output quantizer, whose 32-row workgroups hold fewer rows in flight
             hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
-        _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, self.heads.packed, residual=residual,
-                                    dequant=self.heads.dequant)
-        self._sample(logits.view(-1))
-        return logits.view(-1)
+        logits = self._heads(mlp, residual, head_count)
+        self._sample(logits, head_count)
+        return logits
 
     @torch.inference_mode()
     def capture(self) -> None:
@@ -307,11 +329,14 @@ class FirstAudioGraph:
     ``warmup`` runs the body once at position 0, writing KV rows ``[0, steps)`` as the reference's
     warm-up does."""
 
-    def __init__(self, engine: DecodeStepG32, steps: int = CODEBOOKS):
+    def __init__(self, engine: DecodeStepG32, steps: int = CODEBOOKS, *, head_prefixes: bool = True):
         _require(isinstance(engine, DecodeStepG32), "engine must be a DecodeStepG32")
         _require(0 < steps <= engine.max_length, "steps must be in [1, max_length]")
         self.engine = engine
         self.steps = int(steps)
+        # step s runs with audio length s + 1 at most: the heads beyond the next multiple of 8
+        # are masked by the composition and are not computed (first_audio_graph.py:45, llm.py:272)
+        self.head_prefixes = bool(head_prefixes)
         dev = engine.device
         self.history = torch.empty((self.steps, CODEBOOKS + 1), device=dev, dtype=torch.int64)
         self.status = torch.empty(4, device=dev, dtype=torch.int64)
@@ -320,7 +345,7 @@ class FirstAudioGraph:
     def _body(self) -> None:
         e = self.engine
         for step in range(self.steps):
-            e.forward()
+            e.forward(min((step // 8 + 1) * 8, CODEBOOKS) if self.head_prefixes else CODEBOOKS)
             sampling.advance_step(e.next_ids, e.ids.view(-1), e.position, e.audio_length, e.delay_length, step=step,
                                   history=self.history, status=self.status, audio_start_id=e.audio_start_id,
                                   gen_slot_id=e.text_ids_host[0], delay_slot_id=e.text_ids_host[1])

@@ -219,7 +219,7 @@ def gateup_silu(x: torch.Tensor, w: PackedW4G32, *, rows_per_wave: int = 0, dequ
     return y
 
 
-def _norm_call(name, x, norm_weight, eps, w, n_out, residual, rows_per_wave, dequant):
+def _norm_call(name, x, norm_weight, eps, w, n_out, residual, rows_per_wave, dequant, out=None):
     _check_row(x, w)
     _require(w.K % 2048 == 0 and w.K <= 8192, "the fused norm needs K % 2048 == 0 and K <= 8192")
     _cuda_contig("norm_weight", norm_weight, torch.bfloat16, w.device)
@@ -232,7 +232,12 @@ def _norm_call(name, x, norm_weight, eps, w, n_out, residual, rows_per_wave, deq
         _cuda_contig("residual", residual, torch.bfloat16, w.device)
         _require(residual.numel() == w.K and _aligned(residual, 16), f"residual must be an aligned row of {w.K}")
         summed = torch.empty_like(x)
-    y = torch.empty((*x.shape[:-1], n_out), dtype=torch.bfloat16, device=x.device)
+    if out is None:
+        y = torch.empty((*x.shape[:-1], n_out), dtype=torch.bfloat16, device=x.device)
+    else:
+        _cuda_contig("out", out, torch.bfloat16, w.device)
+        _require(out.numel() == n_out, f"out must hold {n_out} values")
+        y = out
     native.call(name, native.ptr(x), native.ptr(residual) if residual is not None else None, native.ptr(norm_weight),
                 native.ptr(summed) if summed is not None else None, float(eps), native.ptr(w.qw),
                 native.ptr(w.scales), native.ptr(w.zeros), native.ptr(y), w.K, n_out, rows, mode,
@@ -241,10 +246,12 @@ def _norm_call(name, x, norm_weight, eps, w, n_out, residual, rows_per_wave, deq
 
 
 def norm_gemv(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: PackedW4G32, *,
-              residual: torch.Tensor | None = None, rows_per_wave: int = 0, dequant: int = EXACT):
+              residual: torch.Tensor | None = None, rows_per_wave: int = 0, dequant: int = EXACT,
+              out: torch.Tensor | None = None):
     """``gemv(rmsnorm(x))`` in one kernel; with ``residual``: ``s = bf16(x + residual)``,
-    returns ``(s, gemv(rmsnorm(s)))`` (``src/moss_tts/_runtime/dp4a_norm_projection.py:132-166``)."""
-    return _norm_call("moss_w4g32_norm_gemv", x, norm_weight, eps, w, w.N, residual, rows_per_wave, dequant)
+    returns ``(s, gemv(rmsnorm(s)))`` (``src/moss_tts/_runtime/dp4a_norm_projection.py:132-166``).
+    ``out``: a contiguous bf16 buffer of N values to write instead of a new tensor."""
+    return _norm_call("moss_w4g32_norm_gemv", x, norm_weight, eps, w, w.N, residual, rows_per_wave, dequant, out)
 
 
 def norm_gateup_silu(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: PackedW4G32, *,

@@ -224,16 +224,17 @@ def test_advance_step_matches_oracle(dev, text, delay, with_outputs):
         assert np.array_equal(status.cpu().numpy(), r_status)
 
 
-@pytest.mark.parametrize("delay", [-1, 0])
-def test_first_audio_graph_equals_sequential_steps(dev, delay):
+@pytest.mark.parametrize("delay,prefixes", [(-1, True), (0, True), (-1, False)])
+def test_first_audio_graph_equals_sequential_steps(dev, delay, prefixes):
     """32 steps in one graph (device-side advance) give the same next ids, step for step, and the
-    same final state as 32 single decode steps with the host-side update."""
+    same final state as 32 single decode steps with the host-side update; with head prefixes the
+    graph computes only the first 8/16/24/32 audio heads, which changes no emitted id."""
     from moss_tts._runtime.decode import CODEBOOKS, DecodeStepG32, FirstAudioGraph
 
-    print(f"first-audio graph delay={delay}", flush=True)
+    print(f"first-audio graph delay={delay} head_prefixes={prefixes}", flush=True)
     eng = DecodeStepG32.random(1, max_length=128, device=dev, seed=9, text_vocab=256, sample_seed=7)
     eng.capture()
-    burst = FirstAudioGraph(eng, steps=CODEBOOKS)
+    burst = FirstAudioGraph(eng, steps=CODEBOOKS, head_prefixes=prefixes)
     first = torch.full((1, 1, 33), 1024, dtype=torch.int64, device=dev)
     first[0, 0, 0] = eng.audio_start_id
     with pytest.raises(RuntimeError, match="Warm"):
