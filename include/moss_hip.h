@@ -220,6 +220,15 @@ int moss_decode_attention_qkv(const void *qkv, const void *q_norm_w, const void 
                               const void *sin_t, void *k_cache, void *v_cache, const void *position, void *partial,
                               void *lse, void *out, int L, float eps, void *stream);
 
+/* moss_decode_attention_qkv whose merge also quantizes its bf16 output for the W4A8 O projection:
+ * out_qx int8 [4096] in dot4 order, out_sx fp32 [128] and out_qsum int32 [128] per group of 32, as
+ * moss_int8_quantize_g32 forms them from out.  Replaces reduce_quant,
+ * src/moss_tts/_runtime/attention_quant.py:8-32. */
+int moss_decode_attention_qkv_quant(const void *qkv, const void *q_norm_w, const void *k_norm_w, const void *cos_t,
+                                    const void *sin_t, void *k_cache, void *v_cache, const void *position,
+                                    void *partial, void *lse, void *out, void *out_qx, void *out_sx, void *out_qsum,
+                                    int L, float eps, void *stream);
+
 /* ids int64 [T, Q+1] (text token then Q codebook codes), text bf16 [Vt, H], audio bf16
  * [Q, V, H] -> out bf16 [T, H] with a bf16 rounding after each addition; ids are clamped
  * into their tables.  Replaces embedding_sum (src/moss_tts/_runtime/kernels.py:7-26). */

@@ -177,10 +177,33 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
 // (L <= 4096) are loaded together with the lse values, so a typical merge is one round trip.
 constexpr int kMergeChunk = 64;
 
+// QUANT: the merged bf16 row also leaves as int8 groups of 32 (4 per head; the groups of a
+// wave are its two 32-lane halves), each group's scale max(RN(max|x| / 127), 1e-8), codes
+// rint(x * RN(1 / scale)) stored in dot4 order and their sum, as the standalone quantizer forms
+// them (src/moss_tts/_runtime/attention_quant.py:8-23).
+struct MergeQuant {
+    int8_t* __restrict__ qx;
+    float* __restrict__ sx;
+    int* __restrict__ qsum;
+};
+
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 32));
+    return v;
+}
+
+__device__ __forceinline__ int half_wave_sum(int v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 32);
+    return v;
+}
+
+template <bool QUANT>
 __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict__ part,
                                                          const float* __restrict__ lse,
                                                          const int64_t* __restrict__ pos, uint16_t* __restrict__ out,
-                                                         int L, int S) {
+                                                         int L, int S, MergeQuant mq) {
     __shared__ float wts[kMaxSplits];
     __shared__ float red[2];
     const int hq = blockIdx.x, d = threadIdx.x, w = d / kWave;
@@ -212,7 +235,20 @@ __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict
     for (int u = 0; u < kMergeChunk; ++u)
         if (u < active) acc = fmaf(wts[u], v[u], acc);
     for (int s = kMergeChunk; s < active; ++s) acc = fmaf(wts[s], src[(size_t)s * kHeadDim], acc);
-    out[hq * kHeadDim + d] = f32_to_bf16(acc / wsum);
+    const uint16_t o = f32_to_bf16(acc / wsum);
+    out[hq * kHeadDim + d] = o;
+    if constexpr (QUANT) {
+        const float x = bf16_bits(o);
+        const float scale = g32_scale(half_wave_max(fabsf(x)));
+        const int q = (int)rintf(x * (1.0f / scale));
+        const int total = half_wave_sum(q);
+        const int g = hq * (kHeadDim / 32) + d / 32, t = d & 31;
+        mq.qx[g * 32 + 8 * (t >> 3) + dot4_slot(t & 7)] = (int8_t)q;
+        if (t == 0) {
+            mq.sx[g] = scale;
+            mq.qsum[g] = total;
+        }
+    }
 }
 
 // ids int64 [T, Q+1] (text token, then one code per codebook); grid (T, H / 256).
@@ -251,14 +287,16 @@ MOSS_API int moss_decode_attention(const void* q, const void* k_cache, const voi
     hipLaunchKernelGGL(decode_attn_split<false>, dim3(kKvHeads, S), dim3(256), 0, st, (const uint16_t*)q,
                        (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
                        (float*)lse, L, S, QkvArgs{});
-    hipLaunchKernelGGL(decode_attn_merge, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
-                       (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S);
+    hipLaunchKernelGGL(decode_attn_merge<false>, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
+                       (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S, MergeQuant{});
     return moss_launch_status();
 }
 
-MOSS_API int moss_decode_attention_qkv(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_t,
-                                       const void* sin_t, void* k_cache, void* v_cache, const void* position,
-                                       void* partial, void* lse, void* out, int L, float eps, void* stream) {
+namespace {
+
+int attention_qkv(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_t, const void* sin_t,
+                  void* k_cache, void* v_cache, const void* position, void* partial, void* lse, void* out, int L,
+                  float eps, const MergeQuant* mq, void* stream) {
     MOSS_CHECK_ARG(qkv && q_norm_w && k_norm_w && cos_t && sin_t && k_cache && v_cache && position && partial &&
                    lse && out && eps >= 0.f);
     MOSS_CHECK_ARG(L > 0 && L % kSplit == 0 && L / kSplit <= kMaxSplits);
@@ -271,9 +309,32 @@ MOSS_API int moss_decode_attention_qkv(const void* qkv, const void* q_norm_w, co
     hipLaunchKernelGGL(decode_attn_split<true>, dim3(kKvHeads, S), dim3(256), 0, st, (const uint16_t*)qkv,
                        (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
                        (float*)lse, L, S, qa);
-    hipLaunchKernelGGL(decode_attn_merge, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
-                       (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S);
+    if (mq)
+        hipLaunchKernelGGL(decode_attn_merge<true>, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
+                           (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S, *mq);
+    else
+        hipLaunchKernelGGL(decode_attn_merge<false>, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
+                           (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S, MergeQuant{});
     return moss_launch_status();
+}
+
+}  // namespace
+
+MOSS_API int moss_decode_attention_qkv(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_t,
+                                       const void* sin_t, void* k_cache, void* v_cache, const void* position,
+                                       void* partial, void* lse, void* out, int L, float eps, void* stream) {
+    return attention_qkv(qkv, q_norm_w, k_norm_w, cos_t, sin_t, k_cache, v_cache, position, partial, lse, out, L, eps,
+                         nullptr, stream);
+}
+
+MOSS_API int moss_decode_attention_qkv_quant(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                             const void* cos_t, const void* sin_t, void* k_cache, void* v_cache,
+                                             const void* position, void* partial, void* lse, void* out, void* out_qx,
+                                             void* out_sx, void* out_qsum, int L, float eps, void* stream) {
+    MOSS_CHECK_ARG(out_qx && out_sx && out_qsum && MOSS_ALIGNED(out_sx, 4) && MOSS_ALIGNED(out_qsum, 4));
+    const MergeQuant mq{(int8_t*)out_qx, (float*)out_sx, (int*)out_qsum};
+    return attention_qkv(qkv, q_norm_w, k_norm_w, cos_t, sin_t, k_cache, v_cache, position, partial, lse, out, L, eps,
+                         &mq, stream);
 }
 
 MOSS_API int moss_embedding_sum(const void* ids, const void* text, const void* audio, void* out, int T, int H,

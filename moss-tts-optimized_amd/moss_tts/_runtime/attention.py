@@ -12,7 +12,7 @@ import functools
 
 import torch
 
-from . import native
+from . import native, w4a8
 from .w4g32 import _aligned, _cuda_contig, _require
 
 QH, KH, HD = 32, 8, 128
@@ -59,12 +59,15 @@ def decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, 
 
 def decode_attention_qkv(qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, cos: torch.Tensor,
                          sin: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, position: torch.Tensor,
-                         eps: float, *, out: torch.Tensor | None = None, ws=None) -> torch.Tensor:
+                         eps: float, *, out: torch.Tensor | None = None, ws=None, quantize: bool = False,
+                         out_activation=None):
     """q/k head-norm + RoPE + KV-cache write + decode attention in one pass
     (``src/moss_tts/_runtime/kernels.py:211-251``): ``qkv`` bf16 (6144 values: q | k | v),
     head-norm weights bf16 [128], cos/sin bf16 ``[L, 128]`` tables indexed by the device
     position; K/V row ``position`` of the cache is written.  Returns bf16 ``[1, 1, 4096]``,
-    bit-identical to ``qk_rope`` followed by ``decode_attention``."""
+    bit-identical to ``qk_rope`` followed by ``decode_attention``.  ``quantize``: the merge also
+    forms the int8 groups of 32 of that output for a W4A8 projection and ``(out, activation)`` is
+    returned (``src/moss_tts/_runtime/attention_quant.py:8-32``)."""
     _cuda_contig("qkv", qkv, torch.bfloat16)
     dev = qkv.device
     _require(qkv.numel() == (QH + 2 * KH) * HD, "one q||k||v row of 6144 values required")
@@ -87,10 +90,22 @@ def decode_attention_qkv(qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.
     _require(partial.numel() >= QH * splits(L) * HD and lse.numel() >= QH * splits(L), "workspace too small")
     if out is None:
         out = torch.empty((1, 1, QH * HD), device=dev, dtype=torch.bfloat16)
-    native.call("moss_decode_attention_qkv", native.ptr(qkv), native.ptr(q_norm), native.ptr(k_norm),
+    else:
+        _cuda_contig("out", out, torch.bfloat16, dev)
+        _require(out.numel() == QH * HD, f"out must hold {QH * HD} values")
+    if not quantize:
+        _require(out_activation is None, "out_activation needs quantize=True")
+        native.call("moss_decode_attention_qkv", native.ptr(qkv), native.ptr(q_norm), native.ptr(k_norm),
+                    native.ptr(cos), native.ptr(sin), native.ptr(keys), native.ptr(values), native.ptr(position),
+                    native.ptr(partial), native.ptr(lse), native.ptr(out), L, float(eps), native.stream_of(qkv))
+        return out
+    act = out_activation if out_activation is not None else w4a8.empty_activation(QH * HD, dev)
+    w4a8._check_activation(act, QH * HD, dev)
+    native.call("moss_decode_attention_qkv_quant", native.ptr(qkv), native.ptr(q_norm), native.ptr(k_norm),
                 native.ptr(cos), native.ptr(sin), native.ptr(keys), native.ptr(values), native.ptr(position),
-                native.ptr(partial), native.ptr(lse), native.ptr(out), L, float(eps), native.stream_of(qkv))
-    return out
+                native.ptr(partial), native.ptr(lse), native.ptr(out), native.ptr(act.qx), native.ptr(act.scales),
+                native.ptr(act.sums), L, float(eps), native.stream_of(qkv))
+    return out, act
 
 
 def embedding_sum(ids: torch.Tensor, text_weight: torch.Tensor, audio_weight: torch.Tensor) -> torch.Tensor:

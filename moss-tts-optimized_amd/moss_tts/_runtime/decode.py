@@ -9,7 +9,7 @@ and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188
 here INT4-G32 as well.  With ``w4a8`` the four layer projections run the reference's serving
 arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
 ``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer -> q||k||v ->
-attention -> int8 quantizer -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul ->
+attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul ->
 int8 quantizer -> down (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
 The heads matrix holds the 32 audio heads (``audio_stride`` rows each, the first 1024 sampled)
 followed by the 2 text-head rows (gen slot, delay slot; ``llm.py:190-191``); the step ends with the
@@ -184,9 +184,10 @@ class DecodeStepG32:
             else:
                 residual, _, act = w4a8.norm_quant(mlp, residual, layer.input_norm, eps, normalized=False)
             qkv = w4a8.linear(None, layer.qkv.packed, prequantized=act)
-            attn = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
-                                                  self.values[i], self.position, eps, ws=self.ws)
-            o = w4a8.linear(attn.view(-1), layer.o.packed)
+            _, act = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
+                                                    self.keys[i], self.values[i], self.position, eps, ws=self.ws,
+                                                    quantize=True)
+            o = w4a8.linear(None, layer.o.packed, prequantized=act)
             residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
             # the unfused gate/up (one row per wave) plus the standalone quantizer is faster here
             # than the fused output quantizer, whose 32-row workgroups hold fewer rows in flight

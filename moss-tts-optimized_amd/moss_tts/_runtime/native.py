@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "moss_decode_attention_splits": [_I],
     "moss_decode_attention": [_P, _P, _P, _P, _P, _P, _P, _I, _P],
     "moss_decode_attention_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P],
+    "moss_decode_attention_qkv_quant": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P],
     "moss_embedding_sum": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_fp8_linear": [_P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_fp8_gateup_silu": [_P, _P, _P, _P, _I, _I, _I, _I, _P],

@@ -140,6 +140,15 @@ def test_fused_qkv_attention_equals_rope_then_attention(dev, L, position):
     out = attention.decode_attention_qkv(qkv, qn, kn, cos, sin, k2, v2, pos, 1e-6)
     assert torch.equal(out, ref)
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    # the merge with the int8 quantizer: the same bf16 output, and the activation the standalone
+    # quantizer (bit-exact against the oracle) forms from it
+    from moss_tts._runtime import w4a8
+
+    k3, v3 = kc.clone(), vc.clone()
+    out_q, act = attention.decode_attention_qkv(qkv, qn, kn, cos, sin, k3, v3, pos, 1e-6, quantize=True)
+    assert torch.equal(out_q, ref) and torch.equal(k3, k1) and torch.equal(v3, v1)
+    want = w4a8.quantize(ref.view(-1))
+    assert torch.equal(act.qx, want.qx) and torch.equal(act.scales, want.scales) and torch.equal(act.sums, want.sums)
 
 
 def test_decode_attention_ignores_rows_after_position(dev):
