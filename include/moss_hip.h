@@ -135,6 +135,20 @@ int moss_w4a8_gateup_silu(const void *qx, const void *sx, const void *qsum, cons
                           const void *zp, void *y, void *out_qx, void *out_sx, void *out_qsum, int K, int N_half,
                           int rows_per_wave, void *stream);
 
+/* (add+)RMSNorm + int8 group quantizer + W4A8 projection in one kernel: x bf16 [K] (and res:
+ * s = bf16(x + res), stored to sum_out), norm_w bf16 [K], K in {2048, 4096, 8192}; the
+ * activations equal moss_rmsnorm_quant_g32's bit for bit, y as moss_w4a8_gemv.  Replaces the
+ * fused norm + quantize + projection of src/moss_tts/_runtime/dp4a_norm_projection.py:48-166. */
+int moss_w4a8_norm_gemv(const void *x, const void *res, const void *norm_w, void *sum_out, float eps, const void *qw,
+                        const void *sc, const void *zp, void *y, int K, int N, int rows_per_wave, void *stream);
+
+/* The same in front of the paired gate||up with the SiLU*mul epilogue (y bf16 [N_half], as
+ * moss_w4a8_gateup_silu without output quantization).  Replaces gateup_cluster,
+ * src/moss_tts/_runtime/gateup_cluster.py:44-157 (its norm + quantize + gate/up part). */
+int moss_w4a8_norm_gateup_silu(const void *x, const void *res, const void *norm_w, void *sum_out, float eps,
+                               const void *qw, const void *sc, const void *zp, void *y, int K, int N_half,
+                               int rows_per_wave, void *stream);
+
 /* ------------------------------------------------------------- prefill GEMM */
 /* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);
  * weights are dequantized bit-exactly (bf16_rne((q-z)*s)) into LDS and multiplied with

@@ -66,39 +66,69 @@ __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
     return f32_to_bf16(a * u);
 }
 
+// The fused normalization in front of a W4A8 projection (ACT 1: RMSNorm, ACT 2: add-RMSNorm;
+// src/moss_tts/_runtime/dp4a_norm_projection.py:48-96, dp4a_fusions.py:24-61): every
+// 256-thread workgroup recomputes y = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * w) of the one
+// K-wide row (s = x, or bf16(x + res), which workgroup 0 also stores) and its int8 groups of 32
+// into LDS while its weight rows are in flight.  Thread t owns the 8-value chunks t + 256 c and
+// the 4 chunks of a group sit in one DPP quad, with the summation order and rounding points of
+// rmsnorm_rows<RESIDUAL, true>, so the activations are bit-identical to moss_rmsnorm_quant_g32's.
+struct W8Norm {
+    const uint16_t* __restrict__ x;
+    const uint16_t* __restrict__ res;
+    const uint16_t* __restrict__ w;
+    uint16_t* __restrict__ sum_out;
+    float eps;
+};
+
 // Row-per-wave GEMV: lane l owns groups l + 64 j; KG = ceil(G / 64).  QOUT (paired only):
 // 32 / R waves x R rows per workgroup cover one 32-row output group, which the workgroup
 // also quantizes (the down projection's activations), as the reference's fused gate/up does
-// (src/moss_tts/_runtime/dp4a_scaled.py:70-78).
-template <int KG, int R, bool PAIRED, bool QOUT>
+// (src/moss_tts/_runtime/dp4a_scaled.py:70-78).  ACT 0 reads quantized activations; ACT 1 and
+// 2 form them in the workgroup (W8Norm; K = 2048 KG).
+template <int KG, int R, bool PAIRED, bool QOUT, int ACT = 0>
 __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
     const uint32_t* __restrict__ qx, const float* __restrict__ sx, const int* __restrict__ qsum,
     const uint4* __restrict__ qw, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     uint16_t* __restrict__ y, uint8_t* __restrict__ oq, float* __restrict__ osx, int* __restrict__ osum, int G,
-    int n_out) {
+    int n_out, W8Norm nm) {
     static_assert(!QOUT || (PAIRED && (R == 2 || R == 4)), "output quantization covers 32 paired rows");
+    static_assert(ACT == 0 || !QOUT, "the fused normalization runs with 256-thread workgroups");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
     const int row0 = wave * R;
-    if (!QOUT && row0 >= n_out) return;  // wave-uniform; QOUT grids hold whole groups only
+    // wave-uniform; QOUT grids hold whole groups only, and with ACT > 0 every wave takes part in
+    // the workgroup's normalization first
+    if (ACT == 0 && !QOUT && row0 >= n_out) return;
     constexpr int NR = PAIRED ? 2 * R : R;
     // activations first (completions are counted in order): 32 int8 per group, its scale and sum
     uint4 xa[KG], xb[KG];
     float xs[KG];
     int xq[KG];
+    uint4 nx[KG], nr[KG], nw[KG];  // ACT > 0: the chunks t + 256 c of x, res and the norm weight
+    if constexpr (ACT == 0) {
 #pragma unroll
-    for (int j = 0; j < KG; ++j) {
-        const int g = lane + kWave * j;
-        if (g < G) {
-            const uint4* p = reinterpret_cast<const uint4*>(qx + 8 * g);
-            xa[j] = p[0];
-            xb[j] = p[1];
-            xs[j] = sx[g];
-            xq[j] = qsum[g];
-        } else {
-            xa[j] = xb[j] = make_uint4(0u, 0u, 0u, 0u);
-            xs[j] = 0.f;
-            xq[j] = 0;
+        for (int j = 0; j < KG; ++j) {
+            const int g = lane + kWave * j;
+            if (g < G) {
+                const uint4* p = reinterpret_cast<const uint4*>(qx + 8 * g);
+                xa[j] = p[0];
+                xb[j] = p[1];
+                xs[j] = sx[g];
+                xq[j] = qsum[g];
+            } else {
+                xa[j] = xb[j] = make_uint4(0u, 0u, 0u, 0u);
+                xs[j] = 0.f;
+                xq[j] = 0;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < KG; ++c) {
+            const int ci = threadIdx.x + 256 * c;
+            nw[c] = reinterpret_cast<const uint4*>(nm.w)[ci];
+            nx[c] = reinterpret_cast<const uint4*>(nm.x)[ci];
+            if constexpr (ACT == 2) nr[c] = reinterpret_cast<const uint4*>(nm.res)[ci];
         }
     }
     uint4 w[NR][KG];
@@ -123,6 +153,77 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
                 z[r][j] = 0u;
                 zsh[r][j] = 0u;
             }
+        }
+    }
+    if constexpr (ACT > 0) {
+        __shared__ uint2 lq[256 * KG];
+        __shared__ float lsx[64 * KG];
+        __shared__ int lsum[64 * KG];
+        __shared__ float red[4];
+        float v[KG][8];
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < KG; ++c) {
+            const int ci = threadIdx.x + 256 * c;
+            uint32_t sw[4] = {nx[c].x, nx[c].y, nx[c].z, nx[c].w};
+            if constexpr (ACT == 2) {
+                const uint32_t bw[4] = {nr[c].x, nr[c].y, nr[c].z, nr[c].w};
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+                    sw[p] = pack_bf16x2(bf16_lo(sw[p]) + bf16_lo(bw[p]), bf16_hi(sw[p]) + bf16_hi(bw[p]));
+                if (blockIdx.x == 0) reinterpret_cast<uint4*>(nm.sum_out)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                v[c][2 * p] = bf16_lo(sw[p]);
+                v[c][2 * p + 1] = bf16_hi(sw[p]);
+                ss = fmaf(v[c][2 * p], v[c][2 * p], ss);
+                ss = fmaf(v[c][2 * p + 1], v[c][2 * p + 1], ss);
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[threadIdx.x / kWave] = ss;
+        __syncthreads();
+        float total = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) total += red[i];
+        const float inv = rsqrtf(total / (float)(32 * G) + nm.eps);
+#pragma unroll
+        for (int c = 0; c < KG; ++c) {
+            const int ci = threadIdx.x + 256 * c;
+            const uint32_t wv[4] = {nw[c].x, nw[c].y, nw[c].z, nw[c].w};
+            float yv[8];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
+                const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
+                const uint32_t o = pack_bf16x2(a, b);
+                yv[2 * p] = bf16_lo(o);
+                yv[2 * p + 1] = bf16_hi(o);
+            }
+            float m = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(yv[i]));
+            const float scale = g32_scale(quad_max(m));
+            uint32_t lo, hi;
+            const int part = quantize8_dot4(yv, 1.0f / scale, lo, hi);
+            const float gsum = quad_sum((float)part);  // |sum| <= 32 * 127: exact in fp32
+            lq[ci] = make_uint2(lo, hi);
+            if ((ci & 3) == 0) {
+                lsx[ci / 4] = scale;
+                lsum[ci / 4] = (int)gsum;
+            }
+        }
+        __syncthreads();
+        if (row0 >= n_out) return;  // after the workgroup's barriers
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const int g = lane + kWave * j;
+            const uint4* p = reinterpret_cast<const uint4*>(lq) + 2 * g;
+            xa[j] = p[0];
+            xb[j] = p[1];
+            xs[j] = lsx[g];
+            xq[j] = lsum[g];
         }
     }
     uint32_t mask = 0x0F0F0F0Fu;
@@ -191,7 +292,7 @@ int launch_w4a8(const void* qx, const void* sx, const void* qsum, const void* qw
         hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, QOUT && RV != 1>), grid, block, 0, st,              \
                            (const uint32_t*)qx, (const float*)sx, (const int*)qsum, (const uint4*)qw,             \
                            (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (uint8_t*)oq, (float*)osx,      \
-                           (int*)osum, G, n_out);                                                                 \
+                           (int*)osum, G, n_out, W8Norm{});                                                       \
         return moss_launch_status();                                                                              \
     }
 #define MOSS_W4A8_R(KGV) MOSS_W4A8(KGV, 1) MOSS_W4A8(KGV, 2) MOSS_W4A8(KGV, 4)
@@ -199,6 +300,32 @@ int launch_w4a8(const void* qx, const void* sx, const void* qsum, const void* qw
     MOSS_W4A8_R(8)
 #undef MOSS_W4A8_R
 #undef MOSS_W4A8
+    return (int)hipErrorInvalidValue;
+}
+
+// K = 2048 KG, KG in {1, 2, 4} (K = 2048, 4096, 8192).
+template <bool PAIRED>
+int launch_w4a8_norm(const W8Norm& nm, const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
+                     int rows, hipStream_t st) {
+    const int G = K / 32, KG = K / 2048;
+    if (rows == 0) rows = 1;
+    const int waves = (n_out + rows - 1) / rows;
+    const dim3 grid((waves + 3) / 4), block(256);
+#define MOSS_W4A8N(KGV, RV, ACTV)                                                                                 \
+    if (KG == KGV && rows == RV) {                                                                                \
+        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, false, ACTV>), grid, block, 0, st, nullptr,         \
+                           nullptr, nullptr, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,           \
+                           (uint16_t*)y, nullptr, nullptr, nullptr, G, n_out, nm);                                \
+        return moss_launch_status();                                                                              \
+    }
+#define MOSS_W4A8N_R(KGV, ACTV) MOSS_W4A8N(KGV, 1, ACTV) MOSS_W4A8N(KGV, 2, ACTV) MOSS_W4A8N(KGV, 4, ACTV)
+    if (nm.res) {
+        MOSS_W4A8N_R(1, 2) MOSS_W4A8N_R(2, 2) MOSS_W4A8N_R(4, 2)
+    } else {
+        MOSS_W4A8N_R(1, 1) MOSS_W4A8N_R(2, 1) MOSS_W4A8N_R(4, 1)
+    }
+#undef MOSS_W4A8N_R
+#undef MOSS_W4A8N
     return (int)hipErrorInvalidValue;
 }
 
@@ -246,4 +373,29 @@ MOSS_API int moss_w4a8_gateup_silu(const void* qx, const void* sx, const void* q
     MOSS_CHECK_ARG(MOSS_ALIGNED(out_sx, 4) && MOSS_ALIGNED(out_qsum, 4));
     return launch_w4a8<true, true>(qx, sx, qsum, qw, sc, zp, y, out_qx, out_sx, out_qsum, K, N_half,
                                    rows_per_wave, (hipStream_t)stream);
+}
+
+static int w4a8_norm_entry(bool paired, const void* x, const void* res, const void* norm_w, void* sum_out, float eps,
+                           const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
+                           int rows_per_wave, void* stream) {
+    MOSS_CHECK_ARG(x && norm_w && qw && sc && zp && y && n_out > 0 && eps >= 0.f);
+    MOSS_CHECK_ARG(K == 2048 || K == 4096 || K == 8192);
+    MOSS_CHECK_ARG(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(qw, 16));
+    MOSS_CHECK_ARG(!res || (sum_out && MOSS_ALIGNED(res, 16) && MOSS_ALIGNED(sum_out, 16)));
+    const W8Norm nm{(const uint16_t*)x, (const uint16_t*)res, (const uint16_t*)norm_w, (uint16_t*)sum_out, eps};
+    return paired ? launch_w4a8_norm<true>(nm, qw, sc, zp, y, K, n_out, rows_per_wave, (hipStream_t)stream)
+                  : launch_w4a8_norm<false>(nm, qw, sc, zp, y, K, n_out, rows_per_wave, (hipStream_t)stream);
+}
+
+MOSS_API int moss_w4a8_norm_gemv(const void* x, const void* res, const void* norm_w, void* sum_out, float eps,
+                                 const void* qw, const void* sc, const void* zp, void* y, int K, int N,
+                                 int rows_per_wave, void* stream) {
+    return w4a8_norm_entry(false, x, res, norm_w, sum_out, eps, qw, sc, zp, y, K, N, rows_per_wave, stream);
+}
+
+MOSS_API int moss_w4a8_norm_gateup_silu(const void* x, const void* res, const void* norm_w, void* sum_out, float eps,
+                                        const void* qw, const void* sc, const void* zp, void* y, int K, int N_half,
+                                        int rows_per_wave, void* stream) {
+    return w4a8_norm_entry(true, x, res, norm_w, sum_out, eps, qw, sc, zp, y, K, N_half, rows_per_wave, stream);
 }

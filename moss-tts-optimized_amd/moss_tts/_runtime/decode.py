@@ -8,9 +8,10 @@ attention (one kernel) -> split merge -> O GEMV -> add-RMSNorm + gate||up GEMV w
 and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``),
 here INT4-G32 as well.  With ``w4a8`` the four layer projections run the reference's serving
 arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
-``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer -> q||k||v ->
-attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer -> gate||up with SiLU*mul ->
-int8 quantizer -> down (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
+``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer + q||k||v (one
+kernel) -> attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer ->
+gate||up with SiLU*mul -> int8 quantizer -> down
+(``src/moss_tts/_runtime/llm.py:29-56,71-92``).
 The heads matrix holds the 32 audio heads (``audio_stride`` rows each, the first 1024 sampled)
 followed by the 2 text-head rows (gen slot, delay slot; ``llm.py:190-191``); the step ends with the
 reference's sampling and token logic (``llm.py:278-287``): ``sample_topk`` on the text and audio
@@ -179,18 +180,22 @@ class DecodeStepG32:
         residual = x
         mlp = None
         for i, layer in enumerate(self.layers):
+            # add-RMSNorm + quantizer + q||k||v in one kernel, two rows per wave (fewer workgroups
+            # repeat the normalization); measured faster than the separate norm_quant here
             if i == 0:
-                _, _, act = w4a8.norm_quant(x, None, layer.input_norm, eps, normalized=False)
+                qkv = w4a8.norm_linear(x, layer.input_norm, eps, layer.qkv.packed, rows_per_wave=2)
             else:
-                residual, _, act = w4a8.norm_quant(mlp, residual, layer.input_norm, eps, normalized=False)
-            qkv = w4a8.linear(None, layer.qkv.packed, prequantized=act)
+                residual, qkv = w4a8.norm_linear(mlp, layer.input_norm, eps, layer.qkv.packed, residual=residual,
+                                                 rows_per_wave=2)
             _, act = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
                                                     self.keys[i], self.values[i], self.position, eps, ws=self.ws,
                                                     quantize=True)
             o = w4a8.linear(None, layer.o.packed, prequantized=act)
+            # gate/up: the separate add-RMSNorm + quantizer is faster than the fused form here
+            # (3072 workgroups would each repeat the normalization); the SiLU*mul output is
+            # quantized by the standalone quantizer, faster than the gate/up's fused output
+            # quantizer (its 32-row workgroups hold fewer rows in flight)
             residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
-            # the unfused gate/up (one row per wave) plus the standalone quantizer is faster here
-            # than the fused output quantizer, whose 32-row workgroups hold fewer rows in flight
             hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
         logits = self._heads(mlp, residual, head_count)

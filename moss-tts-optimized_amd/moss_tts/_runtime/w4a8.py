@@ -105,6 +105,34 @@ def norm_quant(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Ten
     return summed, y, a
 
 
+def norm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: PackedW4G32, *,
+                residual: torch.Tensor | None = None, paired: bool = False, rows_per_wave: int = 0):
+    """(add+)RMSNorm, the int8 group quantizer and the W4A8 projection in one kernel
+    (``src/moss_tts/_runtime/dp4a_norm_projection.py:48-166``): ``y``, or ``(summed, y)`` with
+    ``residual``; bit-identical to ``norm_quant`` followed by ``linear(prequantized=...)``."""
+    _require(isinstance(w, PackedW4G32), "w must be a PackedW4G32")
+    k = w.K
+    _require(k in (2048, 4096, 8192), "the fused norm needs K in {2048, 4096, 8192}")
+    _require(rows_per_wave in (0, 1, 2, 4), "rows_per_wave must be 0 (auto), 1, 2 or 4")
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.numel() == k and _aligned(x, 16), f"one aligned bf16 row of {k} values required")
+    _cuda_contig("norm_weight", norm_weight, torch.bfloat16, w.device)
+    _require(norm_weight.numel() == k and _aligned(norm_weight, 16), f"norm_weight must be an aligned row of {k}")
+    summed = None
+    if residual is not None:
+        _cuda_contig("residual", residual, torch.bfloat16, w.device)
+        _require(residual.numel() == k and _aligned(residual, 16), f"residual must be an aligned row of {k}")
+        summed = torch.empty_like(x)
+    _require(not paired or w.N % 2 == 0, "gate||up weight needs an even number of rows")
+    n_out = w.N // 2 if paired else w.N
+    y = torch.empty((*x.shape[:-1], n_out), dtype=torch.bfloat16, device=w.device)
+    native.call("moss_w4a8_norm_gateup_silu" if paired else "moss_w4a8_norm_gemv", native.ptr(x),
+                native.ptr(residual) if residual is not None else None, native.ptr(norm_weight),
+                native.ptr(summed) if summed is not None else None, float(eps), native.ptr(w.qw), native.ptr(w.scales),
+                native.ptr(w.zeros), native.ptr(y), k, n_out, rows_per_wave, native.stream_of(x))
+    return y if summed is None else (summed, y)
+
+
 def linear(x: torch.Tensor | None, w: PackedW4G32, *, paired: bool = False, fused: bool = False,
            prequantized: QuantizedActivation | None = None, rows_per_wave: int = 0,
            out: torch.Tensor | None = None, out_activation: QuantizedActivation | None = None):

@@ -97,6 +97,9 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_sample_topk(p, 1, 100, 200, f(0.0), 1, f(0.8), 0, p, 0, p, null) == 1        # stride >= vocab
     assert lib.moss_compose_next_ids(p, p, p, p, p, 0, 0, 0, 1024, p, null) == 1                  # channels
     q = ctypes.c_void_p(8192)
+    assert lib.moss_w4a8_norm_gemv(p, null, p, null, f(1e-6), p, p, p, p, 12288, 64, 0, null) == 1   # K
+    assert lib.moss_w4a8_norm_gemv(p, p, p, null, f(1e-6), p, p, p, p, 4096, 64, 0, null) == 1       # sum_out
+    assert lib.moss_w4a8_norm_gateup_silu(p, null, p, null, f(1e-6), p, p, p, p, 4096, 64, 3, null) == 1  # rows
     assert lib.moss_decode_attention_qkv_quant(p, p, p, p, p, p, p, p, p, p, p, null, p, p, 2048, f(1e-6),
                                                null) == 1                                         # out_qx
     assert lib.moss_decode_attention_qkv_quant(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 2000, f(1e-6),

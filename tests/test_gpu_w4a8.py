@@ -167,6 +167,27 @@ def test_gateup_vs_oracle(dev, k, n_half, fused):
         assert torch.equal(_bits(plain), _bits(y))
 
 
+@pytest.mark.parametrize("k,n,paired,residual,rows", [(4096, 6144, False, False, 0), (4096, 6144, False, True, 2),
+                                                       (4096, 12288, True, True, 0), (4096, 100, True, False, 4),
+                                                       (2048, 300, False, True, 1), (8192, 256, True, True, 0)])
+def test_fused_norm_projection_equals_norm_quant_then_linear(dev, k, n, paired, residual, rows):
+    """The (add+)RMSNorm + quantizer inside the W4A8 projection gives the bits of norm_quant
+    followed by the projection on its activations (which are pinned against the oracle)."""
+    from moss_tts._runtime import w4a8
+
+    print(f"w4a8 fused norm K={k} N={n} paired={paired} residual={residual} rows={rows}", flush=True)
+    pw = _packed(*_weights(2 * n if paired else n, k, 90 + k % 5), dev)
+    x, r = (_row(k, 91) * 3).to(dev), _row(k, 92).to(dev)
+    w = (1 + 0.1 * _row(k, 93)).to(dev)
+    summed, _, act = w4a8.norm_quant(x, r if residual else None, w, 1e-6, normalized=False)
+    want = w4a8.linear(None, pw, paired=paired, prequantized=act, rows_per_wave=rows)
+    got = w4a8.norm_linear(x, w, 1e-6, pw, residual=r if residual else None, paired=paired, rows_per_wave=rows)
+    if residual:
+        got_sum, got = got
+        assert torch.equal(_bits(got_sum), _bits(summed))
+    assert torch.equal(_bits(got), _bits(want))
+
+
 def test_w4a8_mlp_chain_matches_oracle_chain(dev):
     """norm_quant -> fused gate/up -> down, with every activation bit-checked against the
     oracle quantizer on the previous bf16 output."""
