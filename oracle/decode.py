@@ -4,6 +4,13 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  Order of operations:
 ``src/moss_tts/_runtime/llm.py:227-260`` (fused residual path) with the projections as
 dequant-then-matmul (``src/moss_tts/calibration.py:185-188``) rounded to bf16 at each
 projection output, heads ``src/moss_tts/_runtime/llm.py:271-279``.
+
+Pinning (tests/test_oracle_decode.py): ``decode_step`` against transformers' own ``Qwen3Model``
+(the layers the reference's backbone runs) on the same bf16 weights, input embedding and KV rows:
+logits and the written K/V row within 1e-2 relative L2 at positions 0 and 37; a wrong GQA head
+mapping (0.11) or a dropped residual (1.45) fails it.  ``decode_step_w4a8`` against
+``decode_step`` on the same INT4 weights: 4.9e-3 relative L2 (the int8 activation rounding), bar
+3e-2; a dropped residual gives 1.41.
 """
 from __future__ import annotations
 
