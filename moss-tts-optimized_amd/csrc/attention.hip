@@ -54,54 +54,72 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
     if (t0 > p) return;  // uniform over the workgroup
     const bool owner = FUSED && p < t0 + kSplit;  // this split holds the new row (uniform)
 
-    // all global loads first, staged in LDS: 4 threads per cache row, each a 32-dim quarter
-    // (64 contiguous bytes) of K and of V; rows t0..t0+63 lie inside the cache (L % 64 == 0)
+    // Loads, in this order: the q path's (L2 hits; the new K and V rows are loaded by every
+    // workgroup, branch-free, and used by the owner only), then the K/V tile.  Completions are
+    // counted in order, so the head norm + RoPE below runs while the tile is still arriving.
     const int tl = tid >> 2, qd = tid & 3, t = t0 + tl;
-    {
-        const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
-        const uint4* vr = reinterpret_cast<const uint4*>(vc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
-        uint4* kd = reinterpret_cast<uint4*>(&ks[tl][32 * qd]);
-        uint4* vd = reinterpret_cast<uint4*>(&vs[tl][32 * qd]);
-        const uint4 a0 = kr[0], a1 = kr[1], a2 = kr[2], a3 = kr[3];
-        const uint4 b0 = vr[0], b1 = vr[1], b2 = vr[2], b3 = vr[3];
-        kd[0] = a0; kd[1] = a1; kd[2] = a2; kd[3] = a3;
-        vd[0] = b0; vd[1] = b1; vd[2] = b2; vd[3] = b3;
-    }
     const int j = tid / kWave, l = tid & (kWave - 1);
-    uint16_t nk0 = 0, nk1 = 0, nv0 = 0, nv1 = 0;
+    constexpr int D = kHeadDim;
+    uint16_t qx0 = 0, qx1 = 0, qw0 = 0, qw1 = 0, cs0 = 0, cs1 = 0, sn0 = 0, sn1 = 0;
+    uint16_t kx0 = 0, kx1 = 0, kw0 = 0, kw1 = 0, vx0 = 0, vx1 = 0;
+    uint32_t qpair = 0;
     if constexpr (FUSED) {
         // wave j: query head 4 hk + j; lane l: dims l and l + 64
-        constexpr int D = kHeadDim;
         const uint16_t* cr = qa.cos_t + (size_t)p * D;
         const uint16_t* sr = qa.sin_t + (size_t)p * D;
-        const float c0 = bf16_bits(cr[l]), c1 = bf16_bits(cr[l + 64]);
-        const float s0 = bf16_bits(sr[l]), s1 = bf16_bits(sr[l + 64]);
         const uint16_t* qh = q + (size_t)(hk * kGroup + j) * D;
+        const uint16_t* kh = q + (size_t)(kQHeads + hk) * D;
+        const uint16_t* vh = q + (size_t)(kQHeads + kKvHeads + hk) * D;
+        qx0 = qh[l]; qx1 = qh[l + 64];
+        qw0 = qa.qnw[l]; qw1 = qa.qnw[l + 64];
+        cs0 = cr[l]; cs1 = cr[l + 64];
+        sn0 = sr[l]; sn1 = sr[l + 64];
+        kx0 = kh[l]; kx1 = kh[l + 64];
+        kw0 = qa.knw[l]; kw1 = qa.knw[l + 64];
+        vx0 = vh[l]; vx1 = vh[l + 64];
+    } else {
+        qpair = reinterpret_cast<const uint32_t*>(q + (size_t)hk * kGroup * kHeadDim)[tid];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the K/V tile: 4 threads per cache row, each a 32-dim quarter (64 contiguous bytes) of K and
+    // of V; rows t0..t0+63 lie inside the cache (L % 64 == 0)
+    const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
+    const uint4* vr = reinterpret_cast<const uint4*>(vc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
+    const uint4 ka0 = kr[0], ka1 = kr[1], ka2 = kr[2], ka3 = kr[3];
+    const uint4 vb0 = vr[0], vb1 = vr[1], vb2 = vr[2], vb3 = vr[3];
+    __builtin_amdgcn_sched_barrier(0);
+    uint16_t nk0 = 0, nk1 = 0, nv0 = 0, nv1 = 0;
+    if constexpr (FUSED) {
+        const float c0 = bf16_bits(cs0), c1 = bf16_bits(cs1);
+        const float s0 = bf16_bits(sn0), s1 = bf16_bits(sn1);
         uint16_t o0, o1;
-        head_norm_rope(bf16_bits(qh[l]), bf16_bits(qh[l + 64]), bf16_bits(qa.qnw[l]), bf16_bits(qa.qnw[l + 64]), c0,
-                       c1, s0, s1, qa.eps, o0, o1);
+        head_norm_rope(bf16_bits(qx0), bf16_bits(qx1), bf16_bits(qw0), bf16_bits(qw1), c0, c1, s0, s1, qa.eps, o0,
+                       o1);
         qs[j][l] = bf16_bits(o0);
         qs[j][l + 64] = bf16_bits(o1);
         if (owner && j == 0) {  // the new K row of this KV head, into the cache
-            const uint16_t* kh = q + (size_t)(kQHeads + hk) * D;
-            head_norm_rope(bf16_bits(kh[l]), bf16_bits(kh[l + 64]), bf16_bits(qa.knw[l]), bf16_bits(qa.knw[l + 64]),
-                           c0, c1, s0, s1, qa.eps, nk0, nk1);
+            head_norm_rope(bf16_bits(kx0), bf16_bits(kx1), bf16_bits(kw0), bf16_bits(kw1), c0, c1, s0, s1, qa.eps,
+                           nk0, nk1);
             uint16_t* kd = kc + ((size_t)hk * L + p) * D;
             kd[l] = nk0;
             kd[l + 64] = nk1;
         } else if (owner && j == 1) {  // the new V row (a copy), into the cache
-            const uint16_t* vh = q + (size_t)(kQHeads + kKvHeads + hk) * D;
-            nv0 = vh[l];
-            nv1 = vh[l + 64];
+            nv0 = vx0;
+            nv1 = vx1;
             uint16_t* vd = vc + ((size_t)hk * L + p) * D;
             vd[l] = nv0;
             vd[l + 64] = nv1;
         }
     } else {
-        const uint32_t w = reinterpret_cast<const uint32_t*>(q + (size_t)hk * kGroup * kHeadDim)[tid];
         const int jj = (2 * tid) / kHeadDim, d = (2 * tid) % kHeadDim;
-        qs[jj][d] = bf16_lo(w);
-        qs[jj][d + 1] = bf16_hi(w);
+        qs[jj][d] = bf16_lo(qpair);
+        qs[jj][d + 1] = bf16_hi(qpair);
+    }
+    {
+        uint4* kd = reinterpret_cast<uint4*>(&ks[tl][32 * qd]);
+        uint4* vd = reinterpret_cast<uint4*>(&vs[tl][32 * qd]);
+        kd[0] = ka0; kd[1] = ka1; kd[2] = ka2; kd[3] = ka3;
+        vd[0] = vb0; vd[1] = vb1; vd[2] = vb2; vd[3] = vb3;
     }
     __syncthreads();
     if (owner) {  // the new row replaces the stale cache row staged above
@@ -207,14 +225,20 @@ __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict
     __shared__ float wts[kMaxSplits];
     __shared__ float red[2];
     const int hq = blockIdx.x, d = threadIdx.x, w = d / kWave;
-    const int p = (int)min(max(pos[0], (int64_t)0), (int64_t)(L - 1));
-    const int active = p / kSplit + 1;
+    // the partials and this thread's first lse value are loaded together with the position
+    // (clamped into the workspace, branch-free) and masked once the position is known
+    const int64_t p_raw = pos[0];
     const float* src = part + (size_t)hq * S * kHeadDim + d;
     float v[kMergeChunk];
 #pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u) v[u] = u < active ? src[(size_t)u * kHeadDim] : 0.f;
-    float mx = -INFINITY;
-    for (int s = d; s < active; s += 128) mx = fmaxf(mx, lse[hq * S + s]);
+    for (int u = 0; u < kMergeChunk; ++u) v[u] = src[(size_t)min(u, S - 1) * kHeadDim];
+    const float lse0 = lse[hq * S + min(d, S - 1)];
+    const int p = (int)min(max(p_raw, (int64_t)0), (int64_t)(L - 1));
+    const int active = p / kSplit + 1;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u) v[u] = u < active ? v[u] : 0.f;
+    float mx = d < active ? lse0 : -INFINITY;
+    for (int s = d + 128; s < active; s += 128) mx = fmaxf(mx, lse[hq * S + s]);
     mx = wave_max(mx);
     if ((d & (kWave - 1)) == 0) red[w] = mx;
     __syncthreads();
@@ -222,7 +246,7 @@ __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict
     __syncthreads();
     float ws = 0.f;
     for (int s = d; s < active; s += 128) {
-        const float e = expf(lse[hq * S + s] - mx);
+        const float e = expf((s == d ? lse0 : lse[hq * S + s]) - mx);
         wts[s] = e;
         ws += e;
     }
@@ -262,9 +286,19 @@ __global__ __launch_bounds__(256) void embedding_sum_rows(const int64_t* __restr
     const int64_t* row = ids + (size_t)t * (Q + 1);
     const int64_t tok = min(max(row[0], (int64_t)0), (int64_t)(Vt - 1));
     float x = bf16_bits(text[(size_t)tok * H + d]);
-    for (int qi = 0; qi < Q; ++qi) {
-        const int64_t c = min(max(row[qi + 1], (int64_t)0), (int64_t)(V - 1));
-        x = round_bf16(x + bf16_bits(audio[((size_t)qi * V + c) * H + d]));
+    // the codebook rows of the usual Q <= 32 are loaded together, then added in order
+    constexpr int kBatch = 32;
+    for (int q0 = 0; q0 < Q; q0 += kBatch) {
+        uint16_t a[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int qi = min(q0 + u, Q - 1);
+            const int64_t c = min(max(row[qi + 1], (int64_t)0), (int64_t)(V - 1));
+            a[u] = audio[((size_t)qi * V + c) * H + d];
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (q0 + u < Q) x = round_bf16(x + bf16_bits(a[u]));
     }
     out[(size_t)t * H + d] = f32_to_bf16(x);
 }

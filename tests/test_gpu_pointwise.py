@@ -109,6 +109,29 @@ def test_decode_attention(dev, L, position):
     assert torch.equal(out, again)
 
 
+def test_decode_attention_workspace_across_positions(dev):
+    """One workspace through positions with different numbers of active splits: every call
+    matches the oracle and a call on a fresh workspace."""
+    from moss_tts._runtime import attention
+    from oracle import attention as oa
+
+    L = 2048
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn((32, 128), generator=g).bfloat16()
+    kc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
+    vc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    ws = attention.workspace(L, dev)
+    for position in (2047, 5, 63, 64, 1000, 0, 2047, 130):
+        print(f"attention workspace reuse p={position}", flush=True)
+        pos = torch.tensor([position], dtype=torch.int64, device=dev)
+        out = attention.decode_attention(qd, kd, vd, pos, ws=ws)
+        fresh = attention.decode_attention(qd, kd, vd, pos, ws=attention.workspace(L, dev))
+        assert torch.equal(out, fresh), position
+        ref = oa.decode_attention(q, kc, vc, position).reshape(1, 1, 4096)
+        _close(out, ref.bfloat16(), f"attention reuse p={position}", exact_frac=0.95)
+
+
 def test_decode_attention_rejects_unaligned_length(dev):
     from moss_tts._runtime import attention
 
