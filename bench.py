@@ -276,6 +276,8 @@ def main() -> int:
                     help="timed replays of the 36-layer decode step (0 skips it)")
     ap.add_argument("--decode-layers", type=int, default=36)
     ap.add_argument("--no-extras", action="store_true", help="skip the FP8 and prefill GEMM lines")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the 36-layer decode step (both arithmetics) and its lines, for a kernel trace")
     ap.add_argument("--pmc-pass", choices=("gemv", "gemm"), default=None,
                     help="eager launches only, for rocprofv3 --pmc: 'gemv' = a 512 MiB copy of known size, "
                          "then one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy; "
@@ -299,6 +301,11 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     arch = native.device_arch(0)
+    if args.decode_only:
+        _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode step only")
+        for w8 in (False, True):
+            decode_step_bench(torch, args.decode_layers, max(1, args.decode_steps), dev, w4a8=w8)
+        return 0
     _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); building {args.copies} weight copies")
 
     gen = torch.Generator(device=dev).manual_seed(1234)
