@@ -79,16 +79,19 @@ __device__ __forceinline__ StepAddr<BM, BN> step_addr(const uint16_t* __restrict
     return a;
 }
 
-template <int BM, int BN, int FMT>
-__device__ __forceinline__ void load_step(StepRegs<BM, BN>& r, const StepAddr<BM, BN>& a,
-                                          const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
-                                          const uint8_t* __restrict__ zp, int K, int G, int k0) {
-    constexpr int CH = BM / 32, WPT = StepRegs<BM, BN>::WPT;
-    {
-        const uint4* p = reinterpret_cast<const uint4*>(a.x + k0);
+template <int BM, int BN>
+__device__ __forceinline__ void load_a(StepRegs<BM, BN>& r, const StepAddr<BM, BN>& a, int k0) {
+    constexpr int CH = BM / 32;
+    const uint4* p = reinterpret_cast<const uint4*>(a.x + k0);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) r.x[c] = __builtin_bit_cast(u32x4_t, p[c]);
-    }
+    for (int c = 0; c < CH; ++c) r.x[c] = __builtin_bit_cast(u32x4_t, p[c]);
+}
+
+template <int BM, int BN, int FMT>
+__device__ __forceinline__ void load_b(StepRegs<BM, BN>& r, const StepAddr<BM, BN>& a,
+                                       const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
+                                       const uint8_t* __restrict__ zp, int K, int G, int k0) {
+    constexpr int WPT = StepRegs<BM, BN>::WPT;
     if constexpr (FMT == kInt4G32) {
         const int g = (k0 >> 5) + a.half;
         int zb;
@@ -116,6 +119,14 @@ __device__ __forceinline__ void load_step(StepRegs<BM, BN>& r, const StepAddr<BM
     }
 }
 
+template <int BM, int BN, int FMT>
+__device__ __forceinline__ void load_step(StepRegs<BM, BN>& r, const StepAddr<BM, BN>& a,
+                                          const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
+                                          const uint8_t* __restrict__ zp, int K, int G, int k0) {
+    load_a<BM, BN>(r, a, k0);
+    load_b<BM, BN, FMT>(r, a, qw, sc, zp, K, G, k0);
+}
+
 // Keeps the scheduler from moving instructions across this point: the loads of a pipeline stage
 // stay where they are issued instead of being sunk next to their first use (which would shrink
 // the prefetch distance to nothing); the compiler still places the waits before each use.
@@ -127,16 +138,19 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
 }
 
-template <int BM, int BN, int FMT>
-__device__ __forceinline__ void store_step(const StepRegs<BM, BN>& r, const StepAddr<BM, BN>& ad,
-                                           uint16_t (*As)[kLds], uint16_t (*Bs)[kLds], int tid) {
-    constexpr int TPR = 256 / BM, CH = BM / 32, TPU = StepRegs<BM, BN>::TPU, WPT = StepRegs<BM, BN>::WPT;
-    {
-        const int row = tid / TPR, part = tid % TPR;
-        u32x4_t* a = reinterpret_cast<u32x4_t*>(&As[row][0]) + CH * part;
+template <int BM, int BN>
+__device__ __forceinline__ void store_a(const StepRegs<BM, BN>& r, uint16_t (*As)[kLds], int tid) {
+    constexpr int TPR = 256 / BM, CH = BM / 32;
+    const int row = tid / TPR, part = tid % TPR;
+    u32x4_t* a = reinterpret_cast<u32x4_t*>(&As[row][0]) + CH * part;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) a[c] = r.x[c];
-    }
+    for (int c = 0; c < CH; ++c) a[c] = r.x[c];
+}
+
+template <int BM, int BN, int FMT>
+__device__ __forceinline__ void store_b(const StepRegs<BM, BN>& r, const StepAddr<BM, BN>& ad, uint16_t (*Bs)[kLds],
+                                        int tid) {
+    constexpr int TPU = StepRegs<BM, BN>::TPU, WPT = StepRegs<BM, BN>::WPT;
     const int row = (tid / TPU) >> 1;
     constexpr int NOUT = 4 * WPT;  // bf16 pairs per thread (32 / TPU weights)
     uint32_t out[NOUT];
@@ -164,6 +178,13 @@ __device__ __forceinline__ void store_step(const StepRegs<BM, BN>& r, const Step
     uint4* b = reinterpret_cast<uint4*>(&Bs[row][32 * ad.half + (32 / TPU) * ad.sub]);
 #pragma unroll
     for (int c = 0; c < NOUT / 4; ++c) b[c] = make_uint4(out[4 * c], out[4 * c + 1], out[4 * c + 2], out[4 * c + 3]);
+}
+
+template <int BM, int BN, int FMT>
+__device__ __forceinline__ void store_step(const StepRegs<BM, BN>& r, const StepAddr<BM, BN>& ad,
+                                           uint16_t (*As)[kLds], uint16_t (*Bs)[kLds], int tid) {
+    store_a<BM, BN>(r, As, tid);
+    store_b<BM, BN, FMT>(r, ad, Bs, tid);
 }
 
 template <int BM, int BN>
