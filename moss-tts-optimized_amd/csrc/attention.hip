@@ -191,8 +191,9 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
 }
 
 // grid 32 query heads, 128 threads (one per dim).  The splits holding attended rows are
-// weighted by exp(lse - max lse) and summed in split order.  The first 64 splits' partials
-// (L <= 4096) are loaded together with the lse values, so a typical merge is one round trip.
+// weighted by exp(lse - max lse) and summed in split order, with no LDS and no barrier.  The
+// first 64 splits' partials (L <= 4096) are loaded together with the lse values, so a typical
+// merge is one round trip.
 constexpr int kMergeChunk = 64;
 
 // QUANT: the merged bf16 row also leaves as int8 groups of 32 (4 per head; the groups of a
@@ -222,43 +223,33 @@ __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict
                                                          const float* __restrict__ lse,
                                                          const int64_t* __restrict__ pos, uint16_t* __restrict__ out,
                                                          int L, int S, MergeQuant mq) {
-    __shared__ float wts[kMaxSplits];
-    __shared__ float red[2];
-    const int hq = blockIdx.x, d = threadIdx.x, w = d / kWave;
-    // the partials and this thread's first lse value are loaded together with the position
+    const int hq = blockIdx.x, d = threadIdx.x, lane = d & (kWave - 1);
+    // the partials and this lane's first lse value are loaded together with the position
     // (clamped into the workspace, branch-free) and masked once the position is known
     const int64_t p_raw = pos[0];
     const float* src = part + (size_t)hq * S * kHeadDim + d;
     float v[kMergeChunk];
 #pragma unroll
     for (int u = 0; u < kMergeChunk; ++u) v[u] = src[(size_t)min(u, S - 1) * kHeadDim];
-    const float lse0 = lse[hq * S + min(d, S - 1)];
+    const float lse0 = lse[hq * S + min(lane, S - 1)];
     const int p = (int)min(max(p_raw, (int64_t)0), (int64_t)(L - 1));
     const int active = p / kSplit + 1;
-#pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u) v[u] = u < active ? v[u] : 0.f;
-    float mx = d < active ? lse0 : -INFINITY;
-    for (int s = d + 128; s < active; s += 128) mx = fmaxf(mx, lse[hq * S + s]);
+    // each wave covers every split (lane s holds splits s, s + 64, ...): the max, the weights and
+    // their sum need no exchange between the two waves
+    float mx = lane < active ? lse0 : -INFINITY;
+    for (int s = lane + kWave; s < active; s += kWave) mx = fmaxf(mx, lse[hq * S + s]);
     mx = wave_max(mx);
-    if ((d & (kWave - 1)) == 0) red[w] = mx;
-    __syncthreads();
-    mx = fmaxf(red[0], red[1]);
-    __syncthreads();
-    float ws = 0.f;
-    for (int s = d; s < active; s += 128) {
-        const float e = expf((s == d ? lse0 : lse[hq * S + s]) - mx);
-        wts[s] = e;
-        ws += e;
-    }
-    ws = wave_sum(ws);
-    if ((d & (kWave - 1)) == 0) red[w] = ws;
-    __syncthreads();
-    const float wsum = red[0] + red[1];
+    const float e0 = lane < active ? expf(lse0 - mx) : 0.f;  // the weight of split `lane`
+    float ws = e0;
+    for (int s = lane + kWave; s < active; s += kWave) ws += expf(lse[hq * S + s] - mx);
+    const float wsum = wave_sum(ws);
     float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u)
-        if (u < active) acc = fmaf(wts[u], v[u], acc);
-    for (int s = kMergeChunk; s < active; ++s) acc = fmaf(wts[s], src[(size_t)s * kHeadDim], acc);
+    for (int u = 0; u < kMergeChunk; ++u) {  // split order; split u's weight from lane u
+        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), u));
+        if (u < active) acc = fmaf(wu, v[u], acc);
+    }
+    for (int s = kMergeChunk; s < active; ++s) acc = fmaf(expf(lse[hq * S + s] - mx), src[(size_t)s * kHeadDim], acc);
     const uint16_t o = f32_to_bf16(acc / wsum);
     out[hq * kHeadDim + d] = o;
     if constexpr (QUANT) {
