@@ -491,7 +491,7 @@ template <bool PAIRED, bool EXACT>
 int launch_ksplit(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
                   int rows, hipStream_t st) {
     const int W = G / 128;
-    if (rows <= 0) rows = EXACT ? 2 : 4;
+    if (rows <= 0) rows = 4;  // measured on MI355X (K = 12288, N = 4096): 4 rows per wave group in both modes
     const dim3 grid((n_out + rows - 1) / rows);
     const auto* xp = (const uint16_t*)x;
     const auto* qp = (const uint4*)qw;
@@ -572,9 +572,12 @@ int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, v
         if (mode == MOSS_DEQUANT_UNROUNDED) return launch_ksplit<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
         return (int)hipErrorInvalidValue;
     }
-    // measured on MI355X (K = 4096): 2 rows per wave is best for the exact mode in both roles;
-    // the unrounded GEMV is as fast at 4 and the unrounded gate||up at 2
-    if (rows == 0) rows = (G <= 128) ? ((PAIRED || mode == MOSS_DEQUANT_EXACT) ? 2 : 4) : (G <= 256 ? 2 : 1);
+    // measured on MI355X (K = 4096): 2 rows per wave is best for the exact mode in both roles up
+    // to N = 12288 and 4 for the 32-head output projection (N ~ 32800); the unrounded GEMV is as
+    // fast at 4 and the unrounded gate||up at 2
+    if (rows == 0)
+        rows = (G <= 128) ? ((PAIRED || mode == MOSS_DEQUANT_EXACT) ? (!PAIRED && n_out >= 24576 ? 4 : 2) : 4)
+                          : (G <= 256 ? 2 : 1);
     if (mode == MOSS_DEQUANT_EXACT)
         return launch_gemv_mode<PAIRED, true, NORM>(x, qw, sc, zp, y, G, n_out, rows, na, st);
     if (mode == MOSS_DEQUANT_UNROUNDED)
