@@ -298,6 +298,163 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
         }
 }
 
+// Weight-stationary-in-registers 128 x 128 INT4 tile (Y^T = W X^T): the dequantized weights are
+// the MFMA's A operand, formed in the registers of the lane that feeds them, so they never pass
+// through LDS; only the activation tile does.  Wave w owns weight rows n0 + 32 w .. + 31 and
+// all 128 token columns (4 MFMA tiles of 32 x 32).  In a K step of 64 (groups g0, g0 + 1), lane
+// l takes row n0 + 32 w + (l & 31) and group g0 + (l >> 5): its 16 bytes of codes are the A
+// operands of the step's 4 MFMAs (one packed word of 8 codes each, dequantized bit-exactly),
+// and MFMA kk meets the activations x[m][32 (l >> 5) + 8 kk .. + 8] of the same lane, so both
+// operands walk K in the same order.
+// Vector-memory requests are counted per 64-byte segment an instruction touches, so every load
+// is shaped to touch few: eight consecutive threads copy one token row's 128 bytes of a step, and
+// the scales and zero points of a row come once per block of kTs steps (8 groups: 16 bytes of
+// scales, 8 zero bytes that all hold the same nibble half when the row's last 128-group chunk
+// is a multiple of 16 groups long).  Codes travel kTs steps ahead (HBM), activations two steps
+// ahead (mostly L2 hits), scales and zeros one block ahead.
+constexpr int kTs = 4;
+
+struct TBlock {
+    uint4 s;   // scales of groups 8b .. 8b + 7
+    uint2 z;   // zero bytes of those groups
+    uint32_t zsh;
+};
+
+__global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
+                                                           const uint16_t* __restrict__ sc,
+                                                           const uint8_t* __restrict__ zp, uint16_t* __restrict__ Y,
+                                                           int M, int N, int K) {
+    constexpr int BN = 128, BM = 128;
+    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BM][kLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mt = (M + BM - 1) / BM, tiles = gridDim.x;
+    int tile = blockIdx.x;
+    if (tiles % kXcds == 0) tile = (blockIdx.x % kXcds) * (tiles / kXcds) + blockIdx.x / kXcds;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+    const int G = K >> 5, steps = K / kBK;
+    // activation copy: thread t moves 16-byte chunk t % 8 of token rows t / 8 + 32 c, c < 4 (rows
+    // clamped; those outputs are not stored)
+    const int xc = tid & 7, xr = tid >> 3;
+    const uint16_t* xrow[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xrow[c] = X + (size_t)min(m0 + xr + 32 * c, M - 1) * K + 8 * xc;
+    // weights: this lane's row and group half
+    const int half = lane >> 5;
+    const size_t wrow = (size_t)min(n0 + 32 * wave + (lane & 31), N - 1);
+
+    auto load_x = [&](u32x4_t (&x)[4], int k0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) x[c] = __builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(xrow[c] + k0));
+    };
+    auto load_w = [&](uint4& w, int k0) { w = qw[wrow * G + (k0 >> 5) + half]; };
+    auto load_blk = [&](TBlock& t, int blk) {
+        const int g = 8 * blk;
+        int zb;
+        zero_loc(g, G, zb, t.zsh);
+        t.s = *reinterpret_cast<const uint4*>(sc + wrow * G + g);
+        t.z = *reinterpret_cast<const uint2*>(zp + wrow * (G >> 1) + zb);
+    };
+    auto store_x = [&](const u32x4_t (&x)[4], uint16_t (*xs)[kLds]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) *reinterpret_cast<u32x4_t*>(&xs[xr + 32 * c][8 * xc]) = x[c];
+    };
+
+    f32x16_t acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+
+    const int blocks = steps / kTs;
+    uint4 cw[kTs];
+    u32x4_t xv[2][4];
+    TBlock cur, nxt;
+    load_blk(cur, 0);
+    load_blk(nxt, min(1, blocks - 1));
+#pragma unroll
+    for (int i = 0; i < kTs; ++i) load_w(cw[i], min(i, steps - 1) * kBK);
+    load_x(xv[0], 0);
+    load_x(xv[1], min(1, steps - 1) * kBK);
+    pin();
+    store_x(xv[0], Xs[0]);
+    __syncthreads();
+    uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
+    asm volatile("" : "+v"(mask), "+v"(bias_bits));
+    for (int blk = 0; blk < blocks; ++blk) {
+        const int st = blk * kTs;
+#pragma unroll
+        for (int i = 0; i < kTs; ++i) {
+            const int s = st + i;
+            // all 16 activation operands of the step first: their LDS latency is hidden behind the
+            // dequantization below instead of being exposed before each MFMA
+            const uint16_t (*xs)[kLds] = Xs[i % 2];
+            bf16x8_t b[4][4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    b[kk][j] = *reinterpret_cast<const bf16x8_t*>(&xs[32 * j + (lane & 31)][32 * half + 8 * kk]);
+            pin();
+            // this step's weight operands (group 8 blk + 2 i + half), dequantized in registers
+            uint32_t wf[4][4];
+            {
+                const uint32_t sw = i == 0 ? cur.s.x : i == 1 ? cur.s.y : i == 2 ? cur.s.z : cur.s.w;
+                const uint32_t zw = i < 2 ? cur.z.x : cur.z.y;
+                const uint32_t s_lo = (sw >> (16 * half)) & 0xffffu, s_hi = s_lo << 16;
+                const uint32_t zq = (zw >> (8 * (2 * (i & 1) + half) + cur.zsh)) & 15u;
+                const float bias = -(128.0f + (float)zq) * bf16_bits((uint16_t)s_lo);
+                const uint32_t words[4] = {cw[i].x, cw[i].y, cw[i].z, cw[i].w};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    dequant_word_exact((words[kk] & mask) | bias_bits, ((words[kk] >> 4) & mask) | bias_bits,
+                                       ((words[kk] >> 8) & mask) | bias_bits, ((words[kk] >> 12) & mask) | bias_bits,
+                                       s_lo, s_hi, bias, wf[kk]);
+            }
+            pin();
+            // slot i of the code ring is free once dequantized: codes of step s + kTs into it
+            load_w(cw[i], min(s + kTs, steps - 1) * kBK);
+            if (i == kTs - 1) {
+                cur = nxt;
+                load_blk(nxt, min(blk + 2, blocks - 1));
+            }
+            // the next step's activations into the other buffer, which every wave finished reading
+            // before the previous barrier (after the last step this writes clamped data nobody reads);
+            // their register slot then takes step s + 2
+            store_x(xv[(i + 1) % 2], Xs[(i + 1) % 2]);
+            load_x(xv[i % 2], min(s + 2, steps - 1) * kBK);
+            pin();
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{wf[kk][0], wf[kk][1], wf[kk][2], wf[kk][3]});
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[kk][j], acc[j], 0, 0, 0);
+            }
+            __syncthreads();
+        }
+    }
+    // C[n][m] of the 32 x 32 tile (n0 + 32 wave, m0 + 32 j): lane l, element e -> n row
+    // 8 (e / 4) + 4 (l / 32) + e % 4, m column l % 32; the four e of a quad are consecutive n
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = m0 + 32 * j + (lane & 31);
+        if (m >= M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = n0 + 32 * wave + 8 * q + 4 * (lane >> 5);
+            if (n + 3 < N) {
+                uint2 o;
+                o.x = pack_bf16x2(acc[j][4 * q], acc[j][4 * q + 1]);
+                o.y = pack_bf16x2(acc[j][4 * q + 2], acc[j][4 * q + 3]);
+                *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < N) Y[(size_t)m * N + n + e] = f32_to_bf16(acc[j][4 * q + e]);
+            }
+        }
+    }
+}
+
 // y[m, n] = bf16(scale[n] * sum_z part[z, m, n]), z ascending; 4 outputs per thread (N % 4 == 0).
 __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ part, const float* __restrict__ row_scale,
                                                    uint16_t* __restrict__ Y, int MN, int N, int S) {
@@ -378,6 +535,12 @@ int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, v
     if (p.bm == 64 && p.bn == 64) launch_tile<64, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bm == 64) launch_tile<64, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bn == 64) launch_tile<128, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
+    else if (FMT == kInt4G32 && p.split == 1 && (K / kBK) % kTs == 0 && N % 4 == 0 &&
+             (K / 32) % 16 == 0 &&
+             ((K / 32) % 128) % 16 == 0 && MOSS_ALIGNED(y, 8) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8))
+        hipLaunchKernelGGL(w4g32_gemm_t_kernel, dim3((unsigned)(((M + 127) / 128) * ((N + 127) / 128))), dim3(256), 0,
+                           st, (const uint16_t*)x, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,
+                           (uint16_t*)y, M, N, K);
     else launch_tile<128, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     if (p.split > 1) {
         const int mn = M * N;

@@ -181,7 +181,9 @@ def test_gemv_rejects_bad_inputs(dev):
 @pytest.mark.parametrize("m,k,n", [(2, 64, 8), (16, 128, 64), (100, 512, 200), (128, 4096, 128), (512, 1024, 4096),
                                    (37, 4096, 32800), (512, 4096, 6144), (512, 12288, 4096),
                                    # the 128 x 128 tile at full size, with ragged M and N, and an odd step count
-                                   (512, 4096, 24576), (300, 1024, 32808), (260, 1088, 16448)])
+                                   (512, 4096, 24576), (300, 1024, 32808), (260, 1088, 16448),
+                                   # register-weight tile with a 16-group last zero-point chunk (G = 144)
+                                   (260, 4608, 12296)])
 def test_gemm_parity(dev, m, k, n):
     """MFMA GEMM with bit-exact bf16 dequantized weights: fp32 summation order is the only
     difference from the oracle's dequant-then-matmul."""
