@@ -57,21 +57,23 @@ struct StepRegs {
 // Per-thread addressing, fixed for a workgroup: the thread's activation row and weight row.
 template <int BM, int BN>
 struct StepAddr {
-    const uint16_t* x;  // X row start + this thread's column offset
+    const uint16_t* x[BM / 32];  // chunk t % 8 of activation rows t / 8 + 32 c (see step_addr)
     size_t wrow;        // weight row n (clamped)
     int half, sub;      // which 32-wide half of the step, which part of it
 };
 
 // Out-of-range rows and columns load the last valid row / column instead (addresses are clamped
 // here): rows of X and columns of W are independent in the product, and those outputs are never
-// stored.  Every thread then issues the same loads.
+// stored.  Every thread then issues the same loads.  Activations: load c moves 16-byte chunk
+// t % 8 of row t / 8 + 32 c, so the eight threads of a row cover its 128 bytes of the step and
+// an instruction touches 16 64-byte segments (memory requests are counted per segment).
 template <int BM, int BN>
 __device__ __forceinline__ StepAddr<BM, BN> step_addr(const uint16_t* __restrict__ X, int M, int N, int K, int m0,
                                                       int n0, int tid) {
-    constexpr int TPR = 256 / BM, CH = BM / 32, TPU = StepRegs<BM, BN>::TPU;
+    constexpr int CH = BM / 32, TPU = StepRegs<BM, BN>::TPU;
     StepAddr<BM, BN> a;
-    const int row = tid / TPR, part = tid % TPR;
-    a.x = X + (size_t)min(m0 + row, M - 1) * K + 8 * CH * part;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) a.x[c] = X + (size_t)min(m0 + (tid >> 3) + 32 * c, M - 1) * K + 8 * (tid & 7);
     const int unit = tid / TPU;
     a.wrow = (size_t)min(n0 + (unit >> 1), N - 1);
     a.half = unit & 1;
@@ -82,9 +84,8 @@ __device__ __forceinline__ StepAddr<BM, BN> step_addr(const uint16_t* __restrict
 template <int BM, int BN>
 __device__ __forceinline__ void load_a(StepRegs<BM, BN>& r, const StepAddr<BM, BN>& a, int k0) {
     constexpr int CH = BM / 32;
-    const uint4* p = reinterpret_cast<const uint4*>(a.x + k0);
 #pragma unroll
-    for (int c = 0; c < CH; ++c) r.x[c] = __builtin_bit_cast(u32x4_t, p[c]);
+    for (int c = 0; c < CH; ++c) r.x[c] = __builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(a.x[c] + k0));
 }
 
 template <int BM, int BN, int FMT>
@@ -140,11 +141,9 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
 
 template <int BM, int BN>
 __device__ __forceinline__ void store_a(const StepRegs<BM, BN>& r, uint16_t (*As)[kLds], int tid) {
-    constexpr int TPR = 256 / BM, CH = BM / 32;
-    const int row = tid / TPR, part = tid % TPR;
-    u32x4_t* a = reinterpret_cast<u32x4_t*>(&As[row][0]) + CH * part;
+    constexpr int CH = BM / 32;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) a[c] = r.x[c];
+    for (int c = 0; c < CH; ++c) *reinterpret_cast<u32x4_t*>(&As[(tid >> 3) + 32 * c][8 * (tid & 7)]) = r.x[c];
 }
 
 template <int BM, int BN, int FMT>
