@@ -11,6 +11,10 @@
 // epilogue (src/moss_tts/_runtime/fused_mlp.py:20-21).  The fp8 MFMA forms are not used:
 // they would round the bf16 activations to e4m3 as well.
 //
+// INT4 with more than 64 tokens takes the register-weight tile (w4g32_gemm_t_kernel): the
+// dequantized weights are the MFMA's A operand straight from the registers that dequantize them,
+// and only the activations are staged in LDS; the others take the LDS tiles below.
+//
 // Tile: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
 // (BM/2) x (BN/2), K in steps of 64 (two quantization groups).  Pipeline: two LDS buffers and
 // S register stages (stages_for); while step st is multiplied from one LDS buffer and step st + 1
@@ -319,10 +323,13 @@ struct TBlock {
     uint32_t zsh;
 };
 
+// SPLIT: gridDim.y workgroups share a tile, each summing a contiguous K range of whole blocks
+// into fp32 partials part[blockIdx.y, M, N], reduced by gemm_reduce.
+template <bool SPLIT>
 __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
                                                            const uint16_t* __restrict__ sc,
                                                            const uint8_t* __restrict__ zp, uint16_t* __restrict__ Y,
-                                                           int M, int N, int K) {
+                                                           float* __restrict__ part, int M, int N, int K) {
     constexpr int BN = 128, BM = 128;
     __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BM][kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -330,13 +337,14 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
     int tile = blockIdx.x;
     if (tiles % kXcds == 0) tile = (blockIdx.x % kXcds) * (tiles / kXcds) + blockIdx.x / kXcds;
     const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
-    const int G = K >> 5, steps = K / kBK;
+    const int G = K >> 5, steps = SPLIT ? K / kBK / gridDim.y : K / kBK;
+    const int kbase = SPLIT ? blockIdx.y * steps * kBK : 0;  // a multiple of kTs steps (8 groups)
     // activation copy: thread t moves 16-byte chunk t % 8 of token rows t / 8 + 32 c, c < 4 (rows
     // clamped; those outputs are not stored)
     const int xc = tid & 7, xr = tid >> 3;
     const uint16_t* xrow[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) xrow[c] = X + (size_t)min(m0 + xr + 32 * c, M - 1) * K + 8 * xc;
+    for (int c = 0; c < 4; ++c) xrow[c] = X + (size_t)min(m0 + xr + 32 * c, M - 1) * K + kbase + 8 * xc;
     // weights: this lane's row and group half
     const int half = lane >> 5;
     const size_t wrow = (size_t)min(n0 + 32 * wave + (lane & 31), N - 1);
@@ -345,9 +353,9 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
 #pragma unroll
         for (int c = 0; c < 4; ++c) x[c] = __builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(xrow[c] + k0));
     };
-    auto load_w = [&](uint4& w, int k0) { w = qw[wrow * G + (k0 >> 5) + half]; };
+    auto load_w = [&](uint4& w, int k0) { w = qw[wrow * G + ((kbase + k0) >> 5) + half]; };
     auto load_blk = [&](TBlock& t, int blk) {
-        const int g = 8 * blk;
+        const int g = (kbase >> 5) + 8 * blk;
         int zb;
         zero_loc(g, G, zb, t.zsh);
         t.s = *reinterpret_cast<const uint4*>(sc + wrow * G + g);
@@ -433,6 +441,7 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
     }
     // C[n][m] of the 32 x 32 tile (n0 + 32 wave, m0 + 32 j): lane l, element e -> n row
     // 8 (e / 4) + 4 (l / 32) + e % 4, m column l % 32; the four e of a quad are consecutive n
+    // (N % 4 == 0: a quad is all in range or all out)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int m = m0 + 32 * j + (lane & 31);
@@ -440,15 +449,15 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int n = n0 + 32 * wave + 8 * q + 4 * (lane >> 5);
-            if (n + 3 < N) {
+            if (n >= N) continue;
+            if constexpr (SPLIT) {
+                *reinterpret_cast<float4*>(part + ((size_t)blockIdx.y * M + m) * N + n) =
+                    make_float4(acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]);
+            } else {
                 uint2 o;
                 o.x = pack_bf16x2(acc[j][4 * q], acc[j][4 * q + 1]);
                 o.y = pack_bf16x2(acc[j][4 * q + 2], acc[j][4 * q + 3]);
                 *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (n + e < N) Y[(size_t)m * N + n + e] = f32_to_bf16(acc[j][4 * q + e]);
             }
         }
     }
@@ -478,14 +487,35 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ par
 
 struct Plan {
     int bm, bn, split;
+    bool reg;  // the register-weight 128 x 128 INT4 tile
 };
 
-// Tile shape and K split: 64-row tiles for M <= 64; 128-wide N tiles when they already give
-// >= 256 workgroups; a K split (2..8) for M <= 256 while the tiles give fewer than 256
-// workgroups, and a split of 2 up to M = 1024 when the tiles give at most 256 (the fp32
-// partials cost 8 M N bytes per split).
-Plan plan_gemm(int M, int K, int N) {
+// Shapes the register-weight tile takes: more than 64 tokens (it always computes 128), whole
+// blocks of kTs steps, and the 8 zero bytes of every block on one nibble side of their 128-group
+// chunk (the last chunk a multiple of 16 groups long), 16-byte scale rows.
+bool reg_tile_shape(int M, int K, int N) {
+    const int G = K / 32;
+    return M > 64 && N % 4 == 0 && (K / kBK) % kTs == 0 && G % 16 == 0 && (G % 128) % 16 == 0;
+}
+
+// INT4 shapes the register-weight tile takes: a K split (2..8, whole blocks, >= 2 blocks each)
+// while the doubled workgroup count still fits two per CU.  Otherwise the LDS tiles: 64-row
+// tiles for M <= 64; 128-wide N tiles when they already give >= 256 workgroups; a K split
+// (2..8) for M <= 256 while the tiles give fewer than 256 workgroups, and a split of 2 up to
+// M = 1024 when the tiles give at most 256 (the fp32 partials cost 8 M N bytes per split).
+Plan plan_gemm(int M, int K, int N, bool int4) {
     Plan p;
+    p.reg = int4 && reg_tile_shape(M, K, N);
+    if (p.reg) {
+        p.bm = p.bn = 128;
+        p.split = 1;
+        const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+        const int steps = K / kBK;
+        while (p.split < 8 && tiles * p.split * 2 <= 512 && steps % (2 * p.split * kTs) == 0 &&
+               steps / (2 * p.split) >= 2 * kTs)
+            p.split *= 2;
+        return p;
+    }
     p.bm = M <= 64 ? 64 : 128;
     const long mt = (M + p.bm - 1) / p.bm;
     p.bn = mt * ((N + 127) / 128) >= 256 ? 128 : 64;
@@ -527,19 +557,26 @@ void launch_tile(const Plan& p, const void* x, const void* qw, const void* sc, c
 template <int FMT>
 int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K, int N,
                 const float* row_scale, void* ws, long long ws_bytes, hipStream_t st) {
-    Plan p = plan_gemm(M, K, N);
+    Plan p = plan_gemm(M, K, N, FMT == kInt4G32);
+    // the register-weight tile stores 4 outputs (8 bytes) at a time and loads scales and zero
+    // bytes 16 and 8 at a time
+    if (p.reg && !(MOSS_ALIGNED(y, 8) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8))) p = plan_gemm(M, K, N, false);
     if (p.split > 1 &&
         (!ws || ws_bytes < (long long)p.split * M * N * 4 || !MOSS_ALIGNED(ws, 16) || !MOSS_ALIGNED(y, 8)))
         p.split = 1;
-    if (p.bm == 64 && p.bn == 64) launch_tile<64, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
+    if (p.reg) {
+        const dim3 grid((unsigned)(((M + 127) / 128) * ((N + 127) / 128)), (unsigned)p.split);
+        if (p.split > 1)
+            hipLaunchKernelGGL(w4g32_gemm_t_kernel<true>, grid, dim3(256), 0, st, (const uint16_t*)x,
+                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws,
+                               M, N, K);
+        else
+            hipLaunchKernelGGL(w4g32_gemm_t_kernel<false>, grid, dim3(256), 0, st, (const uint16_t*)x,
+                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws,
+                               M, N, K);
+    } else if (p.bm == 64 && p.bn == 64) launch_tile<64, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bm == 64) launch_tile<64, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bn == 64) launch_tile<128, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
-    else if (FMT == kInt4G32 && p.split == 1 && (K / kBK) % kTs == 0 && N % 4 == 0 &&
-             (K / 32) % 16 == 0 &&
-             ((K / 32) % 128) % 16 == 0 && MOSS_ALIGNED(y, 8) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8))
-        hipLaunchKernelGGL(w4g32_gemm_t_kernel, dim3((unsigned)(((M + 127) / 128) * ((N + 127) / 128))), dim3(256), 0,
-                           st, (const uint16_t*)x, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,
-                           (uint16_t*)y, M, N, K);
     else launch_tile<128, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     if (p.split > 1) {
         const int mn = M * N;
@@ -557,9 +594,14 @@ int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* 
     return launch_gemm<kFp8E4M3>(x, w, nullptr, nullptr, y, M, K, N, row_scale, ws, ws_bytes, stream);
 }
 
+// One workspace serves both formats: the larger of the two plans' partial sums.
 long long gemm_workspace_bytes(int M, int K, int N) {
-    const Plan p = plan_gemm(M, K, N);
-    return p.split > 1 ? (long long)p.split * M * N * 4 : 0;
+    long long bytes = 0;
+    for (const bool int4 : {true, false}) {
+        const Plan p = plan_gemm(M, K, N, int4);
+        if (p.split > 1) bytes = std::max(bytes, (long long)p.split * M * N * 4);
+    }
+    return bytes;
 }
 
 }  // namespace moss

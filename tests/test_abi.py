@@ -60,7 +60,9 @@ def test_host_only_entry_points(lib):
     assert lib.moss_abi_version() == 1
     ws = lib.moss_gemm_workspace_bytes(64, 4096, 4096)                            # M=64: K split over workgroups
     assert ws > 0 and ws % (64 * 4096 * 4) == 0 and ws // (64 * 4096 * 4) in (2, 4, 8)
-    assert lib.moss_gemm_workspace_bytes(512, 4096, 6144) == 0                    # prefill tiles fill the GPU
+    assert lib.moss_gemm_workspace_bytes(512, 4096, 24576) == 0                   # prefill tiles fill the GPU
+    assert lib.moss_gemm_workspace_bytes(512, 4096, 6144) == 2 * 512 * 6144 * 4   # 192 INT4 tiles: K split in 2
+    assert lib.moss_gemm_workspace_bytes(512, 12288, 4096) == 4 * 512 * 4096 * 4  # 128 INT4 tiles: K split in 4
     assert lib.moss_error_string(0)
     assert lib.moss_decode_attention_splits(2048) == 32
     assert lib.moss_decode_attention_splits(128) == 2
