@@ -151,9 +151,9 @@ int moss_w4a8_norm_gateup_silu(const void *x, const void *res, const void *norm_
 
 /* ------------------------------------------------------------- prefill GEMM */
 /* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);
- * weights are dequantized bit-exactly (bf16_rne((q-z)*s)) into LDS and multiplied with
- * v_mfma_f32_32x32x16_bf16, fp32 accumulate.  When the output tiles alone cannot fill the GPU
- * (small M) the K dimension is split over workgroups: that needs a caller-owned fp32 workspace
+ * weights are dequantized bit-exactly (bf16_rne((q-z)*s)), in the registers that feed
+ * v_mfma_f32_32x32x16_bf16 (M > 64) or into LDS, fp32 accumulate.  When the output tiles alone
+ * cannot fill the GPU the K dimension is split over workgroups: that needs a caller-owned fp32 workspace
  * of moss_gemm_workspace_bytes(M, K, N) bytes (16-byte aligned; y 8-byte aligned); with a
  * NULL or smaller workspace the GEMM runs unsplit.  Partial sums are added in a fixed order.
  * The reference runs bf16 F.linear here (src/moss_tts/_runtime/llm.py:29,84,130); its INT4
