@@ -286,9 +286,8 @@ def main() -> int:
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures the single-GPU path only: every box in this build has one MI355X, "
-              "and the INT4-G32 decode path runs on one GPU (sharding is described, not run). "
-              "Use --gpus 1.", file=sys.stderr)
+        print("bench.py measures the single-GPU path only: the INT4-G32 decode path runs on one "
+              "MI355X (how it would shard is described, not run). Use --gpus 1.", file=sys.stderr)
         return 2
     if args.steps <= 0 or args.warmup < 0 or args.copies <= 0:
         print("steps must be positive, warmup non-negative", file=sys.stderr)

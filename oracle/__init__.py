@@ -1,8 +1,8 @@
 """CPU oracle for the INT4-G32 quantized-linear path (TEST INFRASTRUCTURE ONLY).
 
 This package restates, on the CPU, the reference algorithms that the HIP kernels in
-``moss-tts-optimized_amd/csrc`` must reproduce.  It is the checker, never the thing
-measured or shipped: only ``tests/``, ``__graft_entry__.smoke()`` and the
+``moss-tts-optimized_amd/csrc`` must reproduce.  It is what the kernels are
+checked against, never the thing measured or shipped: only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it.  Product code never imports it and
 has no CPU fallback.
 
