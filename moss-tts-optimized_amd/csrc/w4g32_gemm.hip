@@ -301,20 +301,22 @@ __global__ __launch_bounds__(256) void w4g32_gemm_kernel(const uint16_t* __restr
         }
 }
 
-// Weight-stationary-in-registers 128 x 128 INT4 tile (Y^T = W X^T): the dequantized weights are
-// the MFMA's A operand, formed in the registers of the lane that feeds them, so they never pass
-// through LDS; only the activation tile does.  Wave w owns weight rows n0 + 32 w .. + 31 and
-// all 128 token columns (4 MFMA tiles of 32 x 32).  In a K step of 64 (groups g0, g0 + 1), lane
-// l takes row n0 + 32 w + (l & 31) and group g0 + (l >> 5): its 16 bytes of codes are the A
-// operands of the step's 4 MFMAs (one packed word of 8 codes each, dequantized bit-exactly),
+// Weight-stationary-in-registers INT4 tile (Y^T = W X^T): the dequantized weights are the MFMA's
+// A operand, formed in the registers of the lane that feeds them, so they never pass through
+// LDS; only the activation tile does.  A workgroup covers 128 weight rows and
+// BM = 32 JT tokens: wave w owns weight rows n0 + 32 w .. + 31 and every token (JT MFMA tiles
+// of 32 x 32).  In a K step of 64, lane l takes row n0 + 32 w + (l & 31) and the 32-wide half
+// (l >> 5) of the step: its 32 weights are the A operands of the step's 4 MFMAs (8 per MFMA),
 // and MFMA kk meets the activations x[m][32 (l >> 5) + 8 kk .. + 8] of the same lane, so both
-// operands walk K in the same order.
+// operands walk K in the same order: one group of 32 codes (16 bytes) per lane and step,
+// dequantized bit-exactly.  (FP8 weights measured slower in this tile than in the LDS tiles at
+// M <= 128 and take those.)
 // Vector-memory requests are counted per 64-byte segment an instruction touches, so every load
 // is shaped to touch few: eight consecutive threads copy one token row's 128 bytes of a step, and
-// the scales and zero points of a row come once per block of kTs steps (8 groups: 16 bytes of
-// scales, 8 zero bytes that all hold the same nibble half when the row's last 128-group chunk
-// is a multiple of 16 groups long).  Codes travel kTs steps ahead (HBM), activations two steps
-// ahead (mostly L2 hits), scales and zeros one block ahead.
+// the scales and zero points of a row come once per block of kTs steps (8 groups: 16 bytes
+// of scales, 8 zero bytes that all hold the same nibble half when the row's last 128-group
+// chunk is a multiple of 16 groups long).  Weights travel kTs steps ahead (HBM), activations
+// two steps ahead (mostly L2 hits), scales and zeros one block ahead.
 constexpr int kTs = 4;
 
 struct TBlock {
@@ -325,12 +327,12 @@ struct TBlock {
 
 // SPLIT: gridDim.y workgroups share a tile, each summing a contiguous K range of whole blocks
 // into fp32 partials part[blockIdx.y, M, N], reduced by gemm_reduce.
-template <bool SPLIT>
+template <int JT, bool SPLIT>
 __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __restrict__ X, const uint4* __restrict__ qw,
                                                            const uint16_t* __restrict__ sc,
                                                            const uint8_t* __restrict__ zp, uint16_t* __restrict__ Y,
                                                            float* __restrict__ part, int M, int N, int K) {
-    constexpr int BN = 128, BM = 128;
+    constexpr int BN = 128, BM = 32 * JT;
     __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BM][kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int mt = (M + BM - 1) / BM, tiles = gridDim.x;
@@ -339,19 +341,19 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
     const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
     const int G = K >> 5, steps = SPLIT ? K / kBK / gridDim.y : K / kBK;
     const int kbase = SPLIT ? blockIdx.y * steps * kBK : 0;  // a multiple of kTs steps (8 groups)
-    // activation copy: thread t moves 16-byte chunk t % 8 of token rows t / 8 + 32 c, c < 4 (rows
-    // clamped; those outputs are not stored)
+    // activation copy: thread t moves 16-byte chunk t % 8 of token rows t / 8 + 32 c, c < JT
+    // (rows clamped; those outputs are not stored)
     const int xc = tid & 7, xr = tid >> 3;
-    const uint16_t* xrow[4];
+    const uint16_t* xrow[JT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) xrow[c] = X + (size_t)min(m0 + xr + 32 * c, M - 1) * K + kbase + 8 * xc;
-    // weights: this lane's row and group half
+    for (int c = 0; c < JT; ++c) xrow[c] = X + (size_t)min(m0 + xr + 32 * c, M - 1) * K + kbase + 8 * xc;
+    // weights: this lane's row and 32-wide half of the step
     const int half = lane >> 5;
     const size_t wrow = (size_t)min(n0 + 32 * wave + (lane & 31), N - 1);
 
-    auto load_x = [&](u32x4_t (&x)[4], int k0) {
+    auto load_x = [&](u32x4_t (&x)[JT], int k0) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) x[c] = __builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(xrow[c] + k0));
+        for (int c = 0; c < JT; ++c) x[c] = __builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(xrow[c] + k0));
     };
     auto load_w = [&](uint4& w, int k0) { w = qw[wrow * G + ((kbase + k0) >> 5) + half]; };
     auto load_blk = [&](TBlock& t, int blk) {
@@ -361,20 +363,20 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
         t.s = *reinterpret_cast<const uint4*>(sc + wrow * G + g);
         t.z = *reinterpret_cast<const uint2*>(zp + wrow * (G >> 1) + zb);
     };
-    auto store_x = [&](const u32x4_t (&x)[4], uint16_t (*xs)[kLds]) {
+    auto store_x = [&](const u32x4_t (&x)[JT], uint16_t (*xs)[kLds]) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) *reinterpret_cast<u32x4_t*>(&xs[xr + 32 * c][8 * xc]) = x[c];
+        for (int c = 0; c < JT; ++c) *reinterpret_cast<u32x4_t*>(&xs[xr + 32 * c][8 * xc]) = x[c];
     };
 
-    f32x16_t acc[4];
+    f32x16_t acc[JT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < JT; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
 
     const int blocks = steps / kTs;
     uint4 cw[kTs];
-    u32x4_t xv[2][4];
+    u32x4_t xv[2][JT];
     TBlock cur, nxt;
     load_blk(cur, 0);
     load_blk(nxt, min(1, blocks - 1));
@@ -392,17 +394,17 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
 #pragma unroll
         for (int i = 0; i < kTs; ++i) {
             const int s = st + i;
-            // all 16 activation operands of the step first: their LDS latency is hidden behind the
+            // all activation operands of the step first: their LDS latency is hidden behind the
             // dequantization below instead of being exposed before each MFMA
             const uint16_t (*xs)[kLds] = Xs[i % 2];
-            bf16x8_t b[4][4];
+            bf16x8_t b[4][JT];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < JT; ++j)
                     b[kk][j] = *reinterpret_cast<const bf16x8_t*>(&xs[32 * j + (lane & 31)][32 * half + 8 * kk]);
             pin();
-            // this step's weight operands (group 8 blk + 2 i + half), dequantized in registers
+            // this step's A operands (group 8 blk + 2 i + half of this lane's row), in registers
             uint32_t wf[4][4];
             {
                 const uint32_t sw = i == 0 ? cur.s.x : i == 1 ? cur.s.y : i == 2 ? cur.s.z : cur.s.w;
@@ -434,7 +436,7 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
             for (int kk = 0; kk < 4; ++kk) {
                 const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{wf[kk][0], wf[kk][1], wf[kk][2], wf[kk][3]});
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[kk][j], acc[j], 0, 0, 0);
+                for (int j = 0; j < JT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[kk][j], acc[j], 0, 0, 0);
             }
             __syncthreads();
         }
@@ -443,20 +445,20 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
     // 8 (e / 4) + 4 (l / 32) + e % 4, m column l % 32; the four e of a quad are consecutive n
     // (N % 4 == 0: a quad is all in range or all out)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < JT; ++j) {
         const int m = m0 + 32 * j + (lane & 31);
         if (m >= M) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int n = n0 + 32 * wave + 8 * q + 4 * (lane >> 5);
             if (n >= N) continue;
+            const float v0 = acc[j][4 * q], v1 = acc[j][4 * q + 1], v2 = acc[j][4 * q + 2], v3 = acc[j][4 * q + 3];
             if constexpr (SPLIT) {
-                *reinterpret_cast<float4*>(part + ((size_t)blockIdx.y * M + m) * N + n) =
-                    make_float4(acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]);
+                *reinterpret_cast<float4*>(part + ((size_t)blockIdx.y * M + m) * N + n) = make_float4(v0, v1, v2, v3);
             } else {
                 uint2 o;
-                o.x = pack_bf16x2(acc[j][4 * q], acc[j][4 * q + 1]);
-                o.y = pack_bf16x2(acc[j][4 * q + 2], acc[j][4 * q + 3]);
+                o.x = pack_bf16x2(v0, v1);
+                o.y = pack_bf16x2(v2, v3);
                 *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
             }
         }
@@ -490,32 +492,45 @@ struct Plan {
     bool reg;  // the register-weight 128 x 128 INT4 tile
 };
 
-// Shapes the register-weight tile takes: more than 64 tokens (it always computes 128), whole
-// blocks of kTs steps, and the 8 zero bytes of every block on one nibble side of their 128-group
-// chunk (the last chunk a multiple of 16 groups long), 16-byte scale rows.
-bool reg_tile_shape(int M, int K, int N) {
+// Shapes the register-weight tile takes: whole blocks of kTs steps, 4-output stores, and for
+// INT4 the 8 zero bytes of every block on one nibble side of their 128-group chunk (the last
+// chunk a multiple of 16 groups long) and 16-byte scale rows.
+bool reg_tile_shape(int K, int N, bool int4) {
     const int G = K / 32;
-    return M > 64 && N % 4 == 0 && (K / kBK) % kTs == 0 && G % 16 == 0 && (G % 128) % 16 == 0;
+    return int4 && N % 4 == 0 && (K / kBK) % kTs == 0 && G % 16 == 0 && (G % 128) % 16 == 0;
 }
 
-// INT4 shapes the register-weight tile takes: a K split (2..8, whole blocks, >= 2 blocks each)
-// while the doubled workgroup count still fits two per CU.  Otherwise the LDS tiles: 64-row
-// tiles for M <= 64; 128-wide N tiles when they already give >= 256 workgroups; a K split
-// (2..8) for M <= 256 while the tiles give fewer than 256 workgroups, and a split of 2 up to
-// M = 1024 when the tiles give at most 256 (the fp32 partials cost 8 M N bytes per split).
+// INT4: the register-weight tile, 32, 64 or 128 tokens deep.  M > 64 (MFMA-bound): split K (2..8,
+// >= 2 blocks each) while the doubled workgroup count still fits two per CU.  M <= 64 (bound by
+// the weight stream): split while the workgroups fit two per CU and the fp32 partials (written
+// and read back once) stay below half the weight bytes.  Shapes it does not take use the LDS
+// tiles: 64-row tiles for M <= 64; 128-wide N tiles when they already give >= 256 workgroups; a
+// K split (2..8) for M <= 256 while the tiles give fewer than 256 workgroups, and a split of 2
+// up to M = 1024 when the tiles give at most 256 (the fp32 partials cost 8 M N bytes per split).
+Plan plan_lds(int M, int K, int N);
+
 Plan plan_gemm(int M, int K, int N, bool int4) {
+    if (!reg_tile_shape(K, N, int4)) return plan_lds(M, K, N);
     Plan p;
-    p.reg = int4 && reg_tile_shape(M, K, N);
-    if (p.reg) {
-        p.bm = p.bn = 128;
+    p.reg = true;
+    {
+        p.bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+        p.bn = 128;
         p.split = 1;
-        const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+        const long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + 127) / 128);
         const int steps = K / kBK;
-        while (p.split < 8 && tiles * p.split * 2 <= 512 && steps % (2 * p.split * kTs) == 0 &&
-               steps / (2 * p.split) >= 2 * kTs)
+        const double wbytes = (double)N * K * 0.5625;  // codes, scales, zero points
+        while (p.split < 16 && tiles * p.split * 2 <= 512 && steps % (2 * p.split * kTs) == 0 &&
+               (M <= 64 ? 2.0 * p.split * M * N * 4 <= 0.5 * wbytes
+                        : (p.split < 8 && steps / (2 * p.split) >= 2 * kTs)))
             p.split *= 2;
         return p;
     }
+}
+
+Plan plan_lds(int M, int K, int N) {
+    Plan p;
+    p.reg = false;
     p.bm = M <= 64 ? 64 : 128;
     const long mt = (M + p.bm - 1) / p.bm;
     p.bn = mt * ((N + 127) / 128) >= 256 ? 128 : 64;
@@ -554,26 +569,33 @@ void launch_tile(const Plan& p, const void* x, const void* qw, const void* sc, c
         launch_tile2<BM, BN, FMT, true>(p, x, qw, sc, zp, y, part, M, K, N, row_scale, st);
 }
 
+template <int JT>
+void launch_reg(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* ws,
+                int M, int K, int N, hipStream_t st) {
+    const dim3 grid((unsigned)(((M + 32 * JT - 1) / (32 * JT)) * ((N + 127) / 128)), (unsigned)p.split);
+    if (p.split > 1)
+        hipLaunchKernelGGL((w4g32_gemm_t_kernel<JT, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                           (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
+    else
+        hipLaunchKernelGGL((w4g32_gemm_t_kernel<JT, false>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                           (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
+}
+
 template <int FMT>
 int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K, int N,
                 const float* row_scale, void* ws, long long ws_bytes, hipStream_t st) {
     Plan p = plan_gemm(M, K, N, FMT == kInt4G32);
     // the register-weight tile stores 4 outputs (8 bytes) at a time and loads scales and zero
     // bytes 16 and 8 at a time
-    if (p.reg && !(MOSS_ALIGNED(y, 8) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8))) p = plan_gemm(M, K, N, false);
+    if (p.reg && !(MOSS_ALIGNED(y, 8) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8)))
+        p = plan_lds(M, K, N);
     if (p.split > 1 &&
         (!ws || ws_bytes < (long long)p.split * M * N * 4 || !MOSS_ALIGNED(ws, 16) || !MOSS_ALIGNED(y, 8)))
         p.split = 1;
     if (p.reg) {
-        const dim3 grid((unsigned)(((M + 127) / 128) * ((N + 127) / 128)), (unsigned)p.split);
-        if (p.split > 1)
-            hipLaunchKernelGGL(w4g32_gemm_t_kernel<true>, grid, dim3(256), 0, st, (const uint16_t*)x,
-                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws,
-                               M, N, K);
-        else
-            hipLaunchKernelGGL(w4g32_gemm_t_kernel<false>, grid, dim3(256), 0, st, (const uint16_t*)x,
-                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws,
-                               M, N, K);
+        if (p.bm == 32) launch_reg<1>(p, x, qw, sc, zp, y, ws, M, K, N, st);
+        else if (p.bm == 64) launch_reg<2>(p, x, qw, sc, zp, y, ws, M, K, N, st);
+        else launch_reg<4>(p, x, qw, sc, zp, y, ws, M, K, N, st);
     } else if (p.bm == 64 && p.bn == 64) launch_tile<64, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bm == 64) launch_tile<64, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bn == 64) launch_tile<128, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
@@ -594,13 +616,11 @@ int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* 
     return launch_gemm<kFp8E4M3>(x, w, nullptr, nullptr, y, M, K, N, row_scale, ws, ws_bytes, stream);
 }
 
-// One workspace serves both formats: the larger of the two plans' partial sums.
+// One workspace serves both formats and the LDS-tile fallback: the largest plan's partial sums.
 long long gemm_workspace_bytes(int M, int K, int N) {
     long long bytes = 0;
-    for (const bool int4 : {true, false}) {
-        const Plan p = plan_gemm(M, K, N, int4);
+    for (const Plan& p : {plan_gemm(M, K, N, true), plan_gemm(M, K, N, false), plan_lds(M, K, N)})
         if (p.split > 1) bytes = std::max(bytes, (long long)p.split * M * N * 4);
-    }
     return bytes;
 }
 

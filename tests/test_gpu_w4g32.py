@@ -183,7 +183,9 @@ def test_gemv_rejects_bad_inputs(dev):
                                    # the 128 x 128 tile at full size, with ragged M and N, and an odd step count
                                    (512, 4096, 24576), (300, 1024, 32808), (260, 1088, 16448),
                                    # register-weight tile with a 16-group last zero-point chunk (G = 144)
-                                   (260, 4608, 12296)])
+                                   (260, 4608, 12296),
+                                   # 32- and 64-token register tiles with a K split, ragged N
+                                   (5, 1024, 1000), (16, 4096, 4096), (48, 4608, 2056)])
 def test_gemm_parity(dev, m, k, n):
     """MFMA GEMM with bit-exact bf16 dequantized weights: fp32 summation order is the only
     difference from the oracle's dequant-then-matmul."""
