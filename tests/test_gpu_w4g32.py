@@ -203,6 +203,42 @@ def test_gemm_parity(dev, m, k, n):
     _assert_rne_or_adjacent(y, ref, abs_sum, k, f"gemm M={m} K={k} N={n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(512, 4096, 6144), (48, 4096, 2056)])
+def test_gemm_fallbacks_match(dev, m, k, n):
+    """The C-ABI's fallbacks give the same products: without a workspace the planned K split is
+    dropped (one pass over K), and scales or zero points that are not 16 / 8-byte aligned send the
+    register-weight tile's shapes to the LDS tiles.  Against the oracle at the GEMM tolerance."""
+    from moss_tts._runtime import native
+
+    print(f"gemm fallbacks M={m} K={k} N={n}", flush=True)
+    q, z, s = _case(n, k, 700 + m)
+    pw = _packed(q, z, s, dev)
+    x = torch.randn((m, k), generator=torch.Generator().manual_seed(9)).bfloat16()
+    xd = x.to(dev)
+    ref = o.linear(x, o.dequantize(q, z, s))
+    assert native.lib().moss_gemm_workspace_bytes(m, k, n) > 0  # these shapes plan a K split
+
+    def run(sc, zp, ws, wb):
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        native.call("moss_w4g32_gemm", native.ptr(xd), native.ptr(pw.qw), native.ptr(sc), native.ptr(zp),
+                    native.ptr(y), m, k, n, ws, wb, native.stream_of(xd))
+        torch.cuda.synchronize()
+        return y
+
+    # no workspace: K is not split
+    _assert_close(run(pw.scales, pw.zeros, None, 0), ref, f"gemm M={m} no workspace")
+    # scales at +2 bytes and zero points at +1 byte from an aligned base
+    sc_buf = torch.empty(pw.scales.numel() + 8, dtype=torch.bfloat16, device=dev)
+    zp_buf = torch.empty(pw.zeros.numel() + 16, dtype=torch.uint8, device=dev)
+    sc_off = sc_buf[1:1 + pw.scales.numel()].view(pw.scales.shape)
+    zp_off = zp_buf[1:1 + pw.zeros.numel()].view(pw.zeros.shape)
+    sc_off.copy_(pw.scales)
+    zp_off.copy_(pw.zeros)
+    assert sc_off.data_ptr() % 16 != 0 and zp_off.data_ptr() % 8 != 0
+    wp, wb, _keep = native.gemm_workspace(m, k, n, dev)
+    _assert_close(run(sc_off, zp_off, wp, wb), ref, f"gemm M={m} misaligned scales")
+
+
 def test_gemm_rows_match_gemv(dev):
     """Row r of the GEMM equals the exact-dequant GEMV of x[r] up to fp32 summation order."""
     from moss_tts._runtime import w4g32
