@@ -412,9 +412,12 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
 
 // ---------------------------------------------------------------------------------------
 // Entry kernels: one name per (role, dequant mode), so profiles tell them apart.
+// The plain GEMV at up to 2 rows per wave fits 6 waves per SIMD (80 VGPRs), so a K = 4096,
+// N = 12288 launch (1536 workgroups) runs in one round on 256 CUs instead of 1.2.
+#define MOSS_ROWS_WAVES(PAIRED, NORM, R) ((!(PAIRED) && (NORM) == 0 && (R) <= 2) ? 6 : 1)
 #define MOSS_ROWS_ENTRY(NAME, PAIRED, EXACT, NORM)                                                           \
     template <int KG, int R, bool FULL>                                                                          \
-    __global__ __launch_bounds__(256) void NAME(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,     \
+    __global__ __launch_bounds__(256, MOSS_ROWS_WAVES(PAIRED, NORM, R)) void NAME(const uint16_t* __restrict__ x, const uint4* __restrict__ qw,     \
                                                 const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp, \
                                                 uint16_t* __restrict__ y, int G, int n_out, NormArgs na) {      \
         gemv_rows<KG, R, PAIRED, FULL, EXACT, NORM>(x, qw, sc, zp, y, G, n_out, na);                             \
