@@ -4,18 +4,19 @@
 // INT4: the reference keeps bf16 weights for prefill (src/moss_tts/_runtime/llm.py:29,84,130);
 // its dequant-then-matmul (src/moss_tts/calibration.py:185-188) is the contract here.  Every
 // weight is dequantized bit-exactly, bf16_rne((q - z) * s) as in
-// src/moss_tts/_runtime/calibrated_quant.py:41-42, into LDS and then multiplied on the
-// matrix cores (v_mfma_f32_32x32x16_bf16).
+// src/moss_tts/_runtime/calibrated_quant.py:41-42, and then multiplied on the matrix cores
+// (v_mfma_f32_32x32x16_bf16).
 // FP8: every e4m3 value is a bf16 value, so the B-tile producer converts exactly
 // (v_cvt_scalef32_pk_bf16_fp8, scale 1) and the row scale multiplies the fp32 sum in the
 // epilogue (src/moss_tts/_runtime/fused_mlp.py:20-21).  The fp8 MFMA forms are not used:
 // they would round the bf16 activations to e4m3 as well.
 //
-// INT4 with more than 64 tokens takes the register-weight tile (w4g32_gemm_t_kernel): the
-// dequantized weights are the MFMA's A operand straight from the registers that dequantize them,
-// and only the activations are staged in LDS; the others take the LDS tiles below.
+// INT4 takes the register-weight tile (w4g32_gemm_t_kernel) wherever its shape conditions hold
+// (reg_tile_shape): the dequantized weights are the MFMA's A operand straight from the
+// registers that dequantize them, and only the activations are staged in LDS.  FP8, other INT4
+// shapes and misaligned scale or zero-point pointers take the LDS tiles:
 //
-// Tile: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
+// LDS tiles: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
 // (BM/2) x (BN/2), K in steps of 64 (two quantization groups).  Pipeline: two LDS buffers and
 // S register stages (stages_for); while step st is multiplied from one LDS buffer and step st + 1
 // is converted into the other, the global loads of step st + S are issued, so every load has
