@@ -204,6 +204,12 @@ def prefill_bench(torch, dev):
                                                "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
         _log(f"[bench] prefill GEMM M=512 {name}: {sec * 1e6:.1f} us, {tf:.0f} TFLOP/s")
         del pw
+    # the four projections of one layer, times the 36 layers (attention and norms not included)
+    us = sum(v["us_per_call"] for v in out.values())
+    flop = 2 * 512 * (HIDDEN * 6144 + HIDDEN * HIDDEN + HIDDEN * 2 * INTER + INTER * HIDDEN)
+    out["projections_36_layers"] = {"ms": round(36 * us / 1e3, 3), "TFLOP/s": round(flop / us / 1e6, 1),
+                                    "frac_of_mfma_bf16_peak": round(flop / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    _log(f"[bench] prefill projections M=512, 36 layers: {36 * us / 1e3:.2f} ms, {flop / us / 1e6:.0f} TFLOP/s")
     return out
 
 
