@@ -98,6 +98,7 @@ def test_quantize_minmax_bitexact(dev, k, n):
 GEMV_SHAPES = [
     (64, 8), (128, 37), (512, 1000), (1536, 768), (2048, 64), (4096, 4096), (4096, 12288),
     (6144, 130), (12288, 4096), (16384, 72),
+    (4096, 32802),  # the heads projection (32 x 1025 + 2 rows): four rows per wave in auto mode
 ]
 
 
@@ -185,7 +186,9 @@ def test_gemv_rejects_bad_inputs(dev):
                                    # register-weight tile with a 16-group last zero-point chunk (G = 144)
                                    (260, 4608, 12296),
                                    # 32- and 64-token register tiles with a K split, ragged N
-                                   (5, 1024, 1000), (16, 4096, 4096), (48, 4608, 2056)])
+                                   (5, 1024, 1000), (16, 4096, 4096), (48, 4608, 2056),
+                                   # N % 4 != 0: the LDS tiles take shapes the register tile would
+                                   (40, 4096, 1001), (130, 4096, 258)])
 def test_gemm_parity(dev, m, k, n):
     """MFMA GEMM with bit-exact bf16 dequantized weights: fp32 summation order is the only
     difference from the oracle's dequant-then-matmul."""
