@@ -206,18 +206,6 @@ struct MergeQuant {
     int* __restrict__ qsum;
 };
 
-__device__ __forceinline__ float half_wave_max(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 32));
-    return v;
-}
-
-__device__ __forceinline__ int half_wave_sum(int v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 32);
-    return v;
-}
-
 template <bool QUANT>
 __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict__ part,
                                                          const float* __restrict__ lse,

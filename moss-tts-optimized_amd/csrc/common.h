@@ -125,6 +125,19 @@ __device__ __forceinline__ int quantize8_dot4(const float* v, float inv, uint32_
 // Byte offset, within its 8-value block, of value t in dot4 order.
 __device__ __forceinline__ int dot4_slot(int t) { return ((t & 3) << 1) | (t >> 2); }
 
+// Max / sum over each 32-lane half of a wave (a group of 32 values, one per lane).
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 32));
+    return v;
+}
+
+__device__ __forceinline__ int half_wave_sum(int v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 32);
+    return v;
+}
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                            __builtin_bit_cast(bf16x2_t, b), c, false);

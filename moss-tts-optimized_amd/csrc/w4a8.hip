@@ -25,38 +25,26 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// One thread per group of 32: reads 64 bytes of bf16, writes 32 int8 in dot4 order, the
-// group scale and the group's code sum (for the zero-point term).
-__global__ __launch_bounds__(256) void int8_quantize_g32(const uint16_t* __restrict__ x, uint2* __restrict__ qx,
+// One 32-lane half-wave per group of 32 (one value per lane): the group's max |x| and code
+// sum are half-wave reductions, so the chain per value is short and a 12288-wide row spreads
+// over 48 workgroups.  Writes the 32 int8 codes in dot4 order (value t of the group at byte
+// 8 (t / 8) + dot4_slot(t % 8)), the group scale and the group's code sum (for the zero-point
+// term).  Lanes past the last group load a clamped value and store nothing.
+__global__ __launch_bounds__(256) void int8_quantize_g32(const uint16_t* __restrict__ x, int8_t* __restrict__ qx,
                                                          float* __restrict__ sx, int* __restrict__ qsum, int G) {
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= G) return;
-    const uint4* p = reinterpret_cast<const uint4*>(x + 32 * g);
-    float v[32];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint4 t = p[c];
-        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[8 * c + 2 * e] = bf16_lo(w[e]);
-            v[8 * c + 2 * e + 1] = bf16_hi(w[e]);
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int g = i >> 5, t = i & 31;
+    const float v = bf16_bits(x[min(i, 32 * G - 1)]);
+    const float sc = g32_scale(half_wave_max(fabsf(v)));
+    const int q = (int)rintf(v * (1.0f / sc));
+    const int sum = half_wave_sum(q);
+    if (g < G) {
+        qx[32 * g + 8 * (t >> 3) + dot4_slot(t & 7)] = (int8_t)q;
+        if (t == 0) {
+            sx[g] = sc;
+            qsum[g] = sum;
         }
     }
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
-    const float sc = g32_scale(m);
-    const float inv = 1.0f / sc;
-    int sum = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        uint32_t lo, hi;
-        sum += quantize8_dot4(v + 8 * b, inv, lo, hi);
-        qx[4 * g + b] = make_uint2(lo, hi);
-    }
-    sx[g] = sc;
-    qsum[g] = sum;
 }
 
 __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
@@ -338,8 +326,8 @@ MOSS_API int moss_int8_quantize_g32(const void* x, void* qx, void* sx, void* qsu
     MOSS_CHECK_ARG(x && qx && sx && qsum && K > 0 && K % 32 == 0);
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qx, 16) && MOSS_ALIGNED(sx, 4) && MOSS_ALIGNED(qsum, 4));
     const int G = K / 32;
-    hipLaunchKernelGGL(int8_quantize_g32, dim3((G + 255) / 256), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, (uint2*)qx, (float*)sx, (int*)qsum, G);
+    hipLaunchKernelGGL(int8_quantize_g32, dim3((32 * G + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, (int8_t*)qx, (float*)sx, (int*)qsum, G);
     return moss_launch_status();
 }
 
