@@ -63,6 +63,9 @@ def test_host_only_entry_points(lib):
     assert lib.moss_gemm_workspace_bytes(512, 4096, 24576) == 0                   # prefill tiles fill the GPU
     assert lib.moss_gemm_workspace_bytes(512, 4096, 6144) == 2 * 512 * 6144 * 4   # 192 INT4 tiles: K split in 2
     assert lib.moss_gemm_workspace_bytes(512, 12288, 4096) == 4 * 512 * 4096 * 4  # 128 INT4 tiles: K split in 4
+    # M=16: 32 INT4 tiles of 32 tokens; the split doubles to 16 (512 workgroups) while the partials
+    # stay under half the weight bytes
+    assert lib.moss_gemm_workspace_bytes(16, 4096, 4096) == 16 * 16 * 4096 * 4
     assert lib.moss_error_string(0)
     assert lib.moss_decode_attention_splits(2048) == 32
     assert lib.moss_decode_attention_splits(128) == 2
