@@ -136,7 +136,8 @@ int moss_w4a8_gateup_silu(const void *qx, const void *sx, const void *qsum, cons
                           int rows_per_wave, void *stream);
 
 /* (add+)RMSNorm + int8 group quantizer + W4A8 projection in one kernel: x bf16 [K] (and res:
- * s = bf16(x + res), stored to sum_out), norm_w bf16 [K], K in {2048, 4096, 8192}; the
+ * s = bf16(x + res), stored to sum_out, which must not overlap x or res; res and sum_out are both
+ * NULL or both set), norm_w bf16 [K], K in {2048, 4096, 8192}; the
  * activations equal moss_rmsnorm_quant_g32's bit for bit, y as moss_w4a8_gemv.  Replaces the
  * fused norm + quantize + projection of src/moss_tts/_runtime/dp4a_norm_projection.py:48-166. */
 int moss_w4a8_norm_gemv(const void *x, const void *res, const void *norm_w, void *sum_out, float eps, const void *qw,
@@ -254,16 +255,13 @@ int moss_embedding_sum(const void *ids, const void *text, const void *audio, voi
  * gives the argmax (first maximal index); otherwise the top_k (1..64) largest of logits/temperature
  * in fp32, descending (ties: lower index first), their softmax, entries whose preceding cumulative
  * probability exceeds top_p removed, and one index drawn in proportion to the rest with a Philox4x32-10
- * uniform (counter = (*position, row, salt), key = seed).  out int64 [rows].
+ * uniform (counter = (*position, row, salt), key = *seed).  seed uint64 [1] and position int64 [1] are
+ * device buffers read when the kernel runs, so a captured graph follows new seeds and positions.
+ * out int64 [rows].
  * Replaces sample_topk, src/moss_tts/_runtime/llm.py:10-19 (torch.topk + softmax + multinomial). */
 int moss_sample_topk(const void *logits, int rows, int stride, int vocab, float temperature, int top_k, float top_p,
-                     unsigned long long seed, const void *position, int salt, void *out, void *stream);
+                     const void *seed, const void *position, int salt, void *out, void *stream);
 
-/* next_ids int64 [1 + channels] from the sampled text index (int64 [1], into text_ids int64 [2]) and
- * audio indices (int64 [channels]): the text token becomes delay_slot_id while *delay_length >= 0 and
- * audio_end_id at *delay_length == 32; audio code c is kept when c < *audio_length and
- * (*delay_length < 0 or c >= *delay_length), else pad_code.  Replaces the token logic of _decode,
- * src/moss_tts/_runtime/llm.py:280-287. */
 int moss_compose_next_ids(const void *text_index, const void *audio_index, const void *text_ids,
                           const void *audio_length, const void *delay_length, long long delay_slot_id,
                           long long audio_end_id, int channels, long long pad_code, void *next_ids, void *stream);

@@ -208,3 +208,20 @@ __device__ __forceinline__ void head_norm_rope(float a, float b, float w0, float
 #define MOSS_ALIGNED(p, a) ((((uintptr_t)(p)) % (a)) == 0)
 
 static inline int moss_launch_status() { return (int)hipGetLastError(); }
+
+// The fused-norm projections: res == NULL normalizes x; otherwise s = bf16(x + res) is normalized
+// and stored to sum_out by one workgroup while the others still read x and res, so sum_out must not
+// overlap either of them (an in-place residual update would race).  K % 2048 == 0, K <= 8192.
+static inline int moss_check_norm_args(const void* x, const void* res, const void* norm_w, void* sum_out, int K,
+                                       float eps) {
+    MOSS_CHECK_ARG(x && norm_w && K > 0 && K % 2048 == 0 && K <= 8192 && eps >= 0.f);
+    MOSS_CHECK_ARG((res == nullptr) == (sum_out == nullptr));
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(res, 16) &&
+                   MOSS_ALIGNED(sum_out, 16));
+    if (sum_out) {
+        const uintptr_t so = (uintptr_t)sum_out, n = (uintptr_t)K * 2;
+        MOSS_CHECK_ARG((so + n <= (uintptr_t)x || (uintptr_t)x + n <= so) &&
+                       (so + n <= (uintptr_t)res || (uintptr_t)res + n <= so));
+    }
+    return 0;
+}

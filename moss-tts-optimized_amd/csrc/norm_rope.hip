@@ -149,7 +149,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
     const uint16_t* wt = is_q ? qw : kw;
     const float a = bf16_bits(qkv[base + l]);       // dim l
     const float b = bf16_bits(qkv[base + l + 64]);  // dim l + 64
-    // positions are validated on the host; the clamp keeps every cache/table access in range
+    // positions live on the device (no host check without a sync): one outside [0, L) is clamped,
+    // so a bad position writes row 0 or L-1 instead of touching memory outside the cache
     const int64_t p = min(max(pos[t], (int64_t)0), (int64_t)(L - 1));
     const size_t crow = cos_by_position ? (size_t)p : (size_t)t;  // table row: by position or token
     const float c0 = bf16_bits(cos_t[crow * D + l]), c1 = bf16_bits(cos_t[crow * D + l + 64]);

@@ -6,8 +6,9 @@
 // lower index first), their softmax, the entries whose cumulative probability before them exceeds
 // top_p removed, and one index drawn in proportion to the rest.
 // Random numbers: Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers: as easy
-// as 1, 2, 3", SC 2011), counter = (position, row, salt), key = seed, so a captured decode graph
-// draws fresh numbers at every position without host involvement.  The draw inverts the
+// as 1, 2, 3", SC 2011), counter = (position, row, salt), key = the 64-bit seed read from a device
+// buffer, so a captured decode graph draws fresh numbers at every position, and for every seed the
+// host writes into that buffer between replays, without host involvement in the graph.  The draw inverts the
 // cumulative distribution: the first j with sum_{i <= j} p_i > u * sum_i p_i, u in [0, 1).
 //
 // compose_next_ids (src/moss_tts/_runtime/llm.py:280-287): text token = text_ids[text index],
@@ -80,7 +81,8 @@ __device__ __forceinline__ int wave_rank(unsigned long long v) {
 // usual case: about 31 for k = 25 over 1024 values) each lane ranks one against the others,
 // otherwise k rounds of wave argmax run over the candidates.
 __global__ __launch_bounds__(64) void sample_topk_rows(const uint16_t* __restrict__ logits, int stride, int vocab,
-                                                       float temperature, int top_k, float top_p, uint2 key,
+                                                       float temperature, int top_k, float top_p,
+                                                       const uint64_t* __restrict__ seed,
                                                        const int64_t* __restrict__ position, uint32_t salt,
                                                        int64_t* __restrict__ out) {
     __shared__ unsigned long long cand[kWave * kMaxPerLane];
@@ -170,6 +172,8 @@ __global__ __launch_bounds__(64) void sample_topk_rows(const uint16_t* __restric
         total_p += q;
     }
     const int64_t pos = *position;
+    const uint64_t sd = *seed;
+    const uint2 key = make_uint2((uint32_t)sd, (uint32_t)(sd >> 32));
     const uint4 rnd = philox4x32_10(make_uint4((uint32_t)pos, (uint32_t)((uint64_t)pos >> 32), (uint32_t)row, salt), key);
     const float u = (float)(rnd.x >> 8) * (1.0f / 16777216.0f);
     const float target = u * total_p;
@@ -252,16 +256,16 @@ __global__ __launch_bounds__(64) void advance_step_kernel(const int64_t* __restr
 using namespace moss;
 
 MOSS_API int moss_sample_topk(const void* logits, int rows, int stride, int vocab, float temperature, int top_k,
-                              float top_p, unsigned long long seed, const void* position, int salt, void* out,
+                              float top_p, const void* seed, const void* position, int salt, void* out,
                               void* stream) {
-    MOSS_CHECK_ARG(logits && position && out && rows > 0 && vocab > 0 && vocab <= kWave * kMaxPerLane &&
+    MOSS_CHECK_ARG(logits && seed && position && out && rows > 0 && vocab > 0 && vocab <= kWave * kMaxPerLane &&
                    stride >= vocab);
     MOSS_CHECK_ARG(!(temperature > 0.f) || (top_k >= 1 && top_k <= kMaxTopK && top_k <= vocab));
-    MOSS_CHECK_ARG(MOSS_ALIGNED(logits, 2) && MOSS_ALIGNED(position, 8) && MOSS_ALIGNED(out, 8));
-    const uint2 key = make_uint2((uint32_t)seed, (uint32_t)(seed >> 32));
+    MOSS_CHECK_ARG(MOSS_ALIGNED(logits, 2) && MOSS_ALIGNED(seed, 8) && MOSS_ALIGNED(position, 8) &&
+                   MOSS_ALIGNED(out, 8));
     hipLaunchKernelGGL(sample_topk_rows, dim3(rows), dim3(kWave), 0, (hipStream_t)stream, (const uint16_t*)logits,
-                       stride, vocab, temperature, top_k, top_p, key, (const int64_t*)position, (uint32_t)salt,
-                       (int64_t*)out);
+                       stride, vocab, temperature, top_k, top_p, (const uint64_t*)seed, (const int64_t*)position,
+                       (uint32_t)salt, (int64_t*)out);
     return moss_launch_status();
 }
 

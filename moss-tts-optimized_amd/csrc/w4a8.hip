@@ -366,11 +366,11 @@ MOSS_API int moss_w4a8_gateup_silu(const void* qx, const void* sx, const void* q
 static int w4a8_norm_entry(bool paired, const void* x, const void* res, const void* norm_w, void* sum_out, float eps,
                            const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
                            int rows_per_wave, void* stream) {
-    MOSS_CHECK_ARG(x && norm_w && qw && sc && zp && y && n_out > 0 && eps >= 0.f);
+    if (int rc = moss_check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
+    MOSS_CHECK_ARG(qw && sc && zp && y && n_out > 0);
     MOSS_CHECK_ARG(K == 2048 || K == 4096 || K == 8192);
     MOSS_CHECK_ARG(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4);
-    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(qw, 16));
-    MOSS_CHECK_ARG(!res || (sum_out && MOSS_ALIGNED(res, 16) && MOSS_ALIGNED(sum_out, 16)));
+    MOSS_CHECK_ARG(MOSS_ALIGNED(qw, 16));
     const W8Norm nm{(const uint16_t*)x, (const uint16_t*)res, (const uint16_t*)norm_w, (uint16_t*)sum_out, eps};
     return paired ? launch_w4a8_norm<true>(nm, qw, sc, zp, y, K, n_out, rows_per_wave, (hipStream_t)stream)
                   : launch_w4a8_norm<false>(nm, qw, sc, zp, y, K, n_out, rows_per_wave, (hipStream_t)stream);

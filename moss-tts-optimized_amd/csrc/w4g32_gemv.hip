@@ -613,25 +613,10 @@ MOSS_API int moss_w4g32_gateup_silu(const void* x, const void* qw, const void* s
                                 (hipStream_t)stream);
 }
 
-// The fused forms: res == NULL normalizes x; otherwise s = bf16(x + res) is normalized and
-// stored to sum_out (which must not overlap x or res: other workgroups still read them).
-static int check_norm_args(const void* x, const void* res, const void* norm_w, void* sum_out, int K, float eps) {
-    MOSS_CHECK_ARG(x && norm_w && K > 0 && K % 2048 == 0 && K <= 8192 && eps >= 0.f);
-    MOSS_CHECK_ARG((res == nullptr) == (sum_out == nullptr));
-    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(res, 16) &&
-                   MOSS_ALIGNED(sum_out, 16));
-    if (sum_out) {
-        const uintptr_t so = (uintptr_t)sum_out, n = (uintptr_t)K * 2;
-        MOSS_CHECK_ARG((so + n <= (uintptr_t)x || (uintptr_t)x + n <= so) &&
-                       (so + n <= (uintptr_t)res || (uintptr_t)res + n <= so));
-    }
-    return 0;
-}
-
 MOSS_API int moss_w4g32_norm_gemv(const void* x, const void* res, const void* norm_w, void* sum_out, float eps,
                                   const void* qw, const void* sc, const void* zp, void* y, int K, int N,
                                   int rows_per_wave, int dequant_mode, void* stream) {
-    if (int rc = check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
+    if (int rc = moss_check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
     MOSS_CHECK_ARG(qw && sc && zp && y && N > 0 && MOSS_ALIGNED(qw, 16));
     const NormArgs na{(const uint16_t*)res, (const uint16_t*)norm_w, (uint16_t*)sum_out, eps};
     if (res)
@@ -642,7 +627,7 @@ MOSS_API int moss_w4g32_norm_gemv(const void* x, const void* res, const void* no
 MOSS_API int moss_w4g32_norm_gateup_silu(const void* x, const void* res, const void* norm_w, void* sum_out,
                                          float eps, const void* qw, const void* sc, const void* zp, void* y, int K,
                                          int N_half, int rows_per_wave, int dequant_mode, void* stream) {
-    if (int rc = check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
+    if (int rc = moss_check_norm_args(x, res, norm_w, sum_out, K, eps)) return rc;
     MOSS_CHECK_ARG(qw && sc && zp && y && N_half > 0 && MOSS_ALIGNED(qw, 16));
     const NormArgs na{(const uint16_t*)res, (const uint16_t*)norm_w, (uint16_t*)sum_out, eps};
     if (res)

@@ -97,7 +97,8 @@ class DecodeStepG32:
         self.ws = attention.workspace(max_length, dev)
         self.audio_stride = audio_stride
         self.greedy = bool(greedy)
-        self.seed = int(seed)
+        # the sampler's Philox key, read on the device at every replay: set per request
+        self.seed_buf = sampling.seed_buffer(int(seed), dev)
         self.audio_end_id = int(audio_end_id)
         self.audio_start_id = int(audio_start_id)
         self.text_ids_host = tuple(int(t) for t in text_ids)
@@ -165,10 +166,10 @@ class DecodeStepG32:
         text top-2 at temperature 1.5, audio top-25 / top-p 0.8 at temperature 1.7, or argmax when
         greedy."""
         n_audio = CODEBOOKS * self.audio_stride
-        sampling.sample_topk(logits[n_audio:n_audio + 2], 0.0 if self.greedy else 1.5, 2, 1.0, seed=self.seed,
+        sampling.sample_topk(logits[n_audio:n_audio + 2], 0.0 if self.greedy else 1.5, 2, 1.0, seed=self.seed_buf,
                              position=self.position, salt=1, out=self.text_index)
         sampling.sample_topk(logits[:head_count * self.audio_stride].view(head_count, self.audio_stride),
-                             0.0 if self.greedy else 1.7, 25, 0.8, seed=self.seed, position=self.position, salt=0,
+                             0.0 if self.greedy else 1.7, 25, 0.8, seed=self.seed_buf, position=self.position, salt=0,
                              vocab=SAMPLED_CODES, out=self.audio_index[:head_count])
         sampling.compose_next_ids(self.text_index, self.audio_index, self.text_ids, self.audio_length,
                                   self.delay_length, delay_slot_id=int(self.text_ids_host[1]),
@@ -229,13 +230,25 @@ class DecodeStepG32:
         self.graph.replay()
         return self.logits
 
+    @property
+    def seed(self) -> int:
+        """The sampler's 64-bit seed (reads the device buffer)."""
+        return int(self.seed_buf.item()) & 0xFFFFFFFFFFFFFFFF
+
+    @seed.setter
+    def seed(self, value: int) -> None:
+        self.seed_buf.fill_(sampling.seed_value(int(value)))
+
     @torch.inference_mode()
     def decode(self, ids: torch.Tensor, position: int, audio_length: int = CODEBOOKS,
-               delay_length: int = -1) -> torch.Tensor:
+               delay_length: int = -1, *, seed: int | None = None) -> torch.Tensor:
         """One step with the reference's ``FastLLM.step`` contract (``llm.py:327-338``): int64 ids
-        ``[1, 33]`` in, the next ids ``[1, 1, 33]`` out (sampled on the device)."""
+        ``[1, 33]`` in, the next ids ``[1, 1, 33]`` out (sampled on the device).  ``seed`` sets the
+        sampler's key first (a captured graph reads it at replay); ``None`` keeps the current one."""
         if not 0 <= position < self.max_length:
             raise ValueError("KV capacity exceeded")
+        if seed is not None:
+            self.seed = seed
         self.audio_length.fill_(audio_length)
         self.delay_length.fill_(delay_length)
         self.step(ids, position)
@@ -390,9 +403,11 @@ class FirstAudioGraph:
                 dst.copy_(src)
 
     @torch.inference_mode()
-    def run(self, ids: torch.Tensor, position: int, *, delay: int = -1) -> tuple[torch.Tensor, torch.Tensor]:
+    def run(self, ids: torch.Tensor, position: int, *, delay: int = -1,
+            seed: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """The ``steps`` next-id rows ``[steps, 33]`` and the final (text token, audio length,
-        delay, position), both device tensors overwritten by the next run."""
+        delay, position), both device tensors overwritten by the next run.  ``seed`` sets the
+        sampler's key for this run (``None`` keeps the engine's current one)."""
         if self.graph is None:
             raise RuntimeError("Warm the first-audio graph before use")
         e = self.engine
@@ -402,6 +417,8 @@ class FirstAudioGraph:
             raise ValueError("Expected a CUDA int64 audio-start row with all 32 channels")
         if delay not in (-1, 0):
             raise ValueError("Only fresh audio or an immediate-delay validation probe is supported")
+        if seed is not None:
+            e.seed = seed
         self._initialize(ids, position, delay)
         self.graph.replay()
         return self.history, self.status

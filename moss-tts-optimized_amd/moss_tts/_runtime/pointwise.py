@@ -45,12 +45,6 @@ def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, e
     return summed, y
 
 
-def add_rmsnorm_into(x, residual, weight, eps, summed, y) -> None:
-    """Allocation-free variant for captured decode graphs (outputs preallocated)."""
-    native.call("moss_rmsnorm", native.ptr(x), native.ptr(residual), native.ptr(weight), native.ptr(summed),
-                native.ptr(y), x.numel() // x.shape[-1], x.shape[-1], float(eps), native.stream_of(x))
-
-
 QH, KH, HD = 32, 8, 128
 QKV = (QH + 2 * KH) * HD
 
@@ -62,7 +56,10 @@ def qk_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, c
     in place and returns ``q`` as ``[1, 32, n, 128]`` (a transposed view, like the reference).
 
     ``cos``/``sin`` hold one row per token, or with ``cos_by_position`` a whole ``[L, 128]``
-    table indexed by each token's (device-side) position."""
+    table indexed by each token's (device-side) position.  Positions are device values and are not
+    checked here: the kernel clamps one outside ``[0, L)`` to the nearest row, so it overwrites
+    that row rather than memory beyond the cache.  ``out``: a contiguous bf16 buffer of
+    ``n * 32 * 128`` values to write ``q`` into (``[1, n, 32, 128]`` order)."""
     _cuda_contig("qkv", qkv, torch.bfloat16)
     dev = qkv.device
     _require(qkv.shape[-1] == QKV, f"Qwen3-8B QKV rows of {QKV} required")
@@ -82,7 +79,12 @@ def qk_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, c
     _cuda_contig("positions", positions, torch.int64, dev)
     _require(positions.numel() == n, "one int64 position per token required")
     _require(n <= L, "more tokens than KV rows")
-    q = out if out is not None else torch.empty((1, n, QH, HD), device=dev, dtype=torch.bfloat16)
+    if out is not None:
+        _cuda_contig("out", out, torch.bfloat16, dev)
+        _require(out.numel() == n * QH * HD, f"out must hold {n * QH * HD} values")
+        q = out.view(1, n, QH, HD)
+    else:
+        q = torch.empty((1, n, QH, HD), device=dev, dtype=torch.bfloat16)
     native.call("moss_qk_norm_rope_kv", native.ptr(qkv), native.ptr(q_weight), native.ptr(k_weight),
                 native.ptr(cos), native.ptr(sin), native.ptr(q), native.ptr(keys), native.ptr(values),
                 native.ptr(positions), L, n, float(eps), int(bool(cos_by_position)), native.stream_of(qkv))

@@ -3,10 +3,12 @@
 ``sample_topk(logits, temperature=1.7, top_k=25, top_p=0.8)`` keeps the reference's signature and
 meaning (``src/moss_tts/_runtime/llm.py:10-19``); the random draw comes from a counter-based
 Philox4x32-10 keyed by ``seed`` and indexed by the device-side ``position`` and the row, so a
-captured decode graph samples fresh values at every position.  ``compose_next_ids`` is the token
-logic of the reference's ``_decode`` (``llm.py:280-287``).  ``advance_step`` is the host loop's
-per-step update (``src/moss_tts/_runtime/streaming.py:107-112``) on the device, so several decode
-steps can be captured in one graph (``src/moss_tts/_runtime/first_audio_graph.py:14-29``).
+captured decode graph samples fresh values at every position.  The key is read from a device
+buffer when the kernel runs (``seed_buffer``), so each request can set its own seed without
+recapturing.  ``compose_next_ids`` is the token logic of the reference's ``_decode``
+(``llm.py:280-287``).  ``advance_step`` is the host loop's per-step update
+(``src/moss_tts/_runtime/streaming.py:107-112``) on the device, so several decode steps can be
+captured in one graph (``src/moss_tts/_runtime/first_audio_graph.py:14-29``).
 """
 from __future__ import annotations
 
@@ -17,13 +19,27 @@ from .w4g32 import _cuda_contig, _require
 
 MAX_TOP_K = 64
 MAX_VOCAB = 2048
+_U64 = 0xFFFFFFFFFFFFFFFF
+
+
+def seed_value(seed: int) -> int:
+    """A 64-bit seed as the signed int64 whose bits the sampler reads as its Philox key."""
+    _require(isinstance(seed, int), "seed must be an int")
+    u = int(seed) & _U64
+    return u - (1 << 64) if u >= 1 << 63 else u
+
+
+def seed_buffer(seed: int, device) -> torch.Tensor:
+    """A device int64 ``[1]`` holding ``seed``'s 64 bits: the sampler's key buffer."""
+    return torch.full((1,), seed_value(seed), dtype=torch.int64, device=device)
 
 
 def sample_topk(logits: torch.Tensor, temperature: float = 1.7, top_k: int = 25, top_p: float = 0.8, *,
-                seed: int = 0, position: torch.Tensor | None = None, salt: int = 0, vocab: int | None = None,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                seed: int | torch.Tensor = 0, position: torch.Tensor | None = None, salt: int = 0,
+                vocab: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 logits ``[rows, stride]`` (or ``[stride]``) -> int64 indices ``[rows]`` into the first
-    ``vocab`` entries of each row."""
+    ``vocab`` entries of each row.  ``seed``: an int, or a device int64 ``[1]`` buffer read when the
+    kernel runs (what a captured graph uses)."""
     _cuda_contig("logits", logits, torch.bfloat16)
     rows = 1 if logits.dim() == 1 else logits.shape[0]
     stride = logits.shape[-1]
@@ -34,13 +50,18 @@ def sample_topk(logits: torch.Tensor, temperature: float = 1.7, top_k: int = 25,
     if position is None:
         position = torch.zeros(1, dtype=torch.int64, device=logits.device)
     _cuda_contig("position", position, torch.int64, logits.device)
+    _require(position.numel() == 1, "position holds one value")
+    if not isinstance(seed, torch.Tensor):
+        seed = seed_buffer(seed, logits.device)
+    _cuda_contig("seed", seed, torch.int64, logits.device)
+    _require(seed.numel() == 1, "seed holds one value")
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     else:
         _cuda_contig("out", out, torch.int64, logits.device)
         _require(out.numel() == rows, f"out must hold {rows} indices")
     native.call("moss_sample_topk", native.ptr(logits), rows, stride, vocab, float(temperature), int(top_k),
-                float(top_p), int(seed) & 0xFFFFFFFFFFFFFFFF, native.ptr(position), int(salt), native.ptr(out),
+                float(top_p), native.ptr(seed), native.ptr(position), int(salt), native.ptr(out),
                 native.stream_of(logits))
     return out
 

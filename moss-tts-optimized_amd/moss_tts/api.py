@@ -38,8 +38,8 @@ class GptqEngine:
     def step(self, ids, position: int):
         return self.decode.step(ids, position)
 
-    def next_ids(self, ids, position: int, audio_length: int, delay_length: int):
-        return self.decode.decode(ids, position, audio_length, delay_length)
+    def next_ids(self, ids, position: int, audio_length: int, delay_length: int, seed: int | None = None):
+        return self.decode.decode(ids, position, audio_length, delay_length, seed=seed)
 
     def enable_first_audio_graph(self, steps: int = 32) -> dict:
         """Capture the steps right after the audio start as one graph
@@ -55,10 +55,10 @@ class GptqEngine:
         self.first_audio = graph
         return {"codebooks": 32, "steps": graph.steps}
 
-    def run_first_audio(self, ids, position: int, delay: int = -1):
+    def run_first_audio(self, ids, position: int, delay: int = -1, seed: int | None = None):
         if self.first_audio is None:
             raise RuntimeError("Warm the first-audio graph before use")
-        return self.first_audio.run(ids, position, delay=delay)
+        return self.first_audio.run(ids, position, delay=delay, seed=seed)
 
 
 class MossTTS:
@@ -152,20 +152,29 @@ class MossTTS:
         with self._request():
             return self._engine.step(ids, position)
 
-    def next_ids(self, ids, position: int, audio_length: int = 32, delay_length: int = -1):
+    def next_ids(self, ids, position: int, audio_length: int = 32, delay_length: int = -1,
+                 seed: int | None = None):
         """The same step with the reference's sampling and delay-pattern logic
         (``FastLLM.step``, ``src/moss_tts/_runtime/llm.py:327-338``): the next ids int64
-        ``[1, 1, 33]``."""
+        ``[1, 1, 33]``.  ``seed`` sets the sampler's seed first; ``None`` keeps the current one
+        (the draws also depend on ``position``)."""
         with self._request():
-            return self._engine.next_ids(ids, position, audio_length, delay_length)
+            return self._engine.next_ids(ids, position, audio_length, delay_length, seed)
 
-    def first_audio(self, ids, position: int, delay: int = -1):
+    def first_audio(self, ids, position: int, delay: int = -1, seed: int | None = None):
         """The steps after the audio start in one graph replay (``FirstAudioGraph.run``): ``ids`` is
         the audio-start row int64 ``[1, 1, 33]``; returns the next-id rows ``[steps, 33]`` and the
         final (text token, audio length, delay, position).  Needs
-        ``engine.enable_first_audio_graph()`` first."""
+        ``engine.enable_first_audio_graph()`` first.  This starts a request's audio: with
+        ``seed=None`` a fresh 63-bit seed is drawn from torch's default CPU generator, which the
+        reference's ``torch.multinomial`` draws also advance, so repeated requests sample
+        differently and ``torch.manual_seed`` makes a run reproducible."""
+        if seed is None:
+            import torch
+
+            seed = int(torch.randint(0, 2**63 - 1, (1,)).item())
         with self._request():
-            return self._engine.run_first_audio(ids, position, delay)
+            return self._engine.run_first_audio(ids, position, delay, seed)
 
     @property
     def engine(self):

@@ -23,16 +23,18 @@ from . import w4g32 as ow
 
 
 def decode_step(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):
-    """``layers``: dicts with bf16 dequantized ``qkv``, ``o``, ``gate_up``, ``down`` weights and
-    ``input_norm``, ``post_norm``, ``q_norm``, ``k_norm``; ``keys``/``values`` lists of
-    ``[1, 8, L, 128]`` caches (updated in place).  Returns bf16 logits."""
+    """``layers``: an iterable of dicts with bf16 dequantized ``qkv``, ``o``, ``gate_up``, ``down``
+    weights (or fp32 tensors holding bf16 values) and ``input_norm``, ``post_norm``, ``q_norm``,
+    ``k_norm``; it is consumed once, in order, so a generator can dequantize one layer at a time.
+    ``keys``/``values`` lists of ``[1, 8, L, 128]`` caches (updated in place).  Returns bf16 logits."""
     p = int(position)
     x = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
     residual = x
-    h = op.rmsnorm(x, layers[0]["input_norm"], eps)
     mlp = None
     for i, L in enumerate(layers):
-        if i > 0:
+        if i == 0:
+            h = op.rmsnorm(x, L["input_norm"], eps)
+        else:
             residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
         qkv = ow.linear(h, L["qkv"]).bfloat16()
         q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],

@@ -272,6 +272,38 @@ def rowunpack(qw: torch.Tensor, zp: torch.Tensor):
     return torch.from_numpy(out.reshape(n, k8 * 8)), torch.from_numpy(z)
 
 
+_ROWPACK_SHIFTS = (0, 16, 4, 20, 8, 24, 12, 28)   # bit offset of code t = 0..7 in a row-packed word
+
+
+def dequantize_rowpack_f32(qw: torch.Tensor, sc: torch.Tensor, zp: torch.Tensor,
+                           out: torch.Tensor | None = None, chunk: int = 512) -> torch.Tensor:
+    """The row-packed weight (layout of :func:`rowpack`) dequantized with multi-threaded torch CPU
+    ops for full-size layers: ``float32 [N, K]`` holding exactly the bf16 values
+    ``bf16_rne(f32(q - z) * f32(s))`` (``calibrated_quant.py:41-42``), ready for ``F.linear``.
+    Works through ``chunk`` rows at a time; ``out`` (fp32, at least ``N * K`` values) is reused
+    when given, so a layer loop does not fault in fresh pages for every projection."""
+    w = qw.contiguous().view(torch.int32)
+    n, k8 = w.shape
+    k = 8 * k8
+    g = k // GROUP
+    shifts = torch.tensor(_ROWPACK_SHIFTS, dtype=torch.int32)
+    zb = zp.contiguous().to(torch.int32)
+    z = torch.empty((n, g), dtype=torch.int32)
+    for c0 in range(0, g, 128):
+        r = min(128, g - c0)
+        blk = zb[:, c0 // 2: c0 // 2 + r // 2]
+        z[:, c0: c0 + r // 2] = blk & 15
+        z[:, c0 + r // 2: c0 + r] = blk >> 4
+    res = torch.empty((n, k)) if out is None else out.view(-1)[: n * k].view(n, k)
+    for r0 in range(0, n, chunk):
+        r1 = min(n, r0 + chunk)
+        codes = (w[r0:r1].unsqueeze(-1) >> shifts) & 15                       # [rows, K/8, 8] in k order
+        d = (codes.view(r1 - r0, g, GROUP) - z[r0:r1, :, None]).float()
+        d.mul_(sc[r0:r1].float()[:, :, None])
+        res[r0:r1] = d.view(r1 - r0, k).bfloat16()
+    return res
+
+
 # ------------------------------------------------------------------- linear contracts
 def linear(x: torch.Tensor, w_bf16: torch.Tensor) -> torch.Tensor:
     """``F.linear(x.float(), w.float())`` in fp32 on the CPU -- ``calibration.py:185-188``."""
@@ -304,15 +336,22 @@ def w4g32_gateup_silu(x: torch.Tensor, q, z, s, n_half: int) -> torch.Tensor:
 
 
 # ------------------------------------------------- CPU baseline (timed in bench.py only)
+def gptq_dequant_cpu(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor) -> torch.Tensor:
+    """The dequant half of :func:`gptq_dequant_linear_cpu`: AutoGPTQ ``qweight int32 [K/8,N]``,
+    ``scales bf16 [G,N]``, ``qzeros int32 [G,N/8]`` -> ``w bf16 [K,N]`` with
+    ``w = bf16((q - z) * s)`` (``calibrated_quant.py:41-42``), in multi-threaded torch CPU ops."""
+    k8, n = qweight.shape
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
+    q = ((qweight.unsqueeze(1) >> shifts[None, :, None]) & 15).reshape(k8 * 8, n)
+    z = ((qzeros.unsqueeze(2) >> shifts[None, None, :]) & 15).reshape(qzeros.shape[0], n)
+    return ((q.view(-1, GROUP, n) - z[:, None, :]).float() * scales.float()[:, None, :]).bfloat16().view(k8 * 8, n)
+
+
 def gptq_dequant_linear_cpu(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                             qzeros: torch.Tensor) -> torch.Tensor:
     """The reference's dequant-then-matmul on the AutoGPTQ layout with multi-threaded torch
     CPU ops, dequantizing on every call: unpack nibbles, ``w = bf16((q - z) * s)``
     (``calibrated_quant.py:41-42``), ``F.linear(x.float(), w.float())``
     (``calibration.py:185-188``).  Returns fp32 ``[M, N]``."""
-    k8, n = qweight.shape
-    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
-    q = ((qweight.unsqueeze(1) >> shifts[None, :, None]) & 15).reshape(k8 * 8, n)
-    z = ((qzeros.unsqueeze(2) >> shifts[None, None, :]) & 15).reshape(qzeros.shape[0], n)
-    w = ((q.view(-1, GROUP, n) - z[:, None, :]).float() * scales.float()[:, None, :]).bfloat16()
-    return torch.nn.functional.linear(x.float(), w.view(k8 * 8, n).t().float())
+    w = gptq_dequant_cpu(qweight, scales, qzeros)
+    return torch.nn.functional.linear(x.float(), w.t().float())

@@ -1,10 +1,30 @@
-"""Shared comparison helpers of the GPU parity tests (bars written out in each docstring)."""
+"""Shared comparison helpers of the parity tests (bars written out in each docstring)."""
+from fractions import Fraction
+
 import torch
 
 from oracle import w4g32 as o
 
 ATOL = 1e-2
 RTOL = 1e-2
+
+
+def rn_f32(fr: Fraction) -> float:
+    """Round a rational to the nearest float32 (ties to even), subnormals included."""
+    if fr == 0:
+        return 0.0
+    sign = -1.0 if fr < 0 else 1.0
+    v = abs(fr)
+    e = v.numerator.bit_length() - v.denominator.bit_length()
+    if Fraction(2) ** e > v:
+        e -= 1
+    ulp = max(e - 23, -149)
+    scaled = v / Fraction(2) ** ulp
+    n = scaled.numerator // scaled.denominator
+    rem = scaled - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * float(n) * 2.0 ** ulp
 
 
 def _assert_close(got, ref, what):

@@ -96,15 +96,27 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, p, p, 4096, 48, 0, null) == 1      # N_half % 32
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, p, p, 4096, 64, 1, null) == 1      # fused rows 2|4
     f = ctypes.c_float
-    assert lib.moss_sample_topk(p, 32, 1025, 1024, f(1.7), 0, f(0.8), 0, p, 0, p, null) == 1      # top_k >= 1
-    assert lib.moss_sample_topk(p, 32, 1025, 1024, f(1.7), 65, f(0.8), 0, p, 0, p, null) == 1     # top_k <= 64
-    assert lib.moss_sample_topk(p, 1, 4096, 4096, f(0.0), 1, f(0.8), 0, p, 0, p, null) == 1      # vocab <= 2048
-    assert lib.moss_sample_topk(p, 1, 100, 200, f(0.0), 1, f(0.8), 0, p, 0, p, null) == 1        # stride >= vocab
+    assert lib.moss_sample_topk(p, 32, 1025, 1024, f(1.7), 0, f(0.8), p, p, 0, p, null) == 1      # top_k >= 1
+    assert lib.moss_sample_topk(p, 32, 1025, 1024, f(1.7), 65, f(0.8), p, p, 0, p, null) == 1     # top_k <= 64
+    assert lib.moss_sample_topk(p, 1, 4096, 4096, f(0.0), 1, f(0.8), p, p, 0, p, null) == 1      # vocab <= 2048
+    assert lib.moss_sample_topk(p, 1, 100, 200, f(0.0), 1, f(0.8), p, p, 0, p, null) == 1        # stride >= vocab
+    assert lib.moss_sample_topk(p, 1, 100, 100, f(1.0), 1, f(0.8), null, p, 0, p, null) == 1     # seed buffer
+    assert lib.moss_sample_topk(p, 1, 100, 100, f(1.0), 1, f(0.8), ctypes.c_void_p(4100), p, 0, p,
+                                null) == 1                                                        # seed alignment
     assert lib.moss_compose_next_ids(p, p, p, p, p, 0, 0, 0, 1024, p, null) == 1                  # channels
     q = ctypes.c_void_p(8192)
     assert lib.moss_w4a8_norm_gemv(p, null, p, null, f(1e-6), p, p, p, p, 12288, 64, 0, null) == 1   # K
     assert lib.moss_w4a8_norm_gemv(p, p, p, null, f(1e-6), p, p, p, p, 4096, 64, 0, null) == 1       # sum_out
     assert lib.moss_w4a8_norm_gateup_silu(p, null, p, null, f(1e-6), p, p, p, p, 4096, 64, 3, null) == 1  # rows
+    # sum_out overlapping x or res (an in-place residual update) races with the other workgroups
+    x0, r0 = ctypes.c_void_p(1 << 20), ctypes.c_void_p(2 << 20)
+    for norm in (lib.moss_w4a8_norm_gemv, lib.moss_w4a8_norm_gateup_silu, lib.moss_w4g32_norm_gemv,
+                 lib.moss_w4g32_norm_gateup_silu):
+        extra = (0,) if norm in (lib.moss_w4g32_norm_gemv, lib.moss_w4g32_norm_gateup_silu) else ()
+        assert norm(x0, r0, p, r0, f(1e-6), p, p, p, p, 4096, 64, 0, *extra, null) == 1         # sum_out == res
+        assert norm(x0, r0, p, ctypes.c_void_p((1 << 20) + 4096), f(1e-6), p, p, p, p, 4096, 64, 0, *extra,
+                    null) == 1                                                                    # overlaps x
+        assert norm(x0, null, p, q, f(1e-6), p, p, p, p, 4096, 64, 0, *extra, null) == 1        # res NULL
     assert lib.moss_decode_attention_qkv_quant(p, p, p, p, p, p, p, p, p, p, p, null, p, p, 2048, f(1e-6),
                                                null) == 1                                         # out_qx
     assert lib.moss_decode_attention_qkv_quant(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 2000, f(1e-6),

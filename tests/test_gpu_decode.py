@@ -52,6 +52,63 @@ def test_decode_step_two_layers(dev):
             assert float(d.max()) <= 0.1 + 0.05 * float(ref[:, :, position].float().abs().max())
 
 
+def test_decode_step_full_size(dev):
+    """The benchmarked configuration itself: 36 layers, KV capacity 2048 filled with N(0,1), the
+    token at position 2047, INT4 heads N = 32 x 1025 + 2, run as the captured graph.  The oracle runs
+    the same step one layer at a time on the CPU (each layer dequantized from the engine's packed
+    weights by the oracle's own unpack), so memory stays at one layer.  Bars: relative L2 of the
+    logits < 2e-2; K/V row 2047 of layers 0 and 35 within the composed drift; every other row of
+    those layers untouched."""
+    import time
+
+    from moss_tts._runtime.decode import DecodeStepG32
+
+    print("decode step: 36 layers, L=2048, p=2047 (graph replay)", flush=True)
+    L, position, n_layers = 2048, 2047, 36
+    eng = DecodeStepG32.random(n_layers, max_length=L, device=dev, seed=4242)
+    eng.capture()                                      # the warm-up steps write KV row 0
+    keys0 = [k.cpu() for k in eng.keys]
+    values0 = [v.cpu() for v in eng.values]
+    ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
+    logits = eng.step(ids, position).float().cpu()
+    torch.cuda.synchronize()
+    print("GPU step done; oracle layer by layer", flush=True)
+    bufs = {}
+
+    def deq(name, m):
+        if name not in bufs:
+            bufs[name] = torch.empty(m.N * m.K)
+        return o.dequantize_rowpack_f32(m.qw.cpu(), m.scales.cpu(), m.zeros.cpu(), out=bufs[name])
+
+    def layers():
+        t0 = time.time()
+        for i, l in enumerate(eng.layers):
+            yield dict(qkv=deq("qkv", l.qkv.packed), o=deq("o", l.o.packed), gate_up=deq("gate_up", l.gate_up.packed),
+                       down=deq("down", l.down.packed), input_norm=l.input_norm.cpu(), post_norm=l.post_norm.cpu(),
+                       q_norm=l.q_norm.cpu(), k_norm=l.k_norm.cpu())
+            if i % 6 == 5:
+                print(f"  oracle layer {i + 1}/{n_layers} ({time.time() - t0:.1f} s)", flush=True)
+
+    keys = [k.clone() for k in keys0]
+    values = [v.clone() for v in values0]
+    heads = eng.heads.packed
+    ref = od.decode_step(layers(), eng.final_norm.cpu(), deq("heads", heads), eng.text_embedding.cpu(),
+                         eng.audio_embedding.cpu(), ids, position, keys, values, eng.cos.cpu(), eng.sin.cpu())
+    ref = ref.float()
+    rel = float((logits - ref).norm() / ref.norm())
+    print(f"relative L2 error of logits: {rel:.3e}", flush=True)
+    assert rel < 2e-2
+    for i in (0, n_layers - 1):
+        got_k, got_v = eng.keys[i].cpu(), eng.values[i].cpu()
+        assert torch.equal(got_k[:, :, :position], keys0[i][:, :, :position])
+        assert torch.equal(got_v[:, :, :position], values0[i][:, :, :position])
+        for got, want in ((got_k, keys[i]), (got_v, values[i])):
+            g_row, r_row = got[:, :, position].float(), want[:, :, position].float()
+            rel_row = float((g_row - r_row).norm() / r_row.norm())
+            print(f"layer {i} KV row {position}: relative L2 {rel_row:.3e}", flush=True)
+            assert rel_row < 2e-2
+
+
 def test_decode_graph_replay_matches_eager(dev):
     from moss_tts._runtime.decode import DecodeStepG32
 

@@ -263,3 +263,35 @@ def test_first_audio_graph_equals_sequential_steps(dev, delay, prefixes):
     assert set(hist[:, 0]) <= {gen, dslot}
     if delay == 0:   # the probe starts the delay counter: every composed text token is the delay slot
         assert (hist[:, 0] == dslot).all() and int(status[2]) == CODEBOOKS
+
+
+def test_seed_per_request(dev):
+    """The sampler reads its key from a device buffer: after capture, a new seed changes the draws
+    of the replayed graph (they follow the oracle's Philox uniforms for that seed), the same seed
+    reproduces them, and the first-audio graph takes a per-run seed the same way."""
+    from moss_tts._runtime.decode import CODEBOOKS, DecodeStepG32, FirstAudioGraph
+
+    print("per-request seed", flush=True)
+    eng = DecodeStepG32.random(1, max_length=128, device=dev, seed=5, text_vocab=256, sample_seed=7)
+    eng.capture()
+    ids = torch.tensor([[17] + [3] * 32], dtype=torch.int64)
+    a = eng.decode(ids, 5, seed=1).view(-1).cpu().numpy()
+    b = eng.decode(ids, 5, seed=2).view(-1).cpu().numpy()
+    assert eng.seed == 2
+    logits = eng.logits.float().cpu().numpy()
+    audio = logits[:CODEBOOKS * eng.audio_stride].reshape(CODEBOOKS, eng.audio_stride)[:, :1024]
+    for c in range(CODEBOOKS):
+        _check_draw(int(b[1 + c]), audio[c], 1.7, 25, 0.8, os_.uniform(2, 5, c, 0), f"seed 2 channel {c}")
+    again = eng.decode(ids, 5, seed=1).view(-1).cpu().numpy()
+    assert np.array_equal(a, again)
+    assert not np.array_equal(a[1:], b[1:])
+    eng.seed = (1 << 64) - 3          # the full 64-bit range round-trips through the int64 buffer
+    assert eng.seed == (1 << 64) - 3
+    burst = FirstAudioGraph(eng, steps=8)
+    burst.warmup()
+    first = torch.full((1, 1, 33), 1024, dtype=torch.int64, device=dev)
+    first[0, 0, 0] = eng.audio_start_id
+    h3 = burst.run(first, 40, seed=3)[0].cpu().numpy().copy()
+    h4 = burst.run(first, 40, seed=4)[0].cpu().numpy().copy()
+    h3b = burst.run(first, 40, seed=3)[0].cpu().numpy().copy()
+    assert np.array_equal(h3, h3b) and not np.array_equal(h3, h4)

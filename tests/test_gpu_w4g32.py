@@ -102,8 +102,11 @@ GEMV_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("k,n", GEMV_SHAPES)
-@pytest.mark.parametrize("rows", [0, 1, 2, 4])
+# explicit rows-per-wave launches at the small shapes; the full-size shapes run the default launch
+GEMV_CASES = [(k, n, rows) for k, n in GEMV_SHAPES for rows in ((0, 1, 2, 4) if k * n <= 4096 * 4096 else (0,))]
+
+
+@pytest.mark.parametrize("k,n,rows", GEMV_CASES)
 @pytest.mark.parametrize("mode", ["exact", "unrounded"])
 def test_gemv_parity(dev, k, n, rows, mode):
     """Both dequant modes meet the 1e-2 bar; the exact mode multiplies x by the bit-exact bf16
@@ -111,8 +114,6 @@ def test_gemv_parity(dev, k, n, rows, mode):
     where fp32 summation order moves a value across a rounding midpoint."""
     from moss_tts._runtime import w4g32
 
-    if k * n > 4096 * 4096 and rows not in (0,):
-        pytest.skip("full-size shapes are covered with the default launch")
     print(f"gemv K={k} N={n} rows={rows} mode={mode}", flush=True)
     q, z, s = _case(n, k, 100 + k + n)
     x = torch.randn((1, k), generator=torch.Generator().manual_seed(1)).bfloat16()
@@ -162,6 +163,64 @@ def test_gemv_exact_properties_full_size(dev, k, n, mode):
     assert torch.count_nonzero(w4g32.gemv(torch.zeros_like(x), pw, dequant=dqm)) == 0
 
 
+def _scale_sweep_weight():
+    """One 32-code group per (bf16 scale, zero point) for every positive finite bf16 scale (bit patterns
+    0x0001..0x7F7F, subnormals included) and all 16 zero points; each group holds every code 0..15
+    twice, rotated by the group index so every code meets every nibble position.  Rows of K = 4096;
+    the groups that pad the last row use scale 1."""
+    scales = torch.arange(1, 0x7F80, dtype=torch.int32)                    # 0x7F80 is +inf
+    n_groups = scales.numel() * 16
+    k, gpr = 4096, 128
+    rows = -(-n_groups // gpr)
+    s_bits = torch.full((rows * gpr,), 0x3F80, dtype=torch.int32)
+    s_bits[:n_groups] = scales.repeat_interleave(16)
+    z = torch.zeros(rows * gpr, dtype=torch.int32)
+    z[:n_groups] = torch.arange(16, dtype=torch.int32).repeat(scales.numel())
+    gi = torch.arange(rows * gpr, dtype=torch.int32)[:, None]
+    q = (torch.arange(32, dtype=torch.int32)[None, :] + gi) % 16
+    s = s_bits.to(torch.int16).view(torch.bfloat16).view(rows, gpr)
+    return q.view(rows, k).to(torch.uint8), z.view(rows, gpr).to(torch.uint8), s, scales
+
+
+def test_exact_dequant_every_bf16_scale(dev):
+    """The bit-exact dequant bf16_rne((q - z) * s) over all 16 x 16 (q, z) pairs and every positive
+    finite bf16 scale, in the three places it is formed: the dequant kernel (plain fp32 product),
+    the decode GEMV's exact mode (one-hot activations select each column; v_dot2 block) and the
+    prefill GEMM's producer (identity activations give the whole matrix; same block).  The dequant
+    kernel must equal the oracle bit for bit everywhere.  A one-hot product reads 0 * w for the
+    other weights of a row, which is NaN where some w is infinite, so the GEMV and GEMM are checked
+    on the rows whose dequantized weights are all finite (every scale up to 2^123)."""
+    from moss_tts._runtime import w4g32
+
+    print("exact dequant over every positive finite bf16 scale", flush=True)
+    q, z, s, scales = _scale_sweep_weight()
+    n, k = q.shape
+    ref = _bits(o.dequantize(q, z, s))
+    pw = _packed(q, z, s, dev)
+    assert torch.equal(_bits(w4g32.dequantize(pw)), ref), "dequant kernel"
+    finite_rows = ((ref & 0x7F80) != 0x7F80).all(1)
+    s_bits = s.contiguous().view(torch.int16).to(torch.int32)
+
+    def check(got_t, what):
+        bad = (got_t != ref) & finite_rows[:, None]
+        nbad = int(bad.sum())
+        if nbad:
+            rows_bad = bad.view(n, 128, 32).any(-1)
+            lo = int(s_bits[rows_bad].min())
+            print(f"{what}: {nbad} mismatches; smallest scale with one: 0x{lo:04x}", flush=True)
+        assert nbad == 0, what
+
+    eye = torch.eye(k, dtype=torch.bfloat16, device=dev)
+    gemm = w4g32.gemm(eye, pw)                                             # [K, N] = dequant(W)^T
+    torch.cuda.synchronize()
+    check(_bits(gemm).t(), "GEMM producer")
+    cols = torch.empty((k, n), dtype=torch.bfloat16, device=dev)
+    for c in range(k):
+        cols[c] = w4g32.gemv(eye[c:c + 1], pw)[0]
+    torch.cuda.synchronize()
+    check(_bits(cols).t(), "GEMV exact mode")
+
+
 def test_gemv_rejects_bad_inputs(dev):
     from moss_tts._runtime import w4g32
 
@@ -180,7 +239,7 @@ def test_gemv_rejects_bad_inputs(dev):
 
 # ------------------------------------------------------------------- prefill GEMM
 @pytest.mark.parametrize("m,k,n", [(2, 64, 8), (16, 128, 64), (100, 512, 200), (128, 4096, 128), (512, 1024, 4096),
-                                   (37, 4096, 32800), (512, 4096, 6144), (512, 12288, 4096),
+                                   (37, 4096, 32800), (512, 4096, 6144), (512, 12288, 4096), (512, 4096, 4096),
                                    # the 128 x 128 tile at full size, with ragged M and N, and an odd step count
                                    (512, 4096, 24576), (300, 1024, 32808), (260, 1088, 16448),
                                    # register-weight tile with a 16-group last zero-point chunk (G = 144)

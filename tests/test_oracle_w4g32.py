@@ -9,8 +9,12 @@ import numpy as np
 import pytest
 import torch
 
+from fractions import Fraction
+
 from oracle import cref
 from oracle import w4g32 as o
+
+from helpers import rn_f32
 
 
 def _bits(t):
@@ -197,6 +201,81 @@ def test_static_scales_known_answers():
     out = _bits(o.static_scales(w))
     assert out[0].tolist() == [0x3F80, 0x4000]
     assert out[1, 0] == o.f32_to_bf16_bits(np.array([np.float32(1e-8) / np.float32(7)], dtype=np.float32))[0]
+
+
+def test_rowpack_f32_dequant_equals_oracle_dequant():
+    """The threaded full-size dequant of the row-packed layout equals ``dequantize(rowunpack(...))``
+    bit for bit, including a ragged last 128-group block of zero points (K = 4096 + 2048)."""
+    g = torch.Generator().manual_seed(13)
+    for n, k in ((40, 256), (8, 6144)):
+        q = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8)
+        z = torch.randint(0, 16, (n, k // 32), generator=g, dtype=torch.uint8)
+        s = (torch.rand((n, k // 32), generator=g) * 0.01 + 1e-4).bfloat16()
+        qw, sc, zp = o.rowpack(q, z, s)
+        got = o.dequantize_rowpack_f32(qw, sc, zp)
+        assert torch.equal(got, o.dequantize(q, z, s).float())
+
+
+def _symmetric_brute(w, s):
+    """calibrated_quant.py:74-77 by brute force: the fp32 quotient w / s formed exactly and rounded
+    once to float32, then the nearest of the 15 levels -7..7 (exact rational distances), ties to the
+    even level."""
+    out = []
+    for v, sv in zip(w, s):
+        q = Fraction(rn_f32(Fraction(float(v)) / Fraction(float(sv))))
+        best = min(range(-7, 8), key=lambda c: (abs(q - c), c % 2))
+        out.append(best)
+    return out
+
+
+def test_quantize_symmetric_brute_force():
+    """Random weights of many magnitudes against their own static scales (the export recipe), and
+    scales that are not the group's own (so clamping happens): every code is the brute-force level."""
+    g = torch.Generator().manual_seed(11)
+    mags = 2.0 ** torch.randint(-20, 4, (24, 1), generator=g).float()
+    w = torch.randn((24, 64), generator=g) * mags
+    w[torch.rand((24, 64), generator=g) < 0.05] = 0
+    for s in (o.static_scales(w), (o.static_scales(w).float() * 0.37).bfloat16()):
+        c = o.quantize_symmetric(w, s)
+        sf = s.float().repeat_interleave(32, 1)
+        for r in range(w.shape[0]):
+            assert c[r].tolist() == _symmetric_brute(w[r].tolist(), sf[r].tolist()), r
+    assert o.quantize_symmetric(w, o.static_scales(w)).abs().max() <= 7
+
+
+def test_quantize_symmetric_ties_and_clamps():
+    """Crafted cases at scale 1 and 0.25: exact half-way values go to the even level, values past
+    +-7.5 clamp to +-7, and a zero group (scale floor 1e-8 / 7) gives zero codes."""
+    vals = [0.5, 1.5, 2.5, -2.5, 3.5, -3.5, 6.5, -6.5, 7.5, -7.5, 7.49, 8.0, -100.0, 1e30, -0.0, 0.0,
+            4.5, 5.5, -0.5, -1.5, 2.4999, 2.5001, 3.0, -7.0, 9.5, -8.5, 0.75, 1.25, 5.0, 6.0, 6.9, -6.9]
+    want = [0, 2, 2, -2, 4, -4, 6, -6, 7, -7, 7, 7, -7, 7, 0, 0,
+            4, 6, 0, -2, 2, 3, 3, -7, 7, -7, 1, 1, 5, 6, 7, -7]
+    for scale in (1.0, 0.25):
+        w = torch.tensor([vals], dtype=torch.float32) * scale
+        s = torch.full((1, 1), scale).bfloat16()
+        assert o.quantize_symmetric(w, s)[0].tolist() == want
+    z = torch.zeros((1, 32))
+    assert not o.quantize_symmetric(z, o.static_scales(z)).any()
+
+
+def test_cpu_baseline_dequant_and_linear_match_oracle():
+    """The CPU baseline (AutoGPTQ layout, dequantized on every call) against the oracle on the same
+    codes: the bf16 weights are bit for bit ``dequantize``'s (transposed), the fp32 outputs agree
+    with ``w4g32_linear`` to fp32 summation order (both are F.linear on the same bf16 weights)."""
+    g = torch.Generator().manual_seed(12)
+    w = torch.randn((96, 256), generator=g) * 0.02
+    q, z, s = o.quantize_minmax_g32(w)
+    qweight, scales, qzeros = o.pack_gptq(q, z, s)
+    wd = o.gptq_dequant_cpu(qweight, scales, qzeros)
+    assert np.array_equal(_bits(wd.t().contiguous()), _bits(o.dequantize(q, z, s)))
+    x = torch.randn((3, 256), generator=g).bfloat16()
+    got = o.gptq_dequant_linear_cpu(x, qweight, scales, qzeros)
+    ref = o.w4g32_linear(x, q, z, s)
+    bound = 1e-6 * (x.float().abs() @ o.dequantize(q, z, s).float().abs().t()) + 1e-30
+    assert torch.all((got - ref).abs() <= bound)
+    # a planted swap of code and zero nibble order would change the weights
+    bad = o.gptq_dequant_cpu(qweight, scales, torch.flip(qzeros, [1]))
+    assert not np.array_equal(_bits(bad), _bits(wd))
 
 
 # ----------------------------------------------------------------- linear contracts
