@@ -100,6 +100,18 @@ int moss_w4g32_norm_gateup_silu(const void *x, const void *res, const void *norm
                                 const void *qw, const void *sc, const void *zp, void *y, int K, int N_half,
                                 int rows_per_wave, int dequant_mode, void *stream);
 
+/* --------------------------------------------------- bf16-weight decode GEMV */
+/* y bf16 [N] = bf16(sum_k f32(W[n,k]) * f32(x[k])), W bf16 [N, K] row-major (16-byte aligned), fp32
+ * accumulate; K % 512 == 0, K / 512 in {1..8, 12, 16}; rows_per_wave in {0 (auto), 1, 2, 4}.  The
+ * reference's bf16 decode projection: linear_decode / _gemv, src/moss_tts/_runtime/kernels.py:93-108,
+ * and F.linear of the output heads, src/moss_tts/_runtime/llm.py:270-279. */
+int moss_bf16_gemv(const void *x, const void *w, void *y, int K, int N, int rows_per_wave, void *stream);
+
+/* The same behind the fused (add+)RMSNorm of moss_w4g32_norm_gemv (same argument rules): the final
+ * norm + audio/text heads of the decode step, src/moss_tts/_runtime/llm.py:188-191,264-279. */
+int moss_bf16_norm_gemv(const void *x, const void *res, const void *norm_w, void *sum_out, float eps, const void *w,
+                        void *y, int K, int N, int rows_per_wave, void *stream);
+
 /* ------------------------------------------------- W4A8 G32 decode mode */
 /* The reference's serving arithmetic: activations quantized to int8 per group of 32, integer
  * dot products against the INT4 codes, fp32 group combine.  Quantized activations ("qact",

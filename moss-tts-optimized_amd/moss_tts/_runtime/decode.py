@@ -5,8 +5,9 @@ add-RMSNorm + q||k||v GEMV (one kernel) -> q/k head-norm + RoPE + KV write + spl
 attention (one kernel) -> split merge -> O GEMV -> add-RMSNorm + gate||up GEMV with SiLU*mul
 (one kernel) -> down GEMV.  The step starts with the
 33-row embedding sum (``src/moss_tts/_runtime/kernels.py:7-26``) and ends with the final norm
-and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``),
-here INT4-G32 as well.  With ``w4a8`` the four layer projections run the reference's serving
+and the 32 concatenated audio-codebook heads (``src/moss_tts/_runtime/llm.py:188-191,271-279``):
+bf16 for an installed model, as the reference keeps them, or INT4-G32 for the synthetic
+36-layer benchmark step.  With ``w4a8`` the four layer projections run the reference's serving
 arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
 ``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer + q||k||v (one
 kernel) -> attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer ->
@@ -26,8 +27,8 @@ from dataclasses import dataclass
 
 import torch
 
-from . import attention, sampling, w4a8, w4g32
-from .modules import QuantGateUpG32, QuantLinearG32
+from . import attention, bf16, sampling, w4a8, w4g32
+from .modules import Bf16Linear, QuantGateUpG32, QuantLinearG32
 from .w4g32 import _require
 
 HIDDEN, INTER, QH, KH, HD = 4096, 12288, 32, 8, 128
@@ -68,7 +69,7 @@ class DecodeStepG32:
     are ``[1, 8, max_length, 128]`` bf16 per layer and kind, like the reference's StaticCache
     (``src/moss_tts/_runtime/llm.py:192-193``)."""
 
-    def __init__(self, layers: list[DecoderLayerG32], final_norm: torch.Tensor, heads: QuantLinearG32,
+    def __init__(self, layers: list[DecoderLayerG32], final_norm: torch.Tensor, heads: QuantLinearG32 | Bf16Linear,
                  text_embedding: torch.Tensor, audio_embedding: torch.Tensor, *, max_length: int,
                  eps: float = 1e-6, theta: float = 1e6, w4a8: bool = False, audio_stride: int = AUDIO_VOCAB,
                  greedy: bool = False, seed: int = 0, text_ids=(GEN_SLOT_ID, DELAY_SLOT_ID),
@@ -112,7 +113,7 @@ class DecodeStepG32:
         self.logits = None
 
     # ------------------------------------------------------------------ forward
-    def forward(self, head_count: int = CODEBOOKS) -> torch.Tensor:
+    def forward(self, head_count: int = CODEBOOKS, trace: list | None = None) -> torch.Tensor:
         """One step from the static ``ids``/``position`` buffers -> logits bf16 ``[N_heads]``.
         Every (add+)RMSNorm runs inside the projection that consumes it (``norm_gemv``).
         ``head_count`` < 32 computes and samples only the first ``head_count`` audio heads: valid
@@ -120,15 +121,20 @@ class DecodeStepG32:
         (``src/moss_tts/_runtime/llm.py:272-279``, ``audio_head_buckets.py``).  The reference fills
         the skipped heads with zeros and samples all 32 rows to keep torch's RNG sequence; here each
         row's Philox draw is independent of the others, so the skipped rows are left unwritten and
-        unsampled and the emitted ids are those of the full step."""
+        unsampled and the emitted ids are those of the full step.  ``trace`` (eager runs only): a list
+        that receives, per layer, copies of the stream state it started from (``residual_in``,
+        ``mlp_in``) and of its intermediates (``qkv``, ``attn``, ``o``, ``act``, ``mlp``, ``residual``),
+        for layer-by-layer checks."""
         _require(head_count in (8, 16, 24, CODEBOOKS), "head_count must be 8, 16, 24 or 32")
         if self.w4a8:
+            _require(trace is None, "trace is available in the W4A16 step")
             return self._forward_w4a8(head_count)
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
         mlp = None
         for i, layer in enumerate(self.layers):
+            state = (residual.clone(), None if mlp is None else mlp.clone()) if trace is not None else None
             if i == 0:
                 qkv = w4g32.norm_gemv(x, layer.input_norm, eps, layer.qkv.packed, dequant=layer.qkv.dequant)
             else:
@@ -140,25 +146,34 @@ class DecodeStepG32:
             residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
                                                    residual=residual, dequant=layer.gate_up.dequant)
             mlp = layer.down(act)
+            if trace is not None:
+                trace.append(dict(residual_in=state[0], mlp_in=state[1], qkv=qkv.clone(), attn=attn.clone(),
+                                  o=o.clone(), act=act.clone(), mlp=mlp.clone(), residual=residual.clone()))
         logits = self._heads(mlp, residual, head_count)
         self._sample(logits, head_count)
         return logits
 
     def _heads(self, mlp: torch.Tensor, residual: torch.Tensor, head_count: int) -> torch.Tensor:
-        """Final add-RMSNorm + the INT4 heads: all rows, or the first ``head_count`` audio heads
-        and the 2 text rows written into one full-size logits buffer."""
+        """Final add-RMSNorm + the heads (bf16 as the reference keeps them, or INT4-G32): all rows,
+        or the first ``head_count`` audio heads and the 2 text rows written into one full-size
+        logits buffer."""
         eps, heads = self.eps, self.heads
+
+        def run(start, stop, out=None):
+            if isinstance(heads, Bf16Linear):
+                w = heads.weight if (start, stop) == (0, heads.out_features) else heads.weight[start:stop]
+                return bf16.norm_gemv(mlp, self.final_norm, eps, w, residual=residual, out=out)[1]
+            w = heads.packed if (start, stop) == (0, heads.out_features) else heads.packed.rows(start, stop)
+            return w4g32.norm_gemv(mlp, self.final_norm, eps, w, residual=residual, dequant=heads.dequant,
+                                   out=out)[1]
+
         if head_count == CODEBOOKS:
-            _, logits = w4g32.norm_gemv(mlp, self.final_norm, eps, heads.packed, residual=residual,
-                                        dequant=heads.dequant)
-            return logits.view(-1)
+            return run(0, heads.out_features).view(-1)
         n_audio = CODEBOOKS * self.audio_stride
         logits = torch.empty(heads.out_features, device=self.device, dtype=torch.bfloat16)
         rows = head_count * self.audio_stride
-        w4g32.norm_gemv(mlp, self.final_norm, eps, heads.packed.rows(0, rows), residual=residual,
-                        dequant=heads.dequant, out=logits[:rows])
-        w4g32.norm_gemv(mlp, self.final_norm, eps, heads.packed.rows(n_audio, n_audio + 2), residual=residual,
-                        dequant=heads.dequant, out=logits[n_audio:])
+        run(0, rows, logits[:rows])
+        run(n_audio, n_audio + 2, logits[n_audio:])
         return logits
 
     def _sample(self, logits: torch.Tensor, head_count: int = CODEBOOKS) -> None:
@@ -237,7 +252,8 @@ class DecodeStepG32:
 
     @seed.setter
     def seed(self, value: int) -> None:
-        self.seed_buf.fill_(sampling.seed_value(int(value)))
+        with torch.inference_mode():
+            self.seed_buf.fill_(sampling.seed_value(int(value)))
 
     @torch.inference_mode()
     def decode(self, ids: torch.Tensor, position: int, audio_length: int = CODEBOOKS,
@@ -256,7 +272,8 @@ class DecodeStepG32:
 
     @property
     def weight_bytes(self) -> int:
-        return sum(layer.nbytes for layer in self.layers) + self.heads.packed.nbytes
+        heads = self.heads.nbytes if isinstance(self.heads, Bf16Linear) else self.heads.packed.nbytes
+        return sum(layer.nbytes for layer in self.layers) + heads
 
     def step_bytes(self, position: int) -> int:
         """Algorithmic HBM bytes of one step at ``position``: packed weights and heads, the
@@ -267,11 +284,12 @@ class DecodeStepG32:
     # ------------------------------------------------------------ installed model
     @classmethod
     @torch.no_grad()
-    def from_model(cls, model, *, max_length: int, dequant: int = w4g32.EXACT, w4a8: bool = False) -> "DecodeStepG32":
+    def from_model(cls, model, *, max_length: int, w4a8: bool = False) -> "DecodeStepG32":
         """The decode step of a MOSS-TTS model after ``install_gptq``: its quantized projections,
-        norm weights and embeddings as they are (no copies); the 32 audio heads (rows
-        ``[:1024]`` of ``lm_heads[1:]``, ``src/moss_tts/_runtime/llm.py:188-191``) concatenated
-        and min-max quantized to INT4-G32 here (the reference keeps them bf16)."""
+        norm weights and embeddings as they are (no copies); the 32 audio heads (rows ``[:1024]`` of
+        ``lm_heads[1:]``) and the gen-slot / delay-slot rows of the text head concatenated into one
+        bf16 matrix, as the reference keeps them (``src/moss_tts/_runtime/llm.py:188-191``), applied
+        by the bf16 GEMV behind the fused final norm."""
         lm = model.language_model
         layers = []
         for i, layer in enumerate(lm.layers):
@@ -294,8 +312,8 @@ class DecodeStepG32:
         if not all(0 <= int(t) < text_head.shape[0] for t in cfg_ids):
             raise ValueError("the gen-slot / delay-slot token ids are outside the text head")
         text_rows = text_head[torch.tensor([int(t) for t in cfg_ids], device=text_head.device)]
-        heads_bf16 = torch.cat([h.weight[:SAMPLED_CODES] for h in model.lm_heads[1:]] + [text_rows], 0)
-        heads = QuantLinearG32(w4g32.quantize_minmax(heads_bf16.float().contiguous()), dequant=dequant)
+        heads = Bf16Linear(torch.cat([h.weight[:SAMPLED_CODES] for h in model.lm_heads[1:]] + [text_rows], 0)
+                           .bfloat16().contiguous())
         audio = torch.stack([e.weight for e in model.emb_ext]).contiguous()
         return cls(layers, lm.norm.weight, heads, lm.embed_tokens.weight.contiguous(), audio,
                    max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6, w4a8=w4a8,
@@ -308,9 +326,11 @@ class DecodeStepG32:
     @torch.inference_mode()
     def random(cls, n_layers: int, *, max_length: int, device, seed: int = 0, text_vocab: int = 151936,
                kv_fill: bool = True, dequant: int = w4g32.EXACT, w4a8: bool = False, greedy: bool = False,
-               sample_seed: int = 0) -> "DecodeStepG32":
+               sample_seed: int = 0, bf16_heads: bool = False) -> "DecodeStepG32":
         """Random-init Qwen3-8B-shaped weights (N(0, 0.02), min-max INT4-G32 quantized on the
-        device), norm weights 1 + N(0, 0.01), embeddings N(0, 1), KV caches N(0, 1)."""
+        device), norm weights 1 + N(0, 0.01), embeddings N(0, 1), KV caches N(0, 1).  The heads are
+        INT4-G32 (32 x 1025 + 2 rows), or with ``bf16_heads`` bf16 N(0, 0.02) as an installed model
+        has them (32 x 1024 + 2 rows)."""
         dev = torch.device(device)
         gen = torch.Generator(device=dev).manual_seed(seed)
 
@@ -326,11 +346,17 @@ class DecodeStepG32:
         layers = [DecoderLayerG32(q((QH + 2 * KH) * HD, HIDDEN), q(HIDDEN, QH * HD),
                                   q(2 * INTER, HIDDEN, QuantGateUpG32), q(HIDDEN, INTER),
                                   norm(HIDDEN), norm(HIDDEN), norm(HD), norm(HD)) for _ in range(n_layers)]
-        heads = q(CODEBOOKS * AUDIO_VOCAB + 2, HIDDEN)  # 32 audio heads of 1025 rows, then the 2 text rows
+        if bf16_heads:
+            stride = SAMPLED_CODES
+            heads = Bf16Linear((torch.randn((CODEBOOKS * stride + 2, HIDDEN), generator=gen, device=dev) * 0.02)
+                               .bfloat16())
+        else:
+            stride = AUDIO_VOCAB
+            heads = q(CODEBOOKS * stride + 2, HIDDEN)  # 32 audio heads of 1025 rows, then the 2 text rows
         text = torch.randn((text_vocab, HIDDEN), generator=gen, device=dev).bfloat16()
         audio = torch.randn((CODEBOOKS, AUDIO_VOCAB, HIDDEN), generator=gen, device=dev).bfloat16()
         eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length, w4a8=w4a8, greedy=greedy,
-                  seed=sample_seed)
+                  seed=sample_seed, audio_stride=stride)
         if kv_fill:
             for t in eng.keys + eng.values:
                 t.copy_(torch.randn(t.shape, generator=gen, device=dev))

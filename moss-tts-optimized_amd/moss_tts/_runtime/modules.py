@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import w4g32
+from . import bf16, w4g32
 from .w4g32 import PackedW4G32, _require
 
 
@@ -66,3 +66,29 @@ class QuantGateUpG32(QuantLinearG32):
         from . import pointwise
 
         return pointwise.silu_mul(w4g32.gemm(x.contiguous(), self.packed))
+
+
+class Bf16Linear(nn.Module):
+    """bf16 weight ``[N, K]`` applied to one row with the bf16 decode GEMV (fp32 accumulate): the
+    reference's bf16 output heads (``src/moss_tts/_runtime/llm.py:188-191,270-279``).  The weight is
+    held as given (a contiguous buffer, no copy)."""
+
+    def __init__(self, weight: torch.Tensor):
+        super().__init__()
+        _require(isinstance(weight, torch.Tensor) and weight.ndim == 2 and weight.dtype == torch.bfloat16,
+                 "a 2-D bf16 weight [out, in] is required")
+        self.in_features = weight.shape[1]
+        self.out_features = weight.shape[0]
+        self.register_buffer("weight", weight.detach().contiguous(), persistent=True)
+
+    @property
+    def nbytes(self) -> int:
+        return self.weight.numel() * self.weight.element_size()
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        _require(x.shape[-1] == self.in_features, f"expected {self.in_features} input features")
+        _require(x.numel() == self.in_features, "the bf16 heads run on one row (the decode step's last token)")
+        return bf16.gemv(x.contiguous(), self.weight)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, dtype=bf16"

@@ -38,6 +38,8 @@ SIGNATURES: dict[str, list] = {
     "moss_gemm_workspace_bytes": [_I, _I, _I],
     "moss_w4g32_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_w4g32_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "moss_bf16_gemv": [_P, _P, _P, _I, _I, _I, _P],
+    "moss_bf16_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P],
     "moss_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "moss_qk_norm_rope_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _P],
     "moss_silu_mul": [_P, _P, _I, _I, _P],

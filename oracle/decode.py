@@ -22,32 +22,51 @@ from . import w4a8 as o8
 from . import w4g32 as ow
 
 
-def decode_step(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):
+def decode_layer(L, i, residual, mlp, position, keys, values, cos, sin, eps=1e-6, linear=None):
+    """One layer of the step (``src/moss_tts/_runtime/llm.py:227-260``) from the stream state
+    ``(residual, mlp)`` (``mlp`` None at layer 0, where ``residual`` is the embedding).  Returns the
+    layer's intermediates ``qkv, attn, o, act, mlp`` and the new ``residual`` (bf16 ``[1, n]``).
+    ``linear(h, w)`` is the fp32 product (default ``F.linear(h.float(), w.float())``)."""
+    lin = linear or ow.linear
+    p = int(position)
+    if mlp is None:
+        h = op.rmsnorm(residual, L["input_norm"], eps)
+    else:
+        residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
+    qkv = lin(h, L["qkv"]).bfloat16()
+    q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],
+                           torch.tensor([p]), eps)
+    attn = oa.decode_attention(q, keys[i], values[i], p).bfloat16().view(1, -1)
+    o = lin(attn, L["o"]).bfloat16()
+    residual, h = op.add_rmsnorm(o, residual, L["post_norm"], eps)
+    y = lin(h, L["gate_up"])
+    n = y.shape[1] // 2
+    act = ow.silu_mul_rounded(y[:, :n], y[:, n:])
+    mlp = lin(act, L["down"]).bfloat16()
+    return dict(qkv=qkv, attn=attn, o=o, act=act, mlp=mlp, residual=residual)
+
+
+def decode_step(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6,
+                linear=None):
     """``layers``: an iterable of dicts with bf16 dequantized ``qkv``, ``o``, ``gate_up``, ``down``
     weights (or fp32 tensors holding bf16 values) and ``input_norm``, ``post_norm``, ``q_norm``,
     ``k_norm``; it is consumed once, in order, so a generator can dequantize one layer at a time.
     ``keys``/``values`` lists of ``[1, 8, L, 128]`` caches (updated in place).  Returns bf16 logits."""
-    p = int(position)
-    x = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
-    residual = x
+    lin = linear or ow.linear
+    residual = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
     mlp = None
     for i, L in enumerate(layers):
-        if i == 0:
-            h = op.rmsnorm(x, L["input_norm"], eps)
-        else:
-            residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
-        qkv = ow.linear(h, L["qkv"]).bfloat16()
-        q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],
-                               torch.tensor([p]), eps)
-        attn = oa.decode_attention(q, keys[i], values[i], p).bfloat16().view(1, -1)
-        o = ow.linear(attn, L["o"]).bfloat16()
-        residual, h = op.add_rmsnorm(o, residual, L["post_norm"], eps)
-        y = ow.linear(h, L["gate_up"])
-        n = y.shape[1] // 2
-        a = ow.silu_mul_rounded(y[:, :n], y[:, n:])
-        mlp = ow.linear(a, L["down"]).bfloat16()
+        out = decode_layer(L, i, residual, mlp, position, keys, values, cos, sin, eps, lin)
+        residual, mlp = out["residual"], out["mlp"]
     _, h = op.add_rmsnorm(mlp, residual, final_norm, eps)
-    return ow.linear(h, heads_w).bfloat16().view(-1)
+    return lin(h, heads_w).bfloat16().view(-1)
+
+
+def reversed_linear(h: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``F.linear`` with the K axis reversed: the same exact products summed in another fp32 order.
+    The distance between ``decode_step`` with it and without it measures how far summation order
+    alone moves a composed step (the oracle's own noise floor)."""
+    return torch.nn.functional.linear(h.float().flip(-1), w.float().flip(-1))
 
 
 def decode_step_w4a8(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):

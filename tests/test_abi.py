@@ -87,6 +87,11 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_fp8_linear(p, p, null, p, 2, 4112, 64, 0, null, 0, null) == 1      # GEMM K % 64
     assert lib.moss_fp8_gateup_silu(p, p, null, p, 2, 4096, 64, 0, null) == 1           # M must be 1
     assert lib.moss_fp8_to_bf16(p, p, 6, null) == 1                                     # count % 4
+    assert lib.moss_bf16_gemv(p, p, p, 4608, 64, 0, null) == 1                           # K / 512 = 9
+    assert lib.moss_bf16_gemv(p, p, p, 4000, 64, 0, null) == 1                           # K % 512
+    assert lib.moss_bf16_gemv(p, odd, p, 4096, 64, 0, null) == 1                         # weight alignment
+    assert lib.moss_bf16_gemv(p, p, p, 4096, 64, 3, null) == 1                           # rows_per_wave
+    assert lib.moss_bf16_norm_gemv(p, null, p, null, ctypes.c_float(1e-6), p, p, 4608, 64, 0, null) == 1  # K
     assert lib.moss_rmsnorm(p, null, p, null, p, 1, 8200, ctypes.c_float(1e-6), null) == 1   # n <= 8192
     assert lib.moss_int8_quantize_g32(p, p, p, p, 40, null) == 1                           # K % 32
     assert lib.moss_rmsnorm_quant_g32(p, null, p, null, null, p, p, p, 1, 4112, ctypes.c_float(1e-6), null) == 1

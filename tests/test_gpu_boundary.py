@@ -6,7 +6,8 @@ export (module swap) and captures the decode step.
 Bars: installed weights equal the reference's dequant of the export bit for bit; the model's
 own (rebound) MLP forward at M=1 (GEMV) and M=64 (GEMM) meets 1e-2 atol + 1e-2 rtol against
 dequant-then-matmul; the captured decode step's logits are within 2e-2 relative L2 of the
-oracle's composed step (the same bound as the synthetic decode test)."""
+oracle's composed step (the same bound as the synthetic decode test), whose heads are the model's
+own bf16 head rows."""
 import os
 from types import SimpleNamespace
 
@@ -68,7 +69,7 @@ def _export(model, folder):
 def test_from_pretrained_install_and_decode(dev, tmp_path):
     from moss_tts import MossTTS
     from moss_tts._runtime import w4g32
-    from moss_tts._runtime.modules import QuantGateUpG32, QuantLinearG32
+    from moss_tts._runtime.modules import Bf16Linear, QuantGateUpG32, QuantLinearG32
     from moss_tts._runtime.presets import install_gptq
 
     print("boundary: building the one-layer model", flush=True)
@@ -105,7 +106,11 @@ def test_from_pretrained_install_and_decode(dev, tmp_path):
     ids = torch.tensor([[17] + [i * 29 % 1025 for i in range(32)]], dtype=torch.int64)
     position = 5
     logits = tts.step(ids, position).float().cpu()
-    heads = w4g32.dequantize(eng.heads.packed).cpu()
+    # the heads stay bf16, as the reference keeps them (llm.py:188-191): audio rows [:1024] of the
+    # 32 codebook heads, then the gen-slot / delay-slot rows of the text head
+    heads = torch.cat([h.weight[:1024] for h in model.lm_heads[1:]] +
+                      [model.lm_heads[0].weight[[100, 101]]]).detach().cpu()
+    assert isinstance(eng.heads, Bf16Linear) and torch.equal(eng.heads.weight.cpu(), heads)
     L0 = dict(qkv=deq["qkv"], o=deq["out"], gate_up=deq["up"], down=deq["down"],
               input_norm=layer.input_layernorm.weight.detach().cpu(),
               post_norm=layer.post_attention_layernorm.weight.detach().cpu(),

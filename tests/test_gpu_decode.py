@@ -7,6 +7,7 @@ position says (the other rows untouched)."""
 import pytest
 import torch
 
+from oracle import attention as oa
 from oracle import decode as od
 from oracle import w4g32 as o
 
@@ -55,13 +56,23 @@ def test_decode_step_two_layers(dev):
 def test_decode_step_full_size(dev):
     """The benchmarked configuration itself: 36 layers, KV capacity 2048 filled with N(0,1), the
     token at position 2047, INT4 heads N = 32 x 1025 + 2, run as the captured graph.  The oracle runs
-    the same step one layer at a time on the CPU (each layer dequantized from the engine's packed
-    weights by the oracle's own unpack), so memory stays at one layer.  Bars: relative L2 of the
-    logits < 2e-2; K/V row 2047 of layers 0 and 35 within the composed drift; every other row of
-    those layers untouched."""
+    on the CPU one layer at a time (each layer dequantized from the engine's packed weights by the
+    oracle's own unpack), so memory stays at one layer.
+
+    * The graph's logits and K/V rows equal an eager run of the same step bit for bit.
+    * Layer by layer (teacher forcing): each oracle layer starts from the GPU's own stream state at
+      that layer; every intermediate (q||k||v, attention, O, SiLU*mul, down, residual) and the K/V
+      row it writes are within relative L2 1e-2 of the GPU's (measured <= 3e-3), and so are the
+      heads' logits from the GPU's final state.  This is the per-operation bar at full size.
+    * End to end: a 36-layer random stack carries any summation-order difference forward, and at
+      this size it reaches about 2e-2 for the oracle against itself with the K axis of every
+      product summed in reverse (``reversed_linear``).  The free-running GPU logits must be within
+      max(2e-2, 1.5x that self-distance) of the free-running oracle; rows of the cache other than
+      2047 are untouched."""
     import time
 
     from moss_tts._runtime.decode import DecodeStepG32
+    from oracle import pointwise as op
 
     print("decode step: 36 layers, L=2048, p=2047 (graph replay)", flush=True)
     L, position, n_layers = 2048, 2047, 36
@@ -71,8 +82,20 @@ def test_decode_step_full_size(dev):
     values0 = [v.cpu() for v in eng.values]
     ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
     logits = eng.step(ids, position).float().cpu()
+    kv_graph = [(eng.keys[i][:, :, position].cpu(), eng.values[i][:, :, position].cpu()) for i in range(n_layers)]
+    trace = []
+    with torch.inference_mode():
+        eager = eng.forward(trace=trace).float().cpu()
     torch.cuda.synchronize()
+    assert torch.equal(eager, logits), "graph replay differs from the eager step"
+    for i in range(n_layers):
+        assert torch.equal(eng.keys[i][:, :, position].cpu(), kv_graph[i][0])
+        assert torch.equal(eng.values[i][:, :, position].cpu(), kv_graph[i][1])
+    for i in (0, n_layers - 1):
+        assert torch.equal(eng.keys[i][:, :, :position].cpu(), keys0[i][:, :, :position])
+        assert torch.equal(eng.values[i][:, :, :position].cpu(), values0[i][:, :, :position])
     print("GPU step done; oracle layer by layer", flush=True)
+
     bufs = {}
 
     def deq(name, m):
@@ -80,33 +103,54 @@ def test_decode_step_full_size(dev):
             bufs[name] = torch.empty(m.N * m.K)
         return o.dequantize_rowpack_f32(m.qw.cpu(), m.scales.cpu(), m.zeros.cpu(), out=bufs[name])
 
-    def layers():
-        t0 = time.time()
-        for i, l in enumerate(eng.layers):
-            yield dict(qkv=deq("qkv", l.qkv.packed), o=deq("o", l.o.packed), gate_up=deq("gate_up", l.gate_up.packed),
-                       down=deq("down", l.down.packed), input_norm=l.input_norm.cpu(), post_norm=l.post_norm.cpu(),
-                       q_norm=l.q_norm.cpu(), k_norm=l.k_norm.cpu())
-            if i % 6 == 5:
-                print(f"  oracle layer {i + 1}/{n_layers} ({time.time() - t0:.1f} s)", flush=True)
+    def rel(a, b):
+        a, b = a.float().flatten(), b.float().flatten()
+        return float((a - b).norm() / b.norm())
 
-    keys = [k.clone() for k in keys0]
-    values = [v.clone() for v in values0]
-    heads = eng.heads.packed
-    ref = od.decode_step(layers(), eng.final_norm.cpu(), deq("heads", heads), eng.text_embedding.cpu(),
-                         eng.audio_embedding.cpu(), ids, position, keys, values, eng.cos.cpu(), eng.sin.cpu())
-    ref = ref.float()
-    rel = float((logits - ref).norm() / ref.norm())
-    print(f"relative L2 error of logits: {rel:.3e}", flush=True)
-    assert rel < 2e-2
-    for i in (0, n_layers - 1):
-        got_k, got_v = eng.keys[i].cpu(), eng.values[i].cpu()
-        assert torch.equal(got_k[:, :, :position], keys0[i][:, :, :position])
-        assert torch.equal(got_v[:, :, :position], values0[i][:, :, :position])
-        for got, want in ((got_k, keys[i]), (got_v, values[i])):
-            g_row, r_row = got[:, :, position].float(), want[:, :, position].float()
-            rel_row = float((g_row - r_row).norm() / r_row.norm())
-            print(f"layer {i} KV row {position}: relative L2 {rel_row:.3e}", flush=True)
-            assert rel_row < 2e-2
+    cos, sin, eps = eng.cos.cpu(), eng.sin.cpu(), eng.eps
+    caches = {m: ([k.clone() for k in keys0], [v.clone() for v in values0]) for m in ("tf", "free", "rev")}
+    text, audio = eng.text_embedding.cpu(), eng.audio_embedding.cpu()
+    x0 = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
+    assert torch.equal(trace[0]["residual_in"].cpu(), x0)
+    state = {"free": (x0, None), "rev": (x0, None)}
+    worst, t0 = 0.0, time.time()
+    for i, l in enumerate(eng.layers):
+        lw = dict(qkv=deq("qkv", l.qkv.packed), o=deq("o", l.o.packed), gate_up=deq("gate_up", l.gate_up.packed),
+                  down=deq("down", l.down.packed), input_norm=l.input_norm.cpu(), post_norm=l.post_norm.cpu(),
+                  q_norm=l.q_norm.cpu(), k_norm=l.k_norm.cpu())
+        t = trace[i]
+        mlp_in = None if t["mlp_in"] is None else t["mlp_in"].cpu()
+        ref = od.decode_layer(lw, i, t["residual_in"].cpu(), mlp_in, position, *caches["tf"], cos, sin, eps)
+        for key in ("qkv", "attn", "o", "act", "mlp", "residual"):
+            err = rel(t[key].cpu(), ref[key])
+            worst = max(worst, err)
+            assert err < 1e-2, f"layer {i} {key}: relative L2 {err:.3e}"
+        for got, want in ((kv_graph[i][0], caches["tf"][0][i]), (kv_graph[i][1], caches["tf"][1][i])):
+            err = rel(got, want[:, :, position])
+            assert err < 1e-2, f"layer {i} KV row: relative L2 {err:.3e}"
+        for mode, lin in (("free", None), ("rev", od.reversed_linear)):
+            out = od.decode_layer(lw, i, *state[mode], position, *caches[mode], cos, sin, eps, lin)
+            state[mode] = (out["residual"], out["mlp"])
+        if i % 6 == 5:
+            print(f"  oracle layer {i + 1}/{n_layers} ({time.time() - t0:.1f} s); worst layer error {worst:.2e}",
+                  flush=True)
+    heads_w = deq("heads", eng.heads.packed)
+    final = eng.final_norm.cpu()
+
+    def head(res, mlp, lin=o.linear):
+        _, h = op.add_rmsnorm(mlp, res, final, eps)
+        return lin(h, heads_w).bfloat16().float().view(-1)
+
+    err = rel(logits, head(trace[-1]["residual"].cpu(), trace[-1]["mlp"].cpu()))
+    print(f"heads from the GPU's final state: relative L2 {err:.3e}", flush=True)
+    assert err < 1e-2
+    free = head(*state["free"])
+    rev = head(*state["rev"], od.reversed_linear)
+    e2e, self_dist = rel(logits, free), rel(rev, free)
+    bar = max(2e-2, 1.5 * self_dist)
+    print(f"end to end: GPU vs oracle {e2e:.3e}; oracle vs reversed-order oracle {self_dist:.3e}; bar {bar:.3e}",
+          flush=True)
+    assert e2e < bar and bar <= 5e-2
 
 
 def test_decode_graph_replay_matches_eager(dev):
