@@ -17,6 +17,9 @@
  *   zp  uint8  [N, G/2]  blocks of 128 groups: for block c (r = min(128, G-128c) groups)
  *                        byte 64c+b = z[128c+b] | z[128c+r/2+b] << 4
  *   w[n,k] = bf16_rne(float(q - z) * float(s))
+ * The GEMVs' exact mode and the GEMMs form that value in registers from (128+q)*s - (128+z)*s in
+ * fp32, exact for every scale below 2^120 (subnormal scales included); moss_w4g32_dequant_bf16 is
+ * exact for every finite scale.  The Python loaders reject scales at or above 2^120.
  */
 #ifndef MOSS_HIP_H
 #define MOSS_HIP_H

@@ -35,6 +35,20 @@ def _aligned(t: torch.Tensor, a: int) -> bool:
     return t.data_ptr() % a == 0
 
 
+#: Scales must lie below this bound: the decode GEMV's exact mode and the prefill GEMM form the
+#: bit-exact dequant from (128 + q) * s and (128 + z) * s in fp32, which stay finite only for
+#: s < 2^120.8 (``moss_w4g32_dequant_bf16`` is exact for every finite scale).  Real group scales
+#: are many orders of magnitude smaller (absmax / 7 of bf16 weights).
+MAX_SCALE = 2.0 ** 120
+
+
+def _check_scales(scales: torch.Tensor) -> None:
+    """Raise unless every scale is finite and below :data:`MAX_SCALE` in magnitude (one reduction
+    and one host sync, at load time)."""
+    _require(bool((scales.float().abs() < MAX_SCALE).all()),
+             "scales must be finite and below 2^120 in magnitude for the exact in-register dequant")
+
+
 @dataclass(frozen=True)
 class PackedW4G32:
     """One INT4-G32 weight in the row-packed layout (see ``include/moss_hip.h``).
@@ -107,6 +121,7 @@ def repack_gptq(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tenso
     _require(k % 64 == 0 and n % 8 == 0, "K must be a multiple of 64 and N of 8")
     _require(tuple(scales.shape) == (k // GROUP, n), f"scales must be [{k // GROUP}, {n}]")
     _require(tuple(qzeros.shape) == (k // GROUP, n // 8), f"qzeros must be [{k // GROUP}, {n // 8}]")
+    _check_scales(scales)
     out = PackedW4G32.empty(n, k, dev)
     native.call("moss_w4g32_repack_gptq", native.ptr(qweight), native.ptr(scales), native.ptr(qzeros),
                 native.ptr(out.qw), native.ptr(out.scales), native.ptr(out.zeros), k, n, native.stream_of(qweight))
@@ -131,6 +146,7 @@ def import_signed(packed: torch.Tensor, scales: torch.Tensor) -> PackedW4G32:
         # the reference's own exactness rule before narrowing scale storage
         # (src/moss_tts/_runtime/dp4a_packing.py:149-152, short_scales.py:37-40)
         _require(torch.equal(sc.float(), scales), "scales are not exactly representable as bf16")
+    _check_scales(sc)
     _require(_aligned(packed, 4), "packed must be 4-byte aligned")
     qw = torch.empty((n, k // 8), dtype=torch.int32, device=dev)
     zp = torch.empty((n, k // 64), dtype=torch.uint8, device=dev)
@@ -148,6 +164,7 @@ def quantize_minmax(w: torch.Tensor) -> PackedW4G32:
     out = PackedW4G32.empty(n, k, w.device)
     native.call("moss_w4g32_quantize_minmax", native.ptr(w), native.ptr(out.qw), native.ptr(out.scales),
                 native.ptr(out.zeros), k, n, native.stream_of(w))
+    _check_scales(out.scales)
     return out
 
 

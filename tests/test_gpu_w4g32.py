@@ -166,9 +166,12 @@ def test_gemv_exact_properties_full_size(dev, k, n, mode):
 def _scale_sweep_weight():
     """One 32-code group per (bf16 scale, zero point) for every positive finite bf16 scale (bit patterns
     0x0001..0x7F7F, subnormals included) and all 16 zero points; each group holds every code 0..15
-    twice, rotated by the group index so every code meets every nibble position.  Rows of K = 4096;
-    the groups that pad the last row use scale 1."""
-    scales = torch.arange(1, 0x7F80, dtype=torch.int32)                    # 0x7F80 is +inf
+    twice, rotated by the group index so every code meets every nibble position.  Rows of K = 4096
+    (8 scales each); the scales below 2^120 (0x7B80) fill whole rows, padded with scale 1, ahead of
+    the larger ones, and the groups that pad the last row use scale 1."""
+    below = torch.arange(1, 0x7B80, dtype=torch.int32)                     # 0x7F80 is +inf
+    pad = torch.full((-below.numel() % 8,), 0x3F80, dtype=torch.int32)
+    scales = torch.cat([below, pad, torch.arange(0x7B80, 0x7F80, dtype=torch.int32)])
     n_groups = scales.numel() * 16
     k, gpr = 4096, 128
     rows = -(-n_groups // gpr)
@@ -187,9 +190,9 @@ def test_exact_dequant_every_bf16_scale(dev):
     finite bf16 scale, in the three places it is formed: the dequant kernel (plain fp32 product),
     the decode GEMV's exact mode (one-hot activations select each column; v_dot2 block) and the
     prefill GEMM's producer (identity activations give the whole matrix; same block).  The dequant
-    kernel must equal the oracle bit for bit everywhere.  A one-hot product reads 0 * w for the
-    other weights of a row, which is NaN where some w is infinite, so the GEMV and GEMM are checked
-    on the rows whose dequantized weights are all finite (every scale up to 2^123)."""
+    kernel must equal the oracle bit for bit everywhere.  The GEMV and GEMM form (128 + q) s in fp32,
+    finite below 2^120.8, so they are held to every scale below 2^120 (the bound the loaders enforce;
+    31,615 scales, subnormals included)."""
     from moss_tts._runtime import w4g32
 
     print("exact dequant over every positive finite bf16 scale", flush=True)
@@ -198,8 +201,9 @@ def test_exact_dequant_every_bf16_scale(dev):
     ref = _bits(o.dequantize(q, z, s))
     pw = _packed(q, z, s, dev)
     assert torch.equal(_bits(w4g32.dequantize(pw)), ref), "dequant kernel"
-    finite_rows = ((ref & 0x7F80) != 0x7F80).all(1)
     s_bits = s.contiguous().view(torch.int16).to(torch.int32)
+    finite_rows = (s_bits < 0x7B80).all(1)                                 # 0x7B80 = 2^120
+    assert int(torch.unique(s_bits[finite_rows]).numel()) == 0x7B7F       # every scale below 2^120
 
     def check(got_t, what):
         bad = (got_t != ref) & finite_rows[:, None]
@@ -219,6 +223,20 @@ def test_exact_dequant_every_bf16_scale(dev):
         cols[c] = w4g32.gemv(eye[c:c + 1], pw)[0]
     torch.cuda.synchronize()
     check(_bits(cols).t(), "GEMV exact mode")
+
+
+def test_loaders_reject_scales_outside_the_exact_range(dev):
+    from moss_tts._runtime import w4g32
+
+    big = torch.full((8, 2), 2.0 ** 121, device=dev).bfloat16()
+    q, z, s = _case(8, 64, 5)
+    qweight, _, qzeros = o.pack_gptq(q, z, s)
+    with pytest.raises(ValueError, match="2\\^120"):
+        w4g32.repack_gptq(qweight.to(dev), big.t().contiguous(), qzeros.to(dev))
+    with pytest.raises(ValueError, match="2\\^120"):
+        w4g32.import_signed(torch.zeros((8, 32), dtype=torch.uint8, device=dev), big)
+    with pytest.raises(ValueError, match="2\\^120"):
+        w4g32.quantize_minmax(torch.full((8, 64), 3e38, device=dev) * torch.tensor([1.0, -1.0], device=dev).repeat(32))
 
 
 def test_gemv_rejects_bad_inputs(dev):
