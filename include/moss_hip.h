@@ -180,6 +180,17 @@ int moss_w4g32_gemm(const void *x, const void *qw, const void *sc, const void *z
 /* Workspace bytes the GEMMs (INT4 and FP8, M > 1) use for an M x K x N problem; 0 = none. */
 long long moss_gemm_workspace_bytes(int M, int K, int N);
 
+/* moss_w4g32_gemm without a workspace argument and without any allocation: the K-split partial sums
+ * go to a 32 MiB device array inside the library (one per GPU, kept until the process ends), which
+ * holds every plan's partials, so the result equals moss_w4g32_gemm's with a full workspace bit for
+ * bit.  A shape whose plan would need more is refused with hipErrorInvalidValue.  The array's device
+ * address is looked up on the first call on each device (make that call outside graph capture);
+ * calls that overlap on one device share the array and race.  No counterpart in the reference: for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int moss_w4g32_gemm_noalloc(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K,
+                            int N, void *stream);
+
 /* --------------------------------------------------- FP8 E4M3 weight-only */
 /* W e4m3 (OCP) [N, K] row-major bytes (16-byte aligned), scale fp32 [N] or NULL (= 1):
  * y bf16 [M, N] = bf16(scale[n] * sum_k f32(W[n,k]) * x[m,k]), fp32 accumulate.

@@ -29,6 +29,8 @@
 // are dealt to the 8 XCDs round-robin), so a weight tile is fetched into one L2.
 #include "common.h"
 
+#include <mutex>
+
 namespace moss {
 namespace {
 
@@ -640,4 +642,46 @@ MOSS_API int moss_w4g32_gemm(const void* x, const void* qw, const void* sc, cons
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && workspace_bytes >= 0);
     return launch_gemm<kInt4G32>(x, qw, sc, zp, y, M, K, N, nullptr, workspace, workspace_bytes,
                                  (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The allocation-free GEMM: the K-split partial sums go to a file-scope device array instead of a
+// caller workspace.  Every plan's partials fit in it (at most 512 workgroups of 128 x 128 fp32
+// outputs, 32 MiB).  Each device holds its own copy at its own address, found once per device with
+// hipGetSymbolAddress; host code uses only that address, never the array's name.  The partials are
+// written in full before the reduction reads them, so nothing needs clearing between calls, but
+// calls that overlap on one device share the array and race.
+static constexpr long long kScratchBytes = 32ll << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / 4];
+
+static constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_of_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return (int)hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+MOSS_API int moss_w4g32_gemm_noalloc(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M,
+                                     int K, int N, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && y && M > 0 && N > 0 && K > 0 && K % 64 == 0);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
+    // a plan whose partials would not fit is refused rather than run differently
+    MOSS_CHECK_ARG(gemm_workspace_bytes(M, K, N) <= kScratchBytes);
+    void* ws = nullptr;
+    if (int rc = scratch_of_current_device(&ws)) return rc;
+    return launch_gemm<kInt4G32>(x, qw, sc, zp, y, M, K, N, nullptr, ws, kScratchBytes, (hipStream_t)stream);
 }

@@ -36,6 +36,7 @@ SIGNATURES: dict[str, list] = {
     "moss_w4g32_gateup_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_w4g32_gemm": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_gemm_workspace_bytes": [_I, _I, _I],
+    "moss_w4g32_gemm_noalloc": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4g32_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_w4g32_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_bf16_gemv": [_P, _P, _P, _I, _I, _I, _P],

@@ -292,3 +292,26 @@ def gemm(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
     native.call("moss_w4g32_gemm", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
                 native.ptr(y), m, w.K, w.N, wp, wb, native.stream_of(x))
     return y
+
+
+#: bytes of the library's scratch array behind :func:`gemm_noalloc` (every GEMM plan's partials fit)
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def gemm_noalloc(x: torch.Tensor, w: PackedW4G32, out: torch.Tensor) -> torch.Tensor:
+    """:func:`gemm` into a caller-provided ``out`` (bf16 ``[..., M, N]``) through the allocation-free
+    entry point: the K-split partials live in the library's own device array, so the call allocates
+    nothing.  Calls that overlap on one device race on that array."""
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.shape[-1] == w.K, f"x must end in a dimension of {w.K}")
+    _require(_aligned(x, 16), "x must be 16-byte aligned")
+    m = x.numel() // w.K
+    _require(m > 0, "empty input")
+    _cuda_contig("out", out, torch.bfloat16, w.device)
+    _require(out.numel() == m * w.N, f"out must hold {m} x {w.N} values")
+    need = int(native.lib().moss_gemm_workspace_bytes(m, w.K, w.N))
+    _require(need <= NOALLOC_SCRATCH_BYTES, f"this GEMM's partial sums ({need} B) exceed the "
+             f"{NOALLOC_SCRATCH_BYTES} B scratch of the allocation-free entry point")
+    native.call("moss_w4g32_gemm_noalloc", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales),
+                native.ptr(w.zeros), native.ptr(out), m, w.K, w.N, native.stream_of(x))
+    return out

@@ -66,6 +66,12 @@ def test_host_only_entry_points(lib):
     # M=16: 32 INT4 tiles of 32 tokens; the split doubles to 16 (512 workgroups) while the partials
     # stay under half the weight bytes
     assert lib.moss_gemm_workspace_bytes(16, 4096, 4096) == 16 * 16 * 4096 * 4
+    # every GEMM plan's partial sums fit the allocation-free entry point's 32 MiB scratch array
+    worst = max(lib.moss_gemm_workspace_bytes(m, k, n) for m in (1, 2, 5, 16, 33, 64, 65, 128, 200, 256, 300,
+                                                                  512, 640, 1000, 1024, 2048, 4096)
+                for k in (64, 1024, 4096, 4608, 12288, 16384) for n in (8, 100, 512, 1000, 2048, 4096, 6144,
+                                                                         12288, 24576, 32800))
+    assert 0 < worst <= 32 << 20
     assert lib.moss_error_string(0)
     assert lib.moss_decode_attention_splits(2048) == 32
     assert lib.moss_decode_attention_splits(128) == 2
@@ -83,6 +89,8 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 3, 0, null) == 1          # rows_per_wave
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 0, 7, null) == 1          # dequant mode
     assert lib.moss_w4g32_gemm(odd, p, p, p, p, 64, 4096, 4096, null, 0, null) == 1    # alignment
+    assert lib.moss_w4g32_gemm_noalloc(odd, p, p, p, p, 64, 4096, 4096, null) == 1     # alignment
+    assert lib.moss_w4g32_gemm_noalloc(p, p, p, p, p, 64, 4000, 4096, null) == 1       # K % 64
     assert lib.moss_fp8_linear(p, p, null, p, 1, 4100, 64, 0, null, 0, null) == 1      # K % 16
     assert lib.moss_fp8_linear(p, p, null, p, 2, 4112, 64, 0, null, 0, null) == 1      # GEMM K % 64
     assert lib.moss_fp8_gateup_silu(p, p, null, p, 2, 4096, 64, 0, null) == 1           # M must be 1
