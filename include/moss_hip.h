@@ -270,6 +270,16 @@ int moss_decode_attention_qkv_quant(const void *qkv, const void *q_norm_w, const
                                     void *partial, void *lse, void *out, void *out_qx, void *out_sx, void *out_qsum,
                                     int L, float eps, void *stream);
 
+/* Causal GQA attention of the prompt pass (Qwen3-8B: 32 query / 8 KV heads, head_dim 128):
+ * q bf16 [n, 32, 128] for the tokens at absolute positions *start .. *start + n - 1 (start int64 [1]
+ * on the device, clamped to [0, L - n]), whose K/V rows are already in the caches bf16 [8, L, 128]
+ * (L % 64 == 0, n <= L <= 32768); token t attends rows 0 .. *start + t with scale 1/sqrt(128),
+ * softmax in fp32, probabilities rounded to bf16 for the P.V product; out bf16 [n, 32 * 128].
+ * Replaces F.scaled_dot_product_attention(..., is_causal=True, enable_gqa=True) of the prefill
+ * forward, src/moss_tts/_runtime/llm.py:116-128. */
+int moss_prefill_attention(const void *q, const void *k_cache, const void *v_cache, const void *start, void *out,
+                           int n, int L, void *stream);
+
 /* ids int64 [T, Q+1] (text token then Q codebook codes), text bf16 [Vt, H], audio bf16
  * [Q, V, H] -> out bf16 [T, H] with a bf16 rounding after each addition; ids are clamped
  * into their tables.  Replaces embedding_sum (src/moss_tts/_runtime/kernels.py:7-26). */

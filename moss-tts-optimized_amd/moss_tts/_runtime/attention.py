@@ -1,10 +1,12 @@
-"""Decode attention over the static bf16 KV cache and the decode-step embedding sum.
+"""Decode and prefill attention over the static bf16 KV cache, and the embedding sum.
 
 ``decode_attention`` mirrors the reference's decode path after q/k-norm + RoPE
 (``src/moss_tts/_runtime/kernels.py:211-251``, native launcher
 ``src/moss_tts/_runtime/attention_native.py:31-44``): validation raises ``ValueError``,
 the split workspaces are caller-owned or allocated with ``torch.empty``, launches go to the
-current stream.  ``embedding_sum`` mirrors ``src/moss_tts/_runtime/kernels.py:21-26``.
+current stream.  ``prefill_attention`` replaces the causal ``scaled_dot_product_attention`` of the
+prompt pass (``src/moss_tts/_runtime/llm.py:116-128``).  ``embedding_sum`` mirrors
+``src/moss_tts/_runtime/kernels.py:21-26``.
 """
 from __future__ import annotations
 
@@ -106,6 +108,36 @@ def decode_attention_qkv(qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.
                 native.ptr(partial), native.ptr(lse), native.ptr(out), native.ptr(act.qx), native.ptr(act.scales),
                 native.ptr(act.sums), L, float(eps), native.stream_of(qkv))
     return out, act
+
+
+def prefill_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, start: torch.Tensor, *,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal attention of ``n`` prompt tokens: ``q`` bf16 ``[n, 32, 128]`` (``[1, n, 32, 128]`` as
+    ``qk_rope`` writes it), the tokens at positions ``start .. start + n - 1`` (``start`` int64 ``[1]``
+    on the device) with their K/V rows already in ``keys``/``values`` ``[1, 8, L, 128]``.  Returns bf16
+    ``[n, 4096]``."""
+    _cuda_contig("q", q, torch.bfloat16)
+    dev = q.device
+    _require(q.numel() % (QH * HD) == 0 and q.numel() > 0, f"q must hold n x {QH} x {HD} values")
+    n = q.numel() // (QH * HD)
+    for name, t in (("keys", keys), ("values", values)):
+        _cuda_contig(name, t, torch.bfloat16, dev)
+    _require(keys.shape == values.shape and keys.ndim == 4 and tuple(keys.shape[:2]) == (1, KH)
+             and keys.shape[3] == HD, "matching [1, 8, L, 128] KV buffers required")
+    L = keys.shape[2]
+    _require(L % 64 == 0 and L <= 32768, "the cache length must be a multiple of 64, at most 32768")
+    _require(n <= L, "more prompt tokens than KV rows")
+    _require(_aligned(q, 16) and _aligned(keys, 16) and _aligned(values, 16), "q and KV buffers must be 16-byte aligned")
+    _cuda_contig("start", start, torch.int64, dev)
+    _require(start.numel() == 1, "one int64 start position required")
+    if out is None:
+        out = torch.empty((n, QH * HD), device=dev, dtype=torch.bfloat16)
+    else:
+        _cuda_contig("out", out, torch.bfloat16, dev)
+        _require(out.numel() == n * QH * HD, f"out must hold {n * QH * HD} values")
+    native.call("moss_prefill_attention", native.ptr(q), native.ptr(keys), native.ptr(values), native.ptr(start),
+                native.ptr(out), n, L, native.stream_of(q))
+    return out
 
 
 def embedding_sum(ids: torch.Tensor, text_weight: torch.Tensor, audio_weight: torch.Tensor) -> torch.Tensor:

@@ -27,7 +27,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import attention, bf16, sampling, w4a8, w4g32
+from . import attention, bf16, pointwise, sampling, w4a8, w4g32
 from .modules import Bf16Linear, QuantGateUpG32, QuantLinearG32
 from .w4g32 import _require
 
@@ -36,6 +36,8 @@ CODEBOOKS, AUDIO_VOCAB = 32, 1025
 SAMPLED_CODES = 1024                      # audio codes a head can emit (1024 is the pad code)
 # MossTTSDelay token ids (the reference model config's defaults)
 GEN_SLOT_ID, DELAY_SLOT_ID, AUDIO_START_ID, AUDIO_END_ID = 151656, 151662, 151652, 151653
+PAD_ID = 151643                           # the text pad token of the prompt buckets
+PREFILL_BUCKETS = (128, 256, 512)         # prompt lengths captured as graphs (presets.py:45)
 
 
 @dataclass
@@ -111,6 +113,8 @@ class DecodeStepG32:
         self.next_ids = torch.zeros(CODEBOOKS + 1, device=dev, dtype=torch.int64)
         self.graph = None
         self.logits = None
+        self.pad_id = PAD_ID
+        self.prefill_graphs = {}
 
     # ------------------------------------------------------------------ forward
     def forward(self, head_count: int = CODEBOOKS, trace: list | None = None) -> torch.Tensor:
@@ -269,6 +273,94 @@ class DecodeStepG32:
         self.delay_length.fill_(delay_length)
         self.step(ids, position)
         return self.next_ids.clone().view(1, 1, CODEBOOKS + 1)
+
+    # ------------------------------------------------------------------ prefill
+    def _prefill_body(self, ids: torch.Tensor, positions: torch.Tensor, start: torch.Tensor,
+                      last: torch.Tensor) -> torch.Tensor:
+        """The prompt pass over ``n`` tokens (``src/moss_tts/_runtime/llm.py:204-207``; layer loop
+        ``src/moss_tts/_runtime/prefill_pointwise.py:46-57``): embedding sum -> per layer the q||k||v
+        GEMM -> q/k head-norm + RoPE with the K/V rows written at ``positions``
+        (``prefill_qkv.py:31-53``) -> causal attention over cache rows ``0 .. position``
+        (``llm.py:116-128``) -> O GEMM -> add-RMSNorm -> gate||up GEMM -> SiLU*mul -> down GEMM ->
+        add-RMSNorm into the next layer; then the final add-RMSNorm + heads on the token ``last``.
+        ``ids`` int64 ``[n, 33]``, ``positions`` int64 ``[n]`` (= start + arange(n)), ``start`` and
+        ``last`` int64 ``[1]``, all on the device.  Returns logits as ``forward`` does."""
+        n, eps = ids.shape[0], self.eps
+        x = attention.embedding_sum(ids, self.text_embedding, self.audio_embedding)
+        residual = x
+        state = pointwise.rmsnorm(x, self.layers[0].input_norm, eps)
+        qbuf = torch.empty((n, QH, HD), device=self.device, dtype=torch.bfloat16)
+        mlp = None
+        for i, layer in enumerate(self.layers):
+            qkv = w4g32.gemm(state, layer.qkv.packed)
+            pointwise.qk_rope(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i], self.values[i],
+                              positions, eps, cos_by_position=True, out=qbuf)
+            attn = attention.prefill_attention(qbuf, self.keys[i], self.values[i], start)
+            o = w4g32.gemm(attn, layer.o.packed)
+            residual, state = pointwise.add_rmsnorm(o, residual, layer.post_norm, eps)
+            act = pointwise.silu_mul(w4g32.gemm(state, layer.gate_up.packed))
+            mlp = w4g32.gemm(act, layer.down.packed)
+            if i + 1 < len(self.layers):
+                residual, state = pointwise.add_rmsnorm(mlp, residual, self.layers[i + 1].input_norm, eps)
+        return self._heads(mlp.index_select(0, last), residual.index_select(0, last), CODEBOOKS)
+
+    def _prefill_inputs(self, ids: torch.Tensor, start: int, rows: int):
+        n = ids.shape[0]
+        static = torch.full((rows, CODEBOOKS + 1), SAMPLED_CODES, device=self.device, dtype=torch.int64)
+        static[:, 0] = self.pad_id
+        static[:n].copy_(ids)
+        positions = torch.arange(start, start + rows, device=self.device, dtype=torch.int64)
+        return (static, positions, torch.full((1,), start, device=self.device, dtype=torch.int64),
+                torch.full((1,), n - 1, device=self.device, dtype=torch.int64))
+
+    @torch.inference_mode()
+    def capture_prefill(self, buckets=PREFILL_BUCKETS) -> None:
+        """Capture the prompt pass for each bucket length as a graph (``llm.py:209-225``): a prompt of
+        ``n`` tokens replays the smallest bucket ``>= n``, padded with the pad token and code 1024; the
+        padded rows write K/V rows past the prompt, which the decode steps overwrite before they are
+        read.  Install before the first request; the graphs share the engine's caches."""
+        for b in sorted(set(int(x) for x in buckets)):
+            if not 0 < b < self.max_length or b in self.prefill_graphs:
+                continue
+            inputs = self._prefill_inputs(torch.full((1, CODEBOOKS + 1), SAMPLED_CODES, device=self.device,
+                                                     dtype=torch.int64), 0, b)
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    self._prefill_body(*inputs)
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            torch.cuda.synchronize(self.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = self._prefill_body(*inputs)
+            torch.cuda.synchronize(self.device)
+            self.prefill_graphs[b] = (graph, inputs, out)
+
+    @torch.inference_mode()
+    def prefill(self, ids: torch.Tensor, start: int = 0) -> torch.Tensor:
+        """The prompt pass (``FastLLM.prefill``, ``src/moss_tts/_runtime/llm.py:303-318``): ``ids`` int64
+        ``[1, n, 33]`` (or ``[n, 33]``) at cache rows ``start .. start + n - 1``; writes those K/V rows of
+        every layer and returns the last token's logits in the layout of ``step`` (32 audio heads, then
+        the 2 text-head rows).  A captured bucket serves the prompt when one fits, else it runs
+        eagerly."""
+        ids = ids.reshape(-1, CODEBOOKS + 1)
+        n = ids.shape[0]
+        if n < 1 or start < 0 or start + n > self.max_length:
+            raise ValueError("Batch must be one and prompt must fit the KV capacity")
+        fits = [b for b in self.prefill_graphs if b >= n and start + b <= self.max_length]
+        if fits:
+            graph, (s_ids, s_pos, s_start, s_last), out = self.prefill_graphs[min(fits)]
+            b = s_ids.shape[0]
+            s_ids.fill_(SAMPLED_CODES)
+            s_ids[:, 0] = self.pad_id
+            s_ids[:n].copy_(ids)
+            s_pos.copy_(torch.arange(start, start + b, dtype=torch.int64))
+            s_start.fill_(start)
+            s_last.fill_(n - 1)
+            graph.replay()
+            return out
+        return self._prefill_body(*self._prefill_inputs(ids.to(self.device), start, n))
 
     @property
     def weight_bytes(self) -> int:

@@ -49,6 +49,7 @@ SIGNATURES: dict[str, list] = {
     "moss_decode_attention_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P],
     "moss_decode_attention_qkv_quant": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P],
     "moss_embedding_sum": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "moss_prefill_attention": [_P, _P, _P, _P, _P, _I, _I, _P],
     "moss_fp8_linear": [_P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_fp8_gateup_silu": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_fp8_to_bf16": [_P, _P, ctypes.c_longlong, _P],

@@ -4,10 +4,10 @@ Signature, argument meaning and the configuration errors raised before anything 
 follow the reference (``src/moss_tts/api.py:36-99``; its checks are pinned by
 ``tests/test_api.py:101-114``).  The SM90 / Triton / nvcc checks of the reference
 (``api.py:79-82,99``) become a gfx950 device check and a check that ``libmoss_hip.so`` loads.
-What this library provides after loading is the INT4-G32 decode path: the model's projections
-swapped for quantized modules (``install_gptq``) and the batch-1 decode step captured as one
-HIP graph (``step``).  The streaming product loop, codec and voice cloning of the reference
-are not part of it.
+What this library provides after loading is the INT4-G32 path: the model's projections swapped
+for quantized modules (``install_gptq``), the prompt pass captured per bucket length (``prefill``)
+and the batch-1 decode step captured as one HIP graph (``step``).  The streaming product loop,
+codec and voice cloning of the reference are not part of it.
 """
 from __future__ import annotations
 
@@ -33,7 +33,12 @@ class GptqEngine:
         return self.decode.graph
 
     def warmup(self) -> None:
+        """Capture the prompt-pass buckets and the decode step (``llm.py:209-225,289-301``)."""
+        self.decode.capture_prefill()
         self.decode.capture()
+
+    def prefill(self, ids, start: int = 0):
+        return self.decode.prefill(ids, start)
 
     def step(self, ids, position: int):
         return self.decode.step(ids, position)
@@ -144,6 +149,14 @@ class MossTTS:
             yield
         finally:
             self._lock.release()
+
+    def prefill(self, ids, start: int = 0):
+        """The prompt pass (``FastLLM.prefill``, ``src/moss_tts/_runtime/llm.py:303-318``): ``ids``
+        int64 ``[1, n, 33]`` written into the KV cache at rows ``start .. start + n - 1``; returns the
+        last token's head logits (32 audio heads, then the 2 text-head rows; a view of the bucket
+        graph's output buffer, valid until the next prompt)."""
+        with self._request():
+            return self._engine.prefill(ids, start)
 
     def step(self, ids, position: int):
         """One batch-1 decode step: ``ids`` int64 ``[1, 33]`` (text token, 32 codebook codes) at

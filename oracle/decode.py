@@ -1,4 +1,5 @@
-"""CPU oracle: one batch-1 decode step composed from the per-operation oracles.
+"""CPU oracle: one batch-1 decode step, and the prompt pass (prefill), composed from the
+per-operation oracles.
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  Order of operations:
 ``src/moss_tts/_runtime/llm.py:227-260`` (fused residual path) with the projections as
@@ -93,3 +94,36 @@ def decode_step_w4a8(layers, final_norm, heads_w, text, audio, ids, position, ke
         mlp = o8.w4a8_linear(a, *L["down"])[0].view(1, -1)
     _, h = op.add_rmsnorm(mlp, residual, final_norm, eps)
     return ow.linear(h, heads_w).bfloat16().view(-1)
+
+
+def prefill(layers, final_norm, heads_w, text, audio, ids, start, keys, values, cos, sin, eps=1e-6,
+            linear=None):
+    """The prompt pass (``src/moss_tts/_runtime/llm.py:204-207``, layer loop
+    ``src/moss_tts/_runtime/prefill_pointwise.py:46-57``): ``ids [n, 33]`` at absolute positions
+    ``start .. start + n - 1``; per layer q||k||v -> q/k head-norm + RoPE, K/V rows written at the
+    positions (``prefill_qkv.py:7-28``) -> causal attention over cache rows ``0 .. position``
+    (``llm.py:116-128``) -> O -> add-RMSNorm -> gate||up -> SiLU*mul -> down -> add-RMSNorm, all
+    projections dequant-then-matmul rounded to bf16.  ``layers`` is consumed once, in order.  Returns
+    the bf16 logits of the last token through the final norm and the heads (``llm.py:206-207``)."""
+    lin = linear or ow.linear
+    n = ids.shape[0]
+    pos = torch.arange(int(start), int(start) + n)
+    x = oa.embedding_sum(ids, text, audio)
+    residual, state = x, None
+    mlp = None
+    for i, L in enumerate(layers):
+        if i == 0:
+            state = op.rmsnorm(x, L["input_norm"], eps)
+        else:
+            residual, state = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
+        qkv = lin(state, L["qkv"]).bfloat16()
+        q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[pos], sin[pos], keys[i], values[i], pos, eps)
+        attn = oa.prefill_attention(q, keys[i], values[i], int(start)).bfloat16().view(n, -1)
+        o = lin(attn, L["o"]).bfloat16()
+        residual, state = op.add_rmsnorm(o, residual, L["post_norm"], eps)
+        y = lin(state, L["gate_up"])
+        h = y.shape[1] // 2
+        act = ow.silu_mul_rounded(y[:, :h], y[:, h:])
+        mlp = lin(act, L["down"]).bfloat16()
+    _, h = op.add_rmsnorm(mlp[-1:], residual[-1:], final_norm, eps)
+    return lin(h, heads_w).bfloat16().view(-1)
