@@ -100,50 +100,64 @@ def _traffic():
         return None
 
 
-def cpu_baseline(torch, budget_s: float):
-    """The oracle's torch-CPU dequant+matmul of one MLP step (dequantizing every call)."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, budget_s: float, gateup, down, h, norm_w):
+    """The oracle's torch-CPU dequant-then-matmul of one MLP step, dequantizing every call as the
+    reference's contract does, on the same weights as the GPU run (``gateup``/``down``: AutoGPTQ
+    ``(qweight, scales, qzeros)`` repacked from the GPU's first weight copy) and the same input:
+    all threads of the affinity mask, then 4 threads (the reference's ``cpu_threads`` default)."""
     from oracle import pointwise as op
     from oracle import w4g32 as ow
 
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(7)
-
-    def rand_gptq(n, k):
-        qweight = torch.randint(-2**31, 2**31 - 1, (k // 8, n), generator=g, dtype=torch.int32)
-        scales = (torch.rand((k // 32, n), generator=g) * 0.005 + 0.001).bfloat16()
-        qzeros = torch.randint(-2**31, 2**31 - 1, (k // 32, n // 8), generator=g, dtype=torch.int32)
-        return qweight, scales, qzeros
-
-    gu = rand_gptq(2 * INTER, HIDDEN)
-    dn = rand_gptq(HIDDEN, INTER)
-    h = torch.randn((1, HIDDEN), generator=g).bfloat16()
-    nw = (1 + torch.randn(HIDDEN, generator=g) * 0.01).bfloat16()
-
     def step():
-        x = op.rmsnorm(h, nw, 1e-6)
-        y = ow.gptq_dequant_linear_cpu(x, *gu)
-        a = ow.silu_mul_rounded(y[:, :INTER], y[:, INTER:])
-        return ow.gptq_dequant_linear_cpu(a, *dn).bfloat16()
-
-    t0 = time.perf_counter()
-    step()
-    first = time.perf_counter() - t0
-    warm = 1 if first > budget_s / 6 else 3
-    for _ in range(warm - 1):
-        step()
-    reps = max(3, min(10, int(budget_s / max(first, 1e-3))))
-    times = []
-    for _ in range(reps):
+        x = op.rmsnorm(h, norm_w, 1e-6)
         t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": round(MLP_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full MLP steps (RMSNorm + gate||up K=4096 N=24576 + SiLU*mul + down K=12288 "
-                      f"N=4096), dequantizing every call; median {med * 1e3:.1f} ms/step after {warm} warm-up",
-            "ms_per_step": round(med * 1e3, 3)}
+        w1 = ow.gptq_dequant_cpu(*gateup)
+        t1 = time.perf_counter()
+        y = torch.nn.functional.linear(x.float(), w1.t().float())
+        t2 = time.perf_counter()
+        a = ow.silu_mul_rounded(y[:, :INTER], y[:, INTER:])
+        t3 = time.perf_counter()
+        w2 = ow.gptq_dequant_cpu(*down)
+        t4 = time.perf_counter()
+        torch.nn.functional.linear(a.float(), w2.t().float()).bfloat16()
+        t5 = time.perf_counter()
+        return t5 - t0, (t1 - t0) + (t4 - t3), (t2 - t1) + (t5 - t4)
+
+    def run(threads: int, budget: float):
+        torch.set_num_threads(threads)
+        first = step()[0]
+        warm = 1 if first > budget / 6 else 3
+        for _ in range(warm - 1):
+            step()
+        reps = max(3, min(10, int(budget / max(first, 1e-3))))
+        rows = sorted((step() for _ in range(reps)), key=lambda r: r[0])
+        med = rows[len(rows) // 2]
+        return {"threads": threads, "ms_per_step": round(med[0] * 1e3, 3), "dequant_ms": round(med[1] * 1e3, 3),
+                "matmul_ms": round(med[2] * 1e3, 3), "GB/s": round(MLP_BYTES / med[0] / 1e9, 3), "reps": reps,
+                "warmup": warm}
+
+    prev = torch.get_num_threads()
+    threads = len(os.sched_getaffinity(0))
+    full = run(threads, budget_s * 0.6)
+    four = run(4, budget_s * 0.4)
+    torch.set_num_threads(prev)
+    return {"value": full["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{full['reps']} full MLP steps (RMSNorm + gate||up K=4096 N=24576 + SiLU*mul + down "
+                      f"K=12288 N=4096) on the GPU run's first weight copy, dequantizing every call; median "
+                      f"after {full['warmup']} warm-up",
+            "ms_per_step": full["ms_per_step"], "dequant_ms": full["dequant_ms"], "matmul_ms": full["matmul_ms"],
+            "cpu_model": _cpu_model(), "threads_4": four}
 
 
 def _per_launch(torch, fns, replays: int = 20) -> float:
@@ -257,6 +271,32 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False)
     torch.cuda.synchronize()
     burst_ms = start.elapsed_time(end) / (3 * 32)
     del burst
+    prefill = None
+    if not w4a8:
+        # the whole prompt pass of 512 tokens (36 layers of INT4 GEMMs, causal attention, norms,
+        # SiLU*mul, the final norm and heads on the last token) as its bucket graph
+        n = 512
+        eng.capture_prefill((n,))
+        g = torch.Generator().manual_seed(5)
+        ids = torch.cat([torch.randint(0, 151643, (n, 1), generator=g), torch.randint(0, 1024, (n, 32), generator=g)], 1)
+        eng.prefill(ids)
+        graph = eng.prefill_graphs[n][0]
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(5):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        pms = start.elapsed_time(end) / 5
+        proj = 2 * n * (HIDDEN * 6144 + HIDDEN * HIDDEN + HIDDEN * 2 * INTER + INTER * HIDDEN) * n_layers
+        attn = n_layers * 32 * 2 * 2 * 128 * n * (n + 1) // 2
+        tf = (proj + attn) / pms / 1e9
+        prefill = {"tokens": n, "layers": n_layers, "ms": round(pms, 3), "TFLOP/s": round(tf, 1),
+                   "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flop": proj + attn,
+                   "parts": "embedding, per layer: norms, INT4 GEMMs, q/k-norm + RoPE + KV write, causal attention, "
+                            "SiLU*mul; final norm + heads on the last token"}
+        _log(f"[bench] prefill of {n} tokens through {n_layers} layers: {pms:.3f} ms, {tf:.0f} TFLOP/s")
+        eng.prefill_graphs.clear()
     nbytes = eng.step_bytes(2047)
     _log(f"[bench] decode step ({n_layers} layers, w4a8={w4a8}): {ms:.3f} ms, {nbytes / ms / 1e6:.0f} GB/s; "
          f"host enqueue {host_ms:.3f} ms per replay; 32-step first-audio graph {burst_ms:.3f} ms per step")
@@ -265,6 +305,8 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False)
            "kv_rows": 2048, "position": 2047, "target_ms": 4.0, "host_enqueue_ms": round(host_ms, 4),
            "first_audio_graph_ms_per_step": round(burst_ms, 4),
            "arithmetic": "w4a8 (int8 activations, integer dot)" if w4a8 else "w4a16 (exact bf16 dequant)"}
+    if prefill is not None:
+        out["prefill_512"] = prefill
     del eng
     torch.cuda.empty_cache()
     return out
@@ -437,6 +479,16 @@ def main() -> int:
          f"down K=12288 N=4096: {dn_s * 1e6:.2f} us, {DOWN_BYTES / dn_s / 1e9:.0f} GB/s")
 
     n_copies = len(copies)
+    # the CPU baseline's weights: the GPU run's first copy, back in the AutoGPTQ layout
+    cpu_weights = None
+    if not args.no_cpu_baseline:
+        from oracle import w4g32 as ow
+
+        def to_gptq(pw):
+            q, z = ow.rowunpack(pw.qw.cpu(), pw.zeros.cpu())
+            return ow.pack_gptq(q, z, pw.scales.cpu())
+
+        cpu_weights = (to_gptq(copies[0][0]), to_gptq(copies[0][1]), h.cpu(), norm_w.cpu())
     del copies, gemv_copies, g_cycle, g_unr, g_rem, g_w8
     torch.cuda.empty_cache()
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
@@ -450,8 +502,10 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         _log("[bench] CPU baseline (oracle, torch CPU) ...")
-        cpu = cpu_baseline(torch, args.cpu_budget)
-        _log(f"[bench] CPU baseline: {cpu['ms_per_step']} ms/step on {cpu['cores']} threads")
+        cpu = cpu_baseline(torch, args.cpu_budget, *cpu_weights)
+        _log(f"[bench] CPU baseline ({cpu['cpu_model']}): {cpu['ms_per_step']} ms/step on {cpu['cores']} threads "
+             f"(dequant {cpu['dequant_ms']} ms, matmul {cpu['matmul_ms']} ms); {cpu['threads_4']['ms_per_step']} "
+             f"ms/step on 4 threads")
 
     line = {
         "metric": METRIC,
