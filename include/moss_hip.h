@@ -61,6 +61,12 @@ int moss_w4g32_dequant_bf16(const void *qw, const void *sc, const void *zp, void
  * src/moss_tts/_runtime/calibrated_quant.py:36-38. */
 int moss_w4g32_quantize_minmax(const void *w, void *qw, void *sc, void *zp, int K, int N, void *stream);
 
+/* fp32 [N,K] -> rowpack with the reference's static symmetric scales and round-to-nearest codes:
+ * s = bf16(max(max|w_g|, 1e-8) / 7) per (row, 32-group), c = clamp(rint(w / s), -7, 7) (IEEE
+ * division, ties to even), stored as q = c + 8 with z = 8 (so the dequant is bf16(c * s)).
+ * static_scales and the no-Hessian rounding of src/moss_tts/_runtime/calibrated_quant.py:36-38,74-77. */
+int moss_w4g32_quantize_symmetric(const void *w, void *qw, void *sc, void *zp, int K, int N, void *stream);
+
 /* ------------------------------------------------------------ decode GEMV */
 /* dequant_mode of the decode GEMVs:
  *   MOSS_DEQUANT_EXACT (0)      every weight is the bit-exact bf16 dequant bf16_rne((q-z)*s)

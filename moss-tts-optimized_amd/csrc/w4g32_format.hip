@@ -172,6 +172,50 @@ __device__ __forceinline__ void quantize_group(const float* __restrict__ wg, uin
     *z_out = (uint32_t)z;
 }
 
+// Symmetric RTN against static scales (src/moss_tts/_runtime/calibrated_quant.py:36-38 and the
+// no-Hessian rounding of :74-77): s = bf16(max(max|w|, 1e-8) / 7), c = clamp(rint(w / s), -7, 7)
+// (IEEE division, ties to even), stored as q = c + 8 with z = 8, so (q - z) s = c s.
+__device__ __forceinline__ void quantize_group_symmetric(const float* __restrict__ wg, uint32_t* __restrict__ qwg,
+                                                         uint16_t* __restrict__ s_out) {
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const float4 t = reinterpret_cast<const float4*>(wg)[c];
+        v[4 * c] = t.x; v[4 * c + 1] = t.y; v[4 * c + 2] = t.z; v[4 * c + 3] = t.w;
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) amax = fmaxf(amax, fabsf(v[t]));
+    const uint16_t sb = f32_to_bf16(fmaxf(amax, 1e-8f) / 7.0f);
+    const float s = bf16_bits(sb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float c = fminf(fmaxf(rintf(v[8 * j + t] / s), -7.0f), 7.0f);
+            const int sh = (t & 1) ? 16 + 4 * (t >> 1) : 4 * (t >> 1);
+            word |= ((uint32_t)((int)c + 8)) << sh;
+        }
+        qwg[j] = word;
+    }
+    *s_out = sb;
+}
+
+__global__ __launch_bounds__(256) void quantize_symmetric(const float* __restrict__ w, uint32_t* __restrict__ qw,
+                                                          uint16_t* __restrict__ sc, uint8_t* __restrict__ zp, int K,
+                                                          int N) {
+    const int G = K >> 5, h = G >> 1;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)N * h) return;
+    const int n = (int)(i / h), b = (int)(i % h);
+    int glo, ghi;
+    zero_byte_groups(b, G, glo, ghi);
+    quantize_group_symmetric(w + (size_t)n * K + 32 * glo, qw + (size_t)n * (K >> 3) + 4 * glo, sc + (size_t)n * G + glo);
+    quantize_group_symmetric(w + (size_t)n * K + 32 * ghi, qw + (size_t)n * (K >> 3) + 4 * ghi, sc + (size_t)n * G + ghi);
+    zp[i] = 0x88;
+}
+
 __global__ __launch_bounds__(256) void quantize_minmax(const float* __restrict__ w, uint32_t* __restrict__ qw,
                                                        uint16_t* __restrict__ sc, uint8_t* __restrict__ zp,
                                                        int K, int N) {
@@ -243,6 +287,14 @@ MOSS_API int moss_w4g32_quantize_minmax(const void* w, void* qw, void* sc, void*
     MOSS_CHECK_ARG(w && qw && sc && zp && K > 0 && N > 0 && K % 64 == 0 && MOSS_ALIGNED(w, 16));
     const size_t threads = (size_t)N * (K / 64);
     hipLaunchKernelGGL(quantize_minmax, dim3(blocks_for(threads, 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)w, (uint32_t*)qw, (uint16_t*)sc, (uint8_t*)zp, K, N);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_w4g32_quantize_symmetric(const void* w, void* qw, void* sc, void* zp, int K, int N, void* stream) {
+    MOSS_CHECK_ARG(w && qw && sc && zp && K > 0 && N > 0 && K % 64 == 0 && MOSS_ALIGNED(w, 16));
+    const size_t threads = (size_t)N * (K / 64);
+    hipLaunchKernelGGL(quantize_symmetric, dim3(blocks_for(threads, 256)), dim3(256), 0, (hipStream_t)stream,
                        (const float*)w, (uint32_t*)qw, (uint16_t*)sc, (uint8_t*)zp, K, N);
     return moss_launch_status();
 }

@@ -37,10 +37,13 @@ class QuantLinearG32(nn.Module):
         return PackedW4G32(self.qw, self.scales, self.zeros)
 
     @classmethod
-    def from_float(cls, weight: torch.Tensor, **kw) -> "QuantLinearG32":
-        """Min-max RTN quantization of a float weight ``[N, K]`` on its device."""
+    def from_float(cls, weight: torch.Tensor, *, symmetric: bool = False, **kw) -> "QuantLinearG32":
+        """Quantize a float weight ``[N, K]`` on its device: min-max RTN, or with ``symmetric`` the
+        reference's static absmax/7 scales and round-to-nearest codes in [-7, 7]
+        (``src/moss_tts/_runtime/calibrated_quant.py:36-38,74-77``)."""
         _require(weight.is_cuda and weight.ndim == 2, "a 2-D device weight [out, in] is required")
-        return cls(w4g32.quantize_minmax(weight.detach().float().contiguous()), **kw)
+        w = weight.detach().float().contiguous()
+        return cls(w4g32.quantize_symmetric(w) if symmetric else w4g32.quantize_minmax(w), **kw)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _require(x.shape[-1] == self.in_features, f"expected {self.in_features} input features")

@@ -32,6 +32,7 @@ SIGNATURES: dict[str, list] = {
     "moss_w4g32_unpack_codes": [_P, _P, _I, _I, _P],
     "moss_w4g32_dequant_bf16": [_P, _P, _P, _P, _I, _I, _P],
     "moss_w4g32_quantize_minmax": [_P, _P, _P, _P, _I, _I, _P],
+    "moss_w4g32_quantize_symmetric": [_P, _P, _P, _P, _I, _I, _P],
     "moss_w4g32_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_w4g32_gateup_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_w4g32_gemm": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],

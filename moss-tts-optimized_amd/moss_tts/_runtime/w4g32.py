@@ -168,6 +168,21 @@ def quantize_minmax(w: torch.Tensor) -> PackedW4G32:
     return out
 
 
+def quantize_symmetric(w: torch.Tensor) -> PackedW4G32:
+    """fp32 ``[N, K]`` -> :class:`PackedW4G32` with the reference's static symmetric scales
+    (``bf16(max|w_g| / 7)``) and round-to-nearest codes in [-7, 7], stored with zero point 8
+    (``src/moss_tts/_runtime/calibrated_quant.py:36-38,74-77``)."""
+    _cuda_contig("w", w, torch.float32)
+    _require(w.ndim == 2 and w.shape[1] % 64 == 0, "w must be [N, K] with K % 64 == 0")
+    _require(_aligned(w, 16), "w must be 16-byte aligned")
+    n, k = w.shape
+    out = PackedW4G32.empty(n, k, w.device)
+    native.call("moss_w4g32_quantize_symmetric", native.ptr(w), native.ptr(out.qw), native.ptr(out.scales),
+                native.ptr(out.zeros), k, n, native.stream_of(w))
+    _check_scales(out.scales)
+    return out
+
+
 def unpack_codes(w: PackedW4G32) -> torch.Tensor:
     """Unsigned 4-bit codes ``uint8 [N, K]``."""
     codes = torch.empty((w.N, w.K), dtype=torch.uint8, device=w.device)

@@ -390,3 +390,28 @@ def test_norm_gemv_rejects_bad_inputs(dev):
                                            native.ptr(pw.qw), native.ptr(pw.scales), native.ptr(pw.zeros),
                                            native.ptr(y), 4096, 64, 0, 0, native.stream_of(x))
     assert rc == 1                                                   # sum_out overlaps x
+
+
+@pytest.mark.parametrize("k,n", [(64, 7), (4096, 200), (12288, 40), (4608, 16)])
+def test_quantize_symmetric_bitexact(dev, k, n):
+    """The device's static-scale symmetric quantizer equals the oracle's ``static_scales`` +
+    ``quantize_symmetric`` bit for bit (codes stored as c + 8 with zero point 8), including groups of
+    zeros (the 1e-8 floor) and ties; the module's ``from_float(symmetric=True)`` holds the same."""
+    from moss_tts._runtime import w4g32
+    from moss_tts._runtime.modules import QuantLinearG32
+
+    print(f"quantize_symmetric K={k} N={n}", flush=True)
+    g = torch.Generator().manual_seed(15)
+    w = torch.randn((n, k), generator=g) * 0.02
+    w[0, :32] = 0.0                                            # a zero group: the 1e-8 / 7 scale
+    w[1, :32] = torch.arange(32).float() * 0.5                 # max 15.5: scale bf16(15.5 / 7), with ties
+    out = w4g32.quantize_symmetric(w.to(dev))
+    s = o.static_scales(w)
+    c = o.quantize_symmetric(w, s)
+    q, z, s2 = o.signed_export_to_codes(o.pack_signed(c), s)
+    qw, sc, zp = o.rowpack(q, z, s2)
+    assert torch.equal(out.qw.cpu(), qw) and torch.equal(out.zeros.cpu(), zp)
+    assert torch.equal(_bits(out.scales), _bits(sc))
+    mod = QuantLinearG32.from_float(w.to(dev), symmetric=True)
+    assert torch.equal(mod.qw.cpu(), qw)
+    assert torch.equal(_bits(w4g32.dequantize(out)), _bits(o.dequantize_signed(c, s)))
