@@ -100,7 +100,8 @@ def call(name: str, *args) -> None:
 
 
 def gemm_workspace(m: int, k: int, n: int, device) -> tuple:
-    """(pointer, bytes) of a fresh fp32 workspace for an M x K x N GEMM, or (None, 0)."""
+    """(pointer, bytes, tensor) of a fresh fp32 workspace for an M x K x N GEMM, or (None, 0, None)
+    when the GEMM needs none; the caller keeps the tensor alive until the launch has run."""
     nbytes = int(lib().moss_gemm_workspace_bytes(int(m), int(k), int(n)))
     if nbytes == 0:
         return None, 0, None
