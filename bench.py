@@ -200,6 +200,38 @@ def fp8_bench(torch, dev):
     return out
 
 
+def small_m_bench(torch, dev):
+    """INT4-G32 linear at K = N = 4096 for M = 2..64 tokens (the weight-streaming kernel) beside the
+    M = 1 GEMV of the same shape; weights rotated over >= 600 MB of distinct copies.  GB/s counts
+    the weight stream plus activations in and outputs out."""
+    from moss_tts._runtime import w4g32
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(97)
+    k = n = HIDDEN
+    wbytes = n * k // 2 + n * (k // 32) * 2 + n * (k // 64)
+    copies = [_quantized(torch, w4g32, n, k, gen, dev) for _ in range(max(2, int(600e6 // wbytes)))]
+    gemv_us = None
+    for m in (1, 2, 7, 15, 16, 32, 64):
+        x = torch.randn((m, k), generator=gen, device=dev).bfloat16()
+        if m == 1:
+            fns = [lambda pw=pw: w4g32.gemv(x, pw) for pw in copies]
+        else:
+            fns = [lambda pw=pw: w4g32.gemm(x, pw) for pw in copies]
+        sec = _per_launch(torch, fns, replays=10)
+        nbytes = wbytes + 2 * m * k + 2 * m * n
+        gbs = nbytes / sec / 1e9
+        if m == 1:
+            gemv_us = sec * 1e6
+        out[f"int4_m{m}_k4096_n4096"] = {"us_per_call": round(sec * 1e6, 3), "GB/s": round(gbs, 1),
+                                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                         "vs_m1_gemv": round(sec * 1e6 / gemv_us, 3)}
+        _log(f"[bench] INT4 M={m} K=N=4096: {sec * 1e6:.2f} us, {gbs:.0f} GB/s, {sec * 1e6 / gemv_us:.2f}x the M=1 GEMV")
+    del copies
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill_bench(torch, dev):
     """INT4-G32 prefill GEMMs at M=512 (QKV N=6144, O N=4096, gate||up N=24576, down K=12288):
     TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak."""
@@ -492,6 +524,7 @@ def main() -> int:
     del copies, gemv_copies, g_cycle, g_unr, g_rem, g_w8
     torch.cuda.empty_cache()
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
+    small_m = small_m_bench(torch, dev) if not args.no_extras else None
     prefill = prefill_bench(torch, dev) if not args.no_extras else None
     decode = decode_w4a8 = None
     if args.decode_steps > 0:
@@ -562,6 +595,7 @@ def main() -> int:
             "decode_step": decode,
             "decode_step_w4a8": decode_w4a8,
             "fp8": fp8_lines,
+            "int4_small_m": small_m,
             "prefill_gemm": prefill,
         },
     }

@@ -36,6 +36,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;
 constexpr int kPad = 8;  // bf16 padding per LDS row: breaks the 128-byte bank period
@@ -490,6 +491,216 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ par
     *reinterpret_cast<uint2*>(Y + i) = o;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Small M (up to 32 tokens INT4, 16 e4m3): weight streaming.  A workgroup owns 16 weight rows over
+// the whole of K, so every weight byte is read once per call and no partial sums leave the
+// workgroup; ceil(N / 16) workgroups of 8 waves, wave w taking the w-th eighth of K, 4 groups of
+// 32 inputs (a quad) per step.  One v_mfma_f32_16x16x32_bf16 per group and token tile: lane
+// (j, q) = (lane % 16, lane / 16) holds inputs 32 g + 8 q .. + 7 of group g, as the A operand 8
+// weights of row n0 + j (one word of INT4 codes dequantized bit-exactly in registers, or 8 e4m3
+// bytes) and as the B operand the same 8 inputs of token 16 tt + j, loaded straight from global
+// memory (the activations, at most 32 x K bf16, stay in L2; the 4 lanes of a token read 64
+// contiguous bytes).  The weights are loaded a whole group per lane (lane (j, q) takes group
+// g + q of the quad, 16 bytes INT4 / 32 bytes e4m3) and then transposed across the 4 lane rows
+// with v_permlane32_swap / v_permlane16_swap, so that lane (j, q) holds word q of each of the
+// quad's groups.  The 8 waves' 16 x 16 fp32 tiles are added in LDS in wave order
+// (deterministic), then scaled (FP8 row scale) and rounded to bf16.  Tokens beyond M load row
+// M - 1 and are not stored.  INT4 scales and zero points come 8 groups per load (16 and 8 bytes).
+constexpr int kStreamRows = 16;
+constexpr int kStreamWaves = 8;
+
+// 4 x 4 transpose across the four 16-lane rows: afterwards register t of row q holds what
+// register q of row t held.
+__device__ __forceinline__ void rows_transpose(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    auto a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    auto b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    r0 = c[0];
+    r1 = c[1];
+    r2 = d[0];
+    r3 = d[1];
+}
+
+template <int FMT, int TT>
+__global__ __launch_bounds__(512) void stream_gemm_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ sc,
+                                                          const uint8_t* __restrict__ zp,
+                                                          const float* __restrict__ row_scale,
+                                                          uint16_t* __restrict__ Y, int M, int N, int K) {
+    constexpr int DQ = 4;                                // quads whose loads are in flight
+    constexpr int CW = FMT == kInt4G32 ? 4 : 8;          // weight words per lane per quad
+    __shared__ float4 red[kStreamWaves][TT][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * kStreamRows, q = lane >> 4, j = lane & 15;
+    const int G = K >> 5, S = G / kStreamWaves;  // groups per wave (a multiple of 16)
+    const int gw = wave * S;                      // the wave's first group
+    const size_t row = (size_t)min(n0 + j, N - 1);
+    const uint16_t* xr[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) xr[tt] = X + (size_t)min(16 * tt + j, M - 1) * K + 32 * gw + 8 * q;
+
+    // quad d: groups gw + 4 d .. + 3
+    auto load_x = [&](u32x4_t (&xv)[4][TT], int d) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) xv[t][tt] = *reinterpret_cast<const u32x4_t*>(xr[tt] + 32 * (4 * d + t));
+    };
+    auto load_w = [&](uint32_t (&w)[CW], int d) {
+        const int g = gw + 4 * d + q;
+        if constexpr (FMT == kInt4G32) {
+            const uint4 v = reinterpret_cast<const uint4*>(W)[row * G + g];
+            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else {
+            const uint4* src = reinterpret_cast<const uint4*>(W + row * K + 32 * g);
+            const uint4 v0 = src[0], v1 = src[1];
+            w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+            w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+        }
+    };
+    // INT4: scales (8 bf16) and zero bytes (8, one nibble side) of groups gw + 8 b .. + 7
+    auto load_sz = [&](uint4& sv, uint2& zv, uint32_t& zsh, int b) {
+        const int g = gw + 8 * b;
+        int zb;
+        zero_loc(g, G, zb, zsh);
+        sv = *reinterpret_cast<const uint4*>(sc + row * G + g);
+        zv = *reinterpret_cast<const uint2*>(zp + row * (G >> 1) + zb);
+    };
+
+    f32x4_t acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int quads = S / 4;
+    uint32_t cw[DQ][CW];
+    u32x4_t xv[DQ][4][TT];
+    uint4 sv[2] = {}, sv_n[2] = {};
+    uint2 zv[2] = {}, zv_n[2] = {};
+    uint32_t zsh[2] = {}, zsh_n[2] = {};
+    if constexpr (FMT == kInt4G32) {
+        load_sz(sv[0], zv[0], zsh[0], 0);
+        load_sz(sv[1], zv[1], zsh[1], 1);
+        if (quads > 4) {
+            load_sz(sv_n[0], zv_n[0], zsh_n[0], 2);
+            load_sz(sv_n[1], zv_n[1], zsh_n[1], 3);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+        load_w(cw[i], i);  // quads >= 4 >= DQ
+        load_x(xv[i], i);
+    }
+    uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
+    asm volatile("" : "+v"(mask), "+v"(bias_bits));
+    for (int d0 = 0; d0 < quads; d0 += 4) {  // quads % 4 == 0; DQ divides 4
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int d = d0 + u, i = u % DQ;
+            pin();
+            // lane (j, q): word q of each group of the quad (INT4), words 2 q, 2 q + 1 (e4m3)
+            uint32_t wq[CW];
+#pragma unroll
+            for (int c = 0; c < CW; ++c) wq[c] = cw[i][c];
+            if constexpr (FMT == kInt4G32) {
+                rows_transpose(wq[0], wq[1], wq[2], wq[3]);
+            } else {
+                // words 2 t, 2 t + 1 of group g + q hold inputs 8 t .. 8 t + 7
+                rows_transpose(wq[0], wq[2], wq[4], wq[6]);
+                rows_transpose(wq[1], wq[3], wq[5], wq[7]);
+            }
+            // the weight slot is free: quad d + DQ into it (a wave-uniform branch: no refill past
+            // the wave's last quad)
+            if (d + DQ < quads) load_w(cw[i], d + DQ);
+            pin();
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {  // group gw + 4 d + t
+                uint32_t a[4];
+                if constexpr (FMT == kInt4G32) {
+                    const int gi = 4 * (u & 1) + t;  // within the 8-group scale block u / 2
+                    const uint4& s8 = sv[u >> 1];
+                    const uint32_t sw = gi < 2 ? s8.x : gi < 4 ? s8.y : gi < 6 ? s8.z : s8.w;
+                    const uint32_t s_lo = (sw >> (16 * (gi & 1))) & 0xffffu, s_hi = s_lo << 16;
+                    const uint32_t zq = ((gi < 4 ? zv[u >> 1].x : zv[u >> 1].y) >> (8 * (gi & 3) + zsh[u >> 1])) & 15u;
+                    const float bias = -(128.0f + (float)zq) * bf16_bits((uint16_t)s_lo);
+                    const uint32_t w = wq[t];
+                    dequant_word_exact((w & mask) | bias_bits, ((w >> 4) & mask) | bias_bits,
+                                       ((w >> 8) & mask) | bias_bits, ((w >> 12) & mask) | bias_bits, s_lo, s_hi,
+                                       bias, a);
+                } else {
+                    a[0] = fp8x2_to_bf16x2<false>(wq[2 * t]);
+                    a[1] = fp8x2_to_bf16x2<true>(wq[2 * t]);
+                    a[2] = fp8x2_to_bf16x2<false>(wq[2 * t + 1]);
+                    a[3] = fp8x2_to_bf16x2<true>(wq[2 * t + 1]);
+                }
+                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, u32x4_t{a[0], a[1], a[2], a[3]});
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt)
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, xv[i][t][tt]),
+                                                                      acc[tt], 0, 0, 0);
+            }
+            pin();
+            if (d + DQ < quads) load_x(xv[i], d + DQ);  // the activation slot, once the MFMAs have read it
+            if (FMT == kInt4G32 && u == 3) {            // the next 16 groups' scale blocks
+                sv[0] = sv_n[0]; zv[0] = zv_n[0]; zsh[0] = zsh_n[0];
+                sv[1] = sv_n[1]; zv[1] = zv_n[1]; zsh[1] = zsh_n[1];
+                if (d0 + 8 < quads) {
+                    load_sz(sv_n[0], zv_n[0], zsh_n[0], d0 / 2 + 4);
+                    load_sz(sv_n[1], zv_n[1], zsh_n[1], d0 / 2 + 5);
+                }
+            }
+        }
+    }
+    // D[r][c] of the 16 x 16 tile: lane l, element e -> weight row 4 (l / 16) + e, token l % 16
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) red[wave][tt][lane] = make_float4(acc[tt][0], acc[tt][1], acc[tt][2], acc[tt][3]);
+    __syncthreads();
+    if (tid >= TT * 64) return;
+    const int tt = tid >> 6, l = tid & 63;
+    float4 sum = red[0][tt][l];
+#pragma unroll
+    for (int w = 1; w < kStreamWaves; ++w) {
+        const float4 r = red[w][tt][l];
+        sum.x += r.x;
+        sum.y += r.y;
+        sum.z += r.z;
+        sum.w += r.w;
+    }
+    float v[4] = {sum.x, sum.y, sum.z, sum.w};
+    const int n = n0 + 4 * (l >> 4), m = 16 * tt + (l & 15);
+    if (m >= M || n >= N) return;  // N % 4 == 0: the 4 rows are all in range or all out
+    if (FMT == kFp8E4M3 && row_scale) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= row_scale[n + e];
+    }
+    *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+
+// Shapes and pointers the streaming kernel takes: 8 waves x 4 steps of 4 groups of K (INT4: the
+// 8 zero bytes of a scale block on one nibble side), 4-row output stores, 16-byte weight,
+// activation and scale loads, 8-byte zero-point loads; and at least 128 workgroups.
+bool stream_shape(int FMT, int M, int K, int N, const void* x, const void* qw, const void* sc, const void* zp,
+                  const void* y) {
+    // up to 32 tokens for INT4 and 16 for e4m3 it is faster on MI355X than the tiles (measured at
+    // K = N = 4096: INT4 M = 32 11.9 vs 12.8 us, M = 64 18.8 vs 16.9 us; e4m3 M = 64 19.8 vs 13.3 us):
+    // every workgroup reads all M x K activations, which outweighs the weight stream as M grows
+    if (M < 1 || M > (FMT == kInt4G32 ? 32 : 16) || N % 4 || N < 128 * kStreamRows) return false;
+    if (!(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && MOSS_ALIGNED(y, 8))) return false;
+    if (K % 4096) return false;  // K / 256 groups per wave: whole 4-quad steps
+    return FMT == kFp8E4M3 || (MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8));
+}
+
+template <int FMT>
+void launch_stream(const void* x, const void* qw, const void* sc, const void* zp, const float* row_scale, void* y,
+                   int M, int K, int N, hipStream_t st) {
+    const dim3 grid((unsigned)((N + kStreamRows - 1) / kStreamRows));
+#define MOSS_STREAM(TTV)                                                                                         \
+    hipLaunchKernelGGL((stream_gemm_kernel<FMT, TTV>), grid, dim3(64 * kStreamWaves), 0, st, (const uint16_t*)x, \
+                       (const uint8_t*)qw, (const uint16_t*)sc, (const uint8_t*)zp, row_scale, (uint16_t*)y, M, N, K)
+    if (M <= 16) MOSS_STREAM(1);
+    else MOSS_STREAM(2);  // M <= 32 (stream_shape)
+#undef MOSS_STREAM
+}
+
 struct Plan {
     int bm, bn, split;
     bool reg;  // the register-weight 128 x 128 INT4 tile
@@ -587,6 +798,10 @@ void launch_reg(const Plan& p, const void* x, const void* qw, const void* sc, co
 template <int FMT>
 int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K, int N,
                 const float* row_scale, void* ws, long long ws_bytes, hipStream_t st) {
+    if (stream_shape(FMT, M, K, N, x, qw, sc, zp, y)) {
+        launch_stream<FMT>(x, qw, sc, zp, row_scale, y, M, K, N, st);
+        return moss_launch_status();
+    }
     Plan p = plan_gemm(M, K, N, FMT == kInt4G32);
     // the register-weight tile stores 4 outputs (8 bytes) at a time and loads scales and zero
     // bytes 16 and 8 at a time

@@ -42,6 +42,8 @@ LINEAR = [
     (1, 4096, 4096), (1, 4096, 12288), (64, 4096, 4096), (64, 4096, 12288),
     (1, 64, 8), (1, 4112, 300), (1, 12288, 4096), (3, 128, 40), (17, 1024, 1000), (512, 4096, 4096),
     (256, 4096, 16384), (300, 1024, 32808),   # 128 x 128 tiles, ragged M and N
+    # the small-M weight-streaming kernel (M <= 16, K % 4096 == 0, N >= 2048), and just past it
+    (2, 4096, 4096), (7, 4096, 4096), (15, 4096, 12288), (16, 12288, 2052), (33, 12288, 4100),
 ]
 
 

@@ -265,7 +265,13 @@ def test_gemv_rejects_bad_inputs(dev):
                                    # 32- and 64-token register tiles with a K split, ragged N
                                    (5, 1024, 1000), (16, 4096, 4096), (48, 4608, 2056),
                                    # N % 4 != 0: the LDS tiles take shapes the register tile would
-                                   (40, 4096, 1001), (130, 4096, 258)])
+                                   (40, 4096, 1001), (130, 4096, 258),
+                                   # the small-M weight-streaming kernel (M <= 32, K % 4096 == 0): one
+                                   # and two token tiles, ragged tiles, a ragged last row tile, K = 12288
+                                   (1, 4096, 2048), (2, 4096, 4096), (7, 4096, 4096), (15, 4096, 4096),
+                                   (17, 4096, 2052), (32, 12288, 4096), (25, 4096, 12296),
+                                   # just past it: the tiles again
+                                   (33, 4096, 6144), (64, 4096, 4096), (50, 12288, 4100)])
 def test_gemm_parity(dev, m, k, n):
     """MFMA GEMM with bit-exact bf16 dequantized weights: fp32 summation order is the only
     difference from the oracle's dequant-then-matmul."""
