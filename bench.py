@@ -246,15 +246,24 @@ def prefill_bench(torch, dev):
         xk = x[:, :k].contiguous()
         sec = _per_launch(torch, [lambda: w4g32.gemm(xk, pw)] * 8, replays=10)
         tf = 2 * 512 * k * n / sec / 1e12
-        out[f"gemm_m512_{name}_k{k}_n{n}"] = {"us_per_call": round(sec * 1e6, 2), "TFLOP/s": round(tf, 1),
-                                               "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
-        _log(f"[bench] prefill GEMM M=512 {name}: {sec * 1e6:.1f} us, {tf:.0f} TFLOP/s")
-        del pw
+        # for scale: the vendor library's plain bf16 GEMM (hipBLASLt through torch.matmul) on the
+        # bit-exact dequantized weights, which does none of the dequantization work
+        wb = w4g32.dequantize(pw)
+        ref_sec = _per_launch(torch, [lambda: torch.matmul(xk, wb.t())] * 8, replays=10)
+        out[f"gemm_m512_{name}_k{k}_n{n}"] = {
+            "us_per_call": round(sec * 1e6, 2), "TFLOP/s": round(tf, 1),
+            "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "hipblaslt_bf16_us_on_dequantized_weights": round(ref_sec * 1e6, 2)}
+        _log(f"[bench] prefill GEMM M=512 {name}: {sec * 1e6:.1f} us, {tf:.0f} TFLOP/s "
+             f"(hipBLASLt bf16 on the dequantized weights: {ref_sec * 1e6:.1f} us)")
+        del pw, wb
     # the four projections of one layer, times the 36 layers (attention and norms not included)
     us = sum(v["us_per_call"] for v in out.values())
+    ref_us = sum(v["hipblaslt_bf16_us_on_dequantized_weights"] for v in out.values())
     flop = 2 * 512 * (HIDDEN * 6144 + HIDDEN * HIDDEN + HIDDEN * 2 * INTER + INTER * HIDDEN)
     out["projections_36_layers"] = {"ms": round(36 * us / 1e3, 3), "TFLOP/s": round(flop / us / 1e6, 1),
-                                    "frac_of_mfma_bf16_peak": round(flop / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+                                    "frac_of_mfma_bf16_peak": round(flop / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+                                    "hipblaslt_bf16_ms_on_dequantized_weights": round(36 * ref_us / 1e3, 3)}
     _log(f"[bench] prefill projections M=512, 36 layers: {36 * us / 1e3:.2f} ms, {flop / us / 1e6:.0f} TFLOP/s")
     return out
 
