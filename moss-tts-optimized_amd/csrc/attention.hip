@@ -19,9 +19,14 @@ constexpr float kScale = 0.08838834764831845f;
 
 constexpr int kMaxSplits = 512;             // L <= 32768
 
-// grid (8 KV heads, S splits), 256 threads.  Each workgroup issues all of its K and V loads
-// (64 rows x 256 B each) before any arithmetic, stages V in LDS, and writes the split's
-// normalized partial output and log-sum-exp.  Splits after the position write nothing.
+// grid (8 KV heads, S splits), 256 threads; wave w owns cache rows t0 + 16 w .. + 15 of the
+// split's 64.  Each wave loads its K rows as the A operand of v_mfma_f32_16x16x32_bf16 (lane l:
+// row l % 16, dims 8 (l / 16) .. + 7 of each 32-dim chunk) and its V rows one 256-byte row per
+// load (lane l: dims 2l, 2l + 1), all before any arithmetic, straight into registers.  The scores
+// of the 4 query heads are 4 MFMAs (B: the heads' q, columns 4..15 zero); the wave's softmax over
+// its 16 rows and its P.V (fp32) need no barrier; the 4 waves' (max, sum, P.V) meet once in LDS,
+// rescaled to the split's max.  Each split writes its normalized partial output and log-sum-exp;
+// splits after the position write nothing.
 //
 // FUSED: q, k and v come raw from the q||k||v projection row.  Every workgroup puts its 4
 // query heads through head RMSNorm + RoPE (row `position` of the cos/sin tables); the one
@@ -36,38 +41,44 @@ struct QkvArgs {
     float eps;
 };
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kWaveRows = kSplit / 4;  // cache rows per wave
+
 template <bool FUSED>
 __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restrict__ q,
                                                          uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                          const int64_t* __restrict__ pos, float* __restrict__ part,
                                                          float* __restrict__ lse, int L, int S, QkvArgs qa) {
-    __shared__ float qs[kGroup][kHeadDim];
-    __shared__ float pr[kGroup][kSplit];
-    __shared__ float denom_s[kGroup];
-    __shared__ __attribute__((aligned(16))) uint16_t ks[kSplit][kHeadDim];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[kSplit][kHeadDim];
+    __shared__ __attribute__((aligned(16))) uint16_t qb[kGroup][kHeadDim];  // the 4 query heads, bf16
+    __shared__ __attribute__((aligned(16))) uint16_t newkv[2][kHeadDim];     // owner: the new K and V rows
+    __shared__ __attribute__((aligned(16))) float pw[4][kGroup][kWaveRows];  // per wave: P[head][row]
+    __shared__ __attribute__((aligned(16))) float ow[4][kGroup][kHeadDim];   // per wave: unnormalized P.V
+    __shared__ float mw[4][kGroup], lw[4][kGroup];
     const int hk = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+    const int w = tid / kWave, l = tid & (kWave - 1);
     // rows [0, p] are attended; a position beyond the cache is clamped to its last row (the
     // host API rejects it first; the clamp keeps every access inside the cache regardless)
     const int p = (int)min(max(pos[0], (int64_t)0), (int64_t)(L - 1));
     const int t0 = split * kSplit;
     if (t0 > p) return;  // uniform over the workgroup
     const bool owner = FUSED && p < t0 + kSplit;  // this split holds the new row (uniform)
+    const int r0 = t0 + kWaveRows * w;            // this wave's first row
+    const bool live = r0 <= p;                    // wave-uniform: the wave holds attended rows
 
     // Loads, in this order: the q path's (L2 hits; the new K and V rows are loaded by every
-    // workgroup, branch-free, and used by the owner only), then the K/V tile.  Completions are
-    // counted in order, so the head norm + RoPE below runs while the tile is still arriving.
-    const int tl = tid >> 2, qd = tid & 3, t = t0 + tl;
-    const int j = tid / kWave, l = tid & (kWave - 1);
+    // workgroup, branch-free, and used by the owner only), then the wave's K and V rows.
+    // Completions are counted in order, so the head norm + RoPE runs while the rows arrive.
     constexpr int D = kHeadDim;
     uint16_t qx0 = 0, qx1 = 0, qw0 = 0, qw1 = 0, cs0 = 0, cs1 = 0, sn0 = 0, sn1 = 0;
     uint16_t kx0 = 0, kx1 = 0, kw0 = 0, kw1 = 0, vx0 = 0, vx1 = 0;
     uint32_t qpair = 0;
     if constexpr (FUSED) {
-        // wave j: query head 4 hk + j; lane l: dims l and l + 64
+        // wave w: query head 4 hk + w; lane l: dims l and l + 64
         const uint16_t* cr = qa.cos_t + (size_t)p * D;
         const uint16_t* sr = qa.sin_t + (size_t)p * D;
-        const uint16_t* qh = q + (size_t)(hk * kGroup + j) * D;
+        const uint16_t* qh = q + (size_t)(hk * kGroup + w) * D;
         const uint16_t* kh = q + (size_t)(kQHeads + hk) * D;
         const uint16_t* vh = q + (size_t)(kQHeads + kKvHeads + hk) * D;
         qx0 = qh[l]; qx1 = qh[l + 64];
@@ -81,113 +92,131 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
         qpair = reinterpret_cast<const uint32_t*>(q + (size_t)hk * kGroup * kHeadDim)[tid];
     }
     __builtin_amdgcn_sched_barrier(0);
-    // the K/V tile: 4 threads per cache row, each a 32-dim quarter (64 contiguous bytes) of K and
-    // of V; rows t0..t0+63 lie inside the cache (L % 64 == 0)
-    const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
-    const uint4* vr = reinterpret_cast<const uint4*>(vc + ((size_t)hk * L + t) * kHeadDim + 32 * qd);
-    const uint4 ka0 = kr[0], ka1 = kr[1], ka2 = kr[2], ka3 = kr[3];
-    const uint4 vb0 = vr[0], vb1 = vr[1], vb2 = vr[2], vb3 = vr[3];
+    // rows r0 .. r0 + 15 lie inside the cache (t0 <= p < L and L % 64 == 0)
+    u32x4_t ka[4] = {};
+    uint32_t vv[kWaveRows] = {};
+    if (live) {
+        const uint16_t* kr = kc + ((size_t)hk * L + r0 + (l & 15)) * D + 8 * (l >> 4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ka[c] = *reinterpret_cast<const u32x4_t*>(kr + 32 * c);
+        const uint32_t* vr = reinterpret_cast<const uint32_t*>(vc + ((size_t)hk * L + r0) * D) + l;
+#pragma unroll
+        for (int r = 0; r < kWaveRows; ++r) vv[r] = vr[r * (D / 2)];
+    }
     __builtin_amdgcn_sched_barrier(0);
-    uint16_t nk0 = 0, nk1 = 0, nv0 = 0, nv1 = 0;
     if constexpr (FUSED) {
         const float c0 = bf16_bits(cs0), c1 = bf16_bits(cs1);
         const float s0 = bf16_bits(sn0), s1 = bf16_bits(sn1);
         uint16_t o0, o1;
         head_norm_rope(bf16_bits(qx0), bf16_bits(qx1), bf16_bits(qw0), bf16_bits(qw1), c0, c1, s0, s1, qa.eps, o0,
                        o1);
-        qs[j][l] = bf16_bits(o0);
-        qs[j][l + 64] = bf16_bits(o1);
-        if (owner && j == 0) {  // the new K row of this KV head, into the cache
+        qb[w][l] = o0;
+        qb[w][l + 64] = o1;
+        if (owner && w == 0) {  // the new K row of this KV head, into the cache
+            uint16_t nk0, nk1;
             head_norm_rope(bf16_bits(kx0), bf16_bits(kx1), bf16_bits(kw0), bf16_bits(kw1), c0, c1, s0, s1, qa.eps,
                            nk0, nk1);
             uint16_t* kd = kc + ((size_t)hk * L + p) * D;
             kd[l] = nk0;
             kd[l + 64] = nk1;
-        } else if (owner && j == 1) {  // the new V row (a copy), into the cache
-            nv0 = vx0;
-            nv1 = vx1;
+            newkv[0][l] = nk0;
+            newkv[0][l + 64] = nk1;
+        } else if (owner && w == 1) {  // the new V row (a copy), into the cache
             uint16_t* vd = vc + ((size_t)hk * L + p) * D;
-            vd[l] = nv0;
-            vd[l + 64] = nv1;
+            vd[l] = vx0;
+            vd[l + 64] = vx1;
+            newkv[1][l] = vx0;
+            newkv[1][l + 64] = vx1;
         }
     } else {
-        const int jj = (2 * tid) / kHeadDim, d = (2 * tid) % kHeadDim;
-        qs[jj][d] = bf16_lo(qpair);
-        qs[jj][d + 1] = bf16_hi(qpair);
-    }
-    {
-        uint4* kd = reinterpret_cast<uint4*>(&ks[tl][32 * qd]);
-        uint4* vd = reinterpret_cast<uint4*>(&vs[tl][32 * qd]);
-        kd[0] = ka0; kd[1] = ka1; kd[2] = ka2; kd[3] = ka3;
-        vd[0] = vb0; vd[1] = vb1; vd[2] = vb2; vd[3] = vb3;
+        reinterpret_cast<uint32_t*>(&qb[0][0])[tid] = qpair;
     }
     __syncthreads();
-    if (owner) {  // the new row replaces the stale cache row staged above
-        if (j == 0) {
-            ks[p - t0][l] = nk0;
-            ks[p - t0][l + 64] = nk1;
-        } else if (j == 1) {
-            vs[p - t0][l] = nv0;
-            vs[p - t0][l + 64] = nv1;
+    if (owner && p >= r0 && p < r0 + kWaveRows) {  // the new row replaces the stale cache row loaded above
+        if (r0 + (l & 15) == p) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ka[c] = *reinterpret_cast<const u32x4_t*>(&newkv[0][32 * c + 8 * (l >> 4)]);
         }
-        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kWaveRows; ++r)
+            if (r0 + r == p) vv[r] = reinterpret_cast<const uint32_t*>(&newkv[1][0])[l];
     }
-    // scores of the 4 query heads for this thread's row quarter, summed over the DPP quad
-    {
-        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-        const uint4* kq = reinterpret_cast<const uint4*>(&ks[tl][32 * qd]);
+    // rows after the position never enter P.V (their cache contents are arbitrary)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 kv = kq[c];
-            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+    for (int r = 0; r < kWaveRows; ++r) vv[r] = r0 + r <= p ? vv[r] : 0u;
+
+    // scores: D[row][head] = K q^T; lane l holds rows 4 (l / 16) + i of head l % 16 (heads 4..15 zero)
+    const int hd = l & 15;
+    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int d = 32 * qd + 8 * c + 2 * e;
-                const float k0 = bf16_lo(kw[e]), k1 = bf16_hi(kw[e]);
-                s0 = fmaf(k1, qs[0][d + 1], fmaf(k0, qs[0][d], s0));
-                s1 = fmaf(k1, qs[1][d + 1], fmaf(k0, qs[1][d], s1));
-                s2 = fmaf(k1, qs[2][d + 1], fmaf(k0, qs[2][d], s2));
-                s3 = fmaf(k1, qs[3][d + 1], fmaf(k0, qs[3][d], s3));
+    for (int c = 0; c < 4; ++c) {
+        const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(&qb[hd & 3][32 * c + 8 * (l >> 4)]);
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        const u32x4_t bq = hd < kGroup ? qv : zero;
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[c]),
+                                                     __builtin_bit_cast(bf16x8_t, bq), sc, 0, 0, 0);
+    }
+    // softmax over the wave's 16 rows, per head: the 4 lanes l % 16 == h hold them
+    float sv[4], m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = r0 + 4 * (l >> 4) + i;
+        sv[i] = t <= p ? sc[i] * kScale : -INFINITY;
+        m = fmaxf(m, sv[i]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    float e[4], sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        e[i] = live ? expf(sv[i] - m) : 0.f;  // a live wave's max is finite (row r0 <= p)
+        sum += e[i];
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    if (hd < kGroup) *reinterpret_cast<float4*>(&pw[w][hd][4 * (l >> 4)]) = make_float4(e[0], e[1], e[2], e[3]);
+    if (l < kGroup) {
+        mw[w][l] = m;
+        lw[w][l] = sum;
+    }
+    // P.V of the wave's rows (the wave reads back what it wrote: no barrier): lane l, dims 2l, 2l + 1
+    float o[kGroup][2];
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+        o[h][0] = 0.f;
+        o[h][1] = 0.f;
+#pragma unroll
+        for (int r4 = 0; r4 < kWaveRows / 4; ++r4) {
+            const float4 pe = *reinterpret_cast<const float4*>(&pw[w][h][4 * r4]);
+            const float pv[4] = {pe.x, pe.y, pe.z, pe.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o[h][0] = fmaf(pv[i], bf16_lo(vv[4 * r4 + i]), o[h][0]);
+                o[h][1] = fmaf(pv[i], bf16_hi(vv[4 * r4 + i]), o[h][1]);
             }
         }
-        s0 += dpp_move<0xB1>(s0); s0 += dpp_move<0x4E>(s0);
-        s1 += dpp_move<0xB1>(s1); s1 += dpp_move<0x4E>(s1);
-        s2 += dpp_move<0xB1>(s2); s2 += dpp_move<0x4E>(s2);
-        s3 += dpp_move<0xB1>(s3); s3 += dpp_move<0x4E>(s3);
-        if (qd == 0) {
-            const bool ok = t <= p;
-            pr[0][tl] = ok ? s0 * kScale : -INFINITY;
-            pr[1][tl] = ok ? s1 * kScale : -INFINITY;
-            pr[2][tl] = ok ? s2 * kScale : -INFINITY;
-            pr[3][tl] = ok ? s3 * kScale : -INFINITY;
-        }
+        *reinterpret_cast<float2*>(&ow[w][h][2 * l]) = make_float2(o[h][0], o[h][1]);
     }
     __syncthreads();
-    // softmax within the split: wave j handles query head j, lane l cache row t0 + l
-    float m;
-    {
-        const float v = pr[j][l];
-        m = wave_max(v);                         // finite: row t0 <= p is valid
-        const float e = (t0 + l <= p) ? expf(v - m) : 0.f;
-        const float d = wave_sum(e);
-        pr[j][l] = e;
-        if (l == 0) denom_s[j] = d;
+    // the split's result: thread (head tid / 64, dims 2 (tid % 64) ..) rescales the 4 waves' parts
+    // to the split's max (wave 0 is live, so it is finite)
+    const int h = w;
+    float mx = mw[0][h];
+#pragma unroll
+    for (int v = 1; v < 4; ++v) mx = fmaxf(mx, mw[v][h]);
+    float den = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const float f = mw[v][h] == -INFINITY ? 0.f : expf(mw[v][h] - mx);
+        const float2 ov = *reinterpret_cast<const float2*>(&ow[v][h][2 * l]);
+        den = fmaf(f, lw[v][h], den);
+        a0 = fmaf(f, ov.x, a0);
+        a1 = fmaf(f, ov.y, a1);
     }
-    __syncthreads();
-    // P.V from LDS: lane l owns dims 2l, 2l+1 of query head j (rows after p never enter)
-    const int hq = hk * kGroup + j;
-    float a0 = 0.f, a1 = 0.f;
-    const int rows = min(kSplit, p - t0 + 1);
-    for (int r = 0; r < rows; ++r) {
-        const uint32_t v = reinterpret_cast<const uint32_t*>(&vs[r][0])[l];
-        const float e = pr[j][r];
-        a0 = fmaf(e, bf16_lo(v), a0);
-        a1 = fmaf(e, bf16_hi(v), a1);
-    }
-    const float den = denom_s[j];
+    const int hq = hk * kGroup + h;
     float* dst = part + ((size_t)hq * S + split) * kHeadDim;
     reinterpret_cast<float2*>(dst)[l] = make_float2(a0 / den, a1 / den);
-    if (l == 0) lse[hq * S + split] = m + logf(den);
+    if (l == 0) lse[hq * S + split] = mx + logf(den);
 }
 
 // grid 32 query heads, 128 threads (one per dim).  The splits holding attended rows are

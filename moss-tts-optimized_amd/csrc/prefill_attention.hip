@@ -19,7 +19,8 @@
 //                 permutation), and O^T keeps one query per lane, so the softmax rescale is a
 //                 per-lane factor.
 // V is stored transposed in LDS (V^T[d][key]) so the A operand is two 8-byte reads per MFMA.
-// The next block's K/V are loaded into registers while this block is multiplied.
+// The next K/V block is loaded into registers (ext vectors, so they stay out of scratch) while the
+// current one is consumed from LDS.
 #include "common.h"
 
 namespace moss {
@@ -34,9 +35,14 @@ constexpr int kBK = 64;              // keys per block
 constexpr int kKPad = kD + 8;        // K rows in LDS (bf16), padded
 constexpr int kVPad = kBK + 4;       // V^T rows in LDS (bf16), padded
 
+constexpr int kRing = 1;             // K/V blocks in flight per thread (2 and 3 measured no faster at
+                                     // 512 tokens, slower at 2048: more VGPRs, one workgroup per CU)
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
 struct KvRegs {
-    uint4 k[4];  // 4 x 8 d of keys (tid / 16) * 4 .. + 3 at d 8 (tid % 16)
-    uint4 v[4];
+    u32x4_t k[4];  // 4 x 8 d of keys (tid / 16) * 4 .. + 3 at d 8 (tid % 16)
+    u32x4_t v[4];
 };
 
 __device__ __forceinline__ void load_kv(KvRegs& r, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
@@ -45,8 +51,8 @@ __device__ __forceinline__ void load_kv(KvRegs& r, const uint16_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const size_t off = (size_t)(key0 + 4 * kg + i) * kD + 8 * dc;
-        r.k[i] = *reinterpret_cast<const uint4*>(kc + off);
-        r.v[i] = *reinterpret_cast<const uint4*>(vc + off);
+        r.k[i] = *reinterpret_cast<const u32x4_t*>(kc + off);
+        r.v[i] = *reinterpret_cast<const u32x4_t*>(vc + off);
     }
 }
 
@@ -58,11 +64,11 @@ __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return (a 
 __device__ __forceinline__ void store_kv(const KvRegs& r, uint16_t (*ks)[kKPad], uint16_t (*vt)[kVPad], int tid) {
     const int dc = tid & 15, kg = tid >> 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&ks[4 * kg + i][8 * dc]) = r.k[i];
-    const uint32_t w[4][4] = {{r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w},
-                              {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w},
-                              {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w},
-                              {r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w}};
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(&ks[4 * kg + i][8 * dc]) = r.k[i];
+    const uint32_t w[4][4] = {{r.v[0][0], r.v[0][1], r.v[0][2], r.v[0][3]},
+                              {r.v[1][0], r.v[1][1], r.v[1][2], r.v[1][3]},
+                              {r.v[2][0], r.v[2][1], r.v[2][2], r.v[2][3]},
+                              {r.v[3][0], r.v[3][1], r.v[3][2], r.v[3][3]}};
 #pragma unroll
     for (int p = 0; p < 4; ++p) {  // d pair 2p, 2p + 1 of the chunk
         const uint2 even = make_uint2(lo_pair(w[0][p], w[1][p]), lo_pair(w[2][p], w[3][p]));
@@ -72,7 +78,7 @@ __device__ __forceinline__ void store_kv(const KvRegs& r, uint16_t (*ks)[kKPad],
     }
 }
 
-__global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t* __restrict__ q,
+__global__ __launch_bounds__(256, 1) void prefill_attention_kernel(const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ k_cache,
                                                                  const uint16_t* __restrict__ v_cache,
                                                                  const int64_t* __restrict__ start,
@@ -107,13 +113,21 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t* 
     float m = -INFINITY, l = 0.f;
     const float c = 0.08838834764831845f * 1.4426950408889634f;  // 1/sqrt(128) * log2(e)
 
-    KvRegs nx;
-    load_kv(nx, kc, vc, 0, tid);
-    for (int b = 0; b < nblk; ++b) {
+    // K/V blocks travel kRing blocks ahead in registers (block b in ring slot b % kRing), so a
+    // block's global loads have kRing - 1 blocks of work to arrive
+    KvRegs ring[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing; ++i)
+        if (i < nblk) load_kv(ring[i], kc, vc, kBK * i, tid);
+    for (int b0 = 0; b0 < nblk; b0 += kRing)
+#pragma unroll
+    for (int slot = 0; slot < kRing; ++slot) {
+        const int b = b0 + slot;
+        if (b >= nblk) break;  // uniform
         __syncthreads();  // the previous block's LDS reads are done
-        store_kv(nx, ks, vt, tid);
+        store_kv(ring[slot], ks, vt, tid);
         __syncthreads();
-        if (b + 1 < nblk) load_kv(nx, kc, vc, kBK * (b + 1), tid);
+        if (b + kRing < nblk) load_kv(ring[slot], kc, vc, kBK * (b + kRing), tid);
 
         // S^T for the two 32-key halves of the block
         f32x16_t s[2];
