@@ -232,6 +232,29 @@ def small_m_bench(torch, dev):
     return out
 
 
+def bf16_heads_bench(torch, dev):
+    """The installed model's output heads: final add-RMSNorm + bf16-weight GEMV, K = 4096,
+    N = 32 x 1024 + 2 (audio codebooks and the text head), weights rotated over >= 600 MB of copies.
+    GB/s counts the bf16 weights, the norm weight and the activations in and out."""
+    from moss_tts._runtime import bf16
+
+    gen = torch.Generator(device=dev).manual_seed(96)
+    k, n = HIDDEN, 32 * 1024 + 2
+    copies = [(torch.randn((n, k), generator=gen, device=dev) * 0.02).bfloat16() for _ in range(3)]
+    x = torch.randn((1, k), generator=gen, device=dev).bfloat16()
+    res = torch.randn((1, k), generator=gen, device=dev).bfloat16()
+    nw = (1 + 0.01 * torch.randn(k, generator=gen, device=dev)).bfloat16()
+    fns = [lambda w=w: bf16.norm_gemv(x, nw, 1e-6, w, residual=res) for w in copies]
+    sec = _per_launch(torch, fns, replays=10)
+    nbytes = 2 * n * k + 2 * k + 3 * 2 * k + 2 * n
+    gbs = nbytes / sec / 1e9
+    _log(f"[bench] bf16 heads (add-RMSNorm + GEMV K={k} N={n}): {sec * 1e6:.2f} us, {gbs:.0f} GB/s")
+    del copies
+    torch.cuda.empty_cache()
+    return {"us_per_call": round(sec * 1e6, 3), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "shape": f"K={k}, N={n}"}
+
+
 def prefill_bench(torch, dev):
     """INT4-G32 prefill GEMMs at M=512 (QKV N=6144, O N=4096, gate||up N=24576, down K=12288):
     TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak."""
@@ -534,6 +557,7 @@ def main() -> int:
     torch.cuda.empty_cache()
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
     small_m = small_m_bench(torch, dev) if not args.no_extras else None
+    heads_bf16 = bf16_heads_bench(torch, dev) if not args.no_extras else None
     prefill = prefill_bench(torch, dev) if not args.no_extras else None
     decode = decode_w4a8 = None
     if args.decode_steps > 0:
@@ -605,6 +629,7 @@ def main() -> int:
             "decode_step_w4a8": decode_w4a8,
             "fp8": fp8_lines,
             "int4_small_m": small_m,
+            "bf16_heads_k4096_n32770": heads_bf16,
             "prefill_gemm": prefill,
         },
     }
