@@ -1,0 +1,164 @@
+"""GPU parity at seeded random shapes inside the documented limits, beside the hand-picked shapes of
+the other tests: INT4-G32 GEMV and gate||up (both dequant modes, every rows-per-wave choice), the
+INT4 GEMM (small-M streaming, tiles, K splits), the FP8 linear (GEMV and GEMM), and decode and
+prompt attention at random cache lengths, positions and start rows.
+
+Reference: fp32 torch math on the same inputs; for INT4 the weights are the bit-exact dequant
+(itself pinned bit for bit against the oracle in test_gpu_w4g32.py), for FP8 the exact e4m3 -> bf16
+values times the row scale, for attention softmax(q k^T / sqrt(128)) v over the visible rows with
+query head h reading KV head h / 4.  Bar: relative L2 error of the bf16 output below 1e-2 (the
+outputs are rounded to bf16 once; the worst case seen over 510 random cases was 7e-3, for the
+gate||up SiLU*mul, which rounds three times).
+"""
+import math
+import random
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+_rng = random.Random(20261202)
+
+
+def _gemv_cases(count):
+    out = []
+    for _ in range(count):
+        out.append((64 * _rng.randint(1, 256), _rng.randint(1, 5000), _rng.choice((0, 1, 2, 4)), _rng.choice((0, 1))))
+    return out
+
+
+def _gemm_cases(count):
+    out = []
+    for _ in range(count):
+        m = _rng.choice((_rng.randint(2, 40), _rng.randint(2, 600)))
+        k = 4096 * _rng.randint(1, 3) if _rng.random() < 0.3 else 64 * _rng.randint(1, 192)
+        n = _rng.randint(1, 5000) if _rng.random() < 0.5 else 4 * _rng.randint(512, 1500)
+        out.append((m, k, n))
+    return out
+
+
+def _fp8_cases(count):
+    out = []
+    for _ in range(count):
+        m = _rng.choice((1, 1, _rng.randint(2, 80)))
+        out.append((m, (16 if m == 1 else 64) * _rng.randint(1, 200), _rng.randint(1, 6000)))
+    return out
+
+
+def _decode_cases(count):
+    out = []
+    for _ in range(count):
+        L = 64 * _rng.randint(1, 64)
+        out.append((L, _rng.randint(0, L - 1)))
+    return out
+
+
+def _prefill_cases(count):
+    out = []
+    for _ in range(count):
+        L = 64 * _rng.randint(1, 40)
+        n = _rng.randint(1, min(L, 1100))
+        out.append((L, n, _rng.randint(0, L - n)))
+    return out
+
+
+GEMV = _gemv_cases(12)
+GEMM = _gemm_cases(12)
+FP8 = _fp8_cases(12)
+DECODE = _decode_cases(12)
+PREFILL = _prefill_cases(12)
+
+
+def _rel(a, b):
+    a, b = a.float(), b.float()
+    return float((a - b).norm() / b.norm().clamp_min(1e-12))
+
+
+def _packed(n, k, seed, dev):
+    from moss_tts._runtime import w4g32
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return w4g32.quantize_minmax(torch.randn((n, k), device=dev, generator=g) * 0.02), g
+
+
+@pytest.mark.parametrize("k,n,rows,mode", GEMV)
+def test_gemv_random_shape(dev, k, n, rows, mode):
+    from moss_tts._runtime import w4g32
+
+    print(f"gemv K={k} N={n} rows={rows} mode={mode}", flush=True)
+    pw, g = _packed(n, k, k + n, dev)
+    x = torch.randn((1, k), device=dev, generator=g).bfloat16()
+    ref = x.float() @ w4g32.dequantize(pw).float().t()
+    assert _rel(w4g32.gemv(x, pw, rows_per_wave=rows, dequant=mode), ref) < TOL
+    if n % 2 == 0:
+        half = n // 2
+        gate, up = ref[:, :half].bfloat16().float(), ref[:, half:].bfloat16().float()
+        want = torch.nn.functional.silu(gate).bfloat16().float() * up
+        assert _rel(w4g32.gateup_silu(x, pw, rows_per_wave=rows, dequant=mode), want) < TOL
+
+
+@pytest.mark.parametrize("m,k,n", GEMM)
+def test_gemm_random_shape(dev, m, k, n):
+    from moss_tts._runtime import w4g32
+
+    print(f"gemm M={m} K={k} N={n}", flush=True)
+    pw, g = _packed(n, k, m + k + n, dev)
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    ref = x.float() @ w4g32.dequantize(pw).float().t()
+    assert _rel(w4g32.gemm(x, pw), ref) < TOL
+
+
+@pytest.mark.parametrize("m,k,n", FP8)
+def test_fp8_linear_random_shape(dev, m, k, n):
+    from moss_tts._runtime import fp8
+
+    print(f"fp8 M={m} K={k} N={n}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(m + k + n)
+    wb = torch.randint(0, 256, (n, k), device=dev, dtype=torch.uint8, generator=g)
+    wb[(wb & 0x7F) == 0x7F] = 0  # no NaN codes
+    s = torch.rand((n,), device=dev, generator=g) + 0.5
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    ref = (x.float() @ fp8.to_bf16(wb).float().t()) * s
+    assert _rel(fp8.linear(x, wb, s), ref) < TOL
+
+
+def _attention_ref(q, kc, vc, last_row):
+    """q fp32-able [T, 32, 128], caches [8, L, 128]; token t sees rows 0 .. last_row[t]."""
+    out = torch.empty((q.shape[0], 32, 128), device=q.device)
+    rows = torch.arange(kc.shape[1], device=q.device)[None, :]
+    for h in range(32):
+        kh, vh = kc[h // 4].float(), vc[h // 4].float()
+        sc = (q[:, h].float() @ kh.t()) / math.sqrt(128)
+        sc = sc.masked_fill(rows > last_row[:, None], float("-inf"))
+        out[:, h] = torch.softmax(sc, -1) @ vh
+    return out
+
+
+@pytest.mark.parametrize("L,p", DECODE)
+def test_decode_attention_random_shape(dev, L, p):
+    from moss_tts._runtime import attention
+
+    print(f"decode attention L={L} p={p}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(L + p)
+    q = torch.randn((32, 128), device=dev, generator=g).bfloat16()
+    kc = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    vc = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    y = attention.decode_attention(q, kc, vc, torch.tensor([p], device=dev)).view(32, 128)
+    ref = _attention_ref(q.view(1, 32, 128), kc[0], vc[0], torch.tensor([p], device=dev))[0]
+    assert _rel(y, ref) < TOL
+
+
+@pytest.mark.parametrize("L,n,start", PREFILL)
+def test_prefill_attention_random_shape(dev, L, n, start):
+    from moss_tts._runtime import attention
+
+    print(f"prefill attention L={L} n={n} start={start}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(L + n + start)
+    q = torch.randn((n, 32, 128), device=dev, generator=g).bfloat16()
+    kc = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    vc = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    y = attention.prefill_attention(q, kc, vc, torch.tensor([start], device=dev)).view(n, 32, 128)
+    ref = _attention_ref(q, kc[0], vc[0], start + torch.arange(n, device=dev))
+    assert _rel(y, ref) < TOL
