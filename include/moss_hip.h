@@ -304,6 +304,15 @@ int moss_embedding_sum(const void *ids, const void *text, const void *audio, voi
 int moss_sample_topk(const void *logits, int rows, int stride, int vocab, float temperature, int top_k, float top_p,
                      const void *seed, const void *position, int salt, void *out, void *stream);
 
+/* Two moss_sample_topk calls with one seed and position in one launch (the decode step's text row
+ * and its audio rows): set a's rows_a rows, then set b's rows_b rows, each row sampled exactly as
+ * moss_sample_topk samples it (row numbers restart at 0 in set b), so the outputs equal the two
+ * separate calls'.  Replaces the pair of sample_topk calls of src/moss_tts/_runtime/llm.py:280,284. */
+int moss_sample_topk_pair(const void *logits_a, int rows_a, int stride_a, int vocab_a, float temperature_a,
+                          int top_k_a, float top_p_a, int salt_a, void *out_a, const void *logits_b, int rows_b,
+                          int stride_b, int vocab_b, float temperature_b, int top_k_b, float top_p_b, int salt_b,
+                          void *out_b, const void *seed, const void *position, void *stream);
+
 int moss_compose_next_ids(const void *text_index, const void *audio_index, const void *text_ids,
                           const void *audio_length, const void *delay_length, long long delay_slot_id,
                           long long audio_end_id, int channels, long long pad_code, void *next_ids, void *stream);

@@ -75,21 +75,34 @@ __device__ __forceinline__ int wave_rank(unsigned long long v) {
     return r;
 }
 
+// One set of rows sampled with one setting (the arguments of moss_sample_topk).
+struct SampleRows {
+    const uint16_t* __restrict__ logits;
+    int stride, vocab;
+    float temperature;
+    int top_k;
+    float top_p;
+    uint32_t salt;
+    int64_t* __restrict__ out;
+};
+
 // One wave per row; lane l holds logits l + 64 j as unique keys (value, then lower index first).
 // Selection: T = the k-th largest of the 64 per-lane maxima; at least k keys are >= T, so the top k
 // are among the keys >= T.  Those candidates are compacted into LDS; when at most 64 remain (the
 // usual case: about 31 for k = 25 over 1024 values) each lane ranks one against the others,
 // otherwise k rounds of wave argmax run over the candidates.
-__global__ __launch_bounds__(64) void sample_topk_rows(const uint16_t* __restrict__ logits, int stride, int vocab,
-                                                       float temperature, int top_k, float top_p,
-                                                       const uint64_t* __restrict__ seed,
-                                                       const int64_t* __restrict__ position, uint32_t salt,
-                                                       int64_t* __restrict__ out) {
+__device__ __forceinline__ void sample_row(const SampleRows& a, int row, const uint64_t* __restrict__ seed,
+                                           const int64_t* __restrict__ position) {
     __shared__ unsigned long long cand[kWave * kMaxPerLane];
     __shared__ float val[kMaxTopK];
     __shared__ int idx[kMaxTopK];
     __shared__ float prob[kMaxTopK];
-    const int row = blockIdx.x, lane = threadIdx.x;
+    const uint16_t* logits = a.logits;
+    const int stride = a.stride, vocab = a.vocab, top_k = a.top_k;
+    const float temperature = a.temperature, top_p = a.top_p;
+    const uint32_t salt = a.salt;
+    int64_t* out = a.out;
+    const int lane = threadIdx.x;
     const uint16_t* lr = logits + (size_t)row * stride;
     const bool greedy = !(temperature > 0.f);
     const int k = greedy ? 1 : top_k;
@@ -187,6 +200,20 @@ __global__ __launch_bounds__(64) void sample_topk_rows(const uint16_t* __restric
     out[row] = idx[pick];
 }
 
+__global__ __launch_bounds__(64) void sample_topk_rows(SampleRows a, const uint64_t* __restrict__ seed,
+                                                       const int64_t* __restrict__ position) {
+    sample_row(a, blockIdx.x, seed, position);
+}
+
+// Two sets in one launch: workgroups [0, rows_a) sample set a, the rest set b (row numbering, and
+// with it the random stream, restarts at 0 for b), each exactly as sample_topk_rows would.
+__global__ __launch_bounds__(64) void sample_topk_pair(SampleRows a, int rows_a, SampleRows b,
+                                                       const uint64_t* __restrict__ seed,
+                                                       const int64_t* __restrict__ position) {
+    if ((int)blockIdx.x < rows_a) sample_row(a, blockIdx.x, seed, position);
+    else sample_row(b, (int)blockIdx.x - rows_a, seed, position);
+}
+
 __global__ __launch_bounds__(64) void compose_next_ids_kernel(const int64_t* __restrict__ text_index,
                                                               const int64_t* __restrict__ audio_index,
                                                               const int64_t* __restrict__ text_ids,
@@ -255,17 +282,39 @@ __global__ __launch_bounds__(64) void advance_step_kernel(const int64_t* __restr
 
 using namespace moss;
 
+static bool sample_args_ok(const void* logits, int rows, int stride, int vocab, float temperature, int top_k,
+                           const void* out) {
+    return logits && out && rows > 0 && vocab > 0 && vocab <= kWave * kMaxPerLane && stride >= vocab &&
+           (!(temperature > 0.f) || (top_k >= 1 && top_k <= kMaxTopK && top_k <= vocab)) && MOSS_ALIGNED(logits, 2) &&
+           MOSS_ALIGNED(out, 8);
+}
+
 MOSS_API int moss_sample_topk(const void* logits, int rows, int stride, int vocab, float temperature, int top_k,
                               float top_p, const void* seed, const void* position, int salt, void* out,
                               void* stream) {
-    MOSS_CHECK_ARG(logits && seed && position && out && rows > 0 && vocab > 0 && vocab <= kWave * kMaxPerLane &&
-                   stride >= vocab);
-    MOSS_CHECK_ARG(!(temperature > 0.f) || (top_k >= 1 && top_k <= kMaxTopK && top_k <= vocab));
-    MOSS_CHECK_ARG(MOSS_ALIGNED(logits, 2) && MOSS_ALIGNED(seed, 8) && MOSS_ALIGNED(position, 8) &&
-                   MOSS_ALIGNED(out, 8));
-    hipLaunchKernelGGL(sample_topk_rows, dim3(rows), dim3(kWave), 0, (hipStream_t)stream, (const uint16_t*)logits,
-                       stride, vocab, temperature, top_k, top_p, (const uint64_t*)seed, (const int64_t*)position,
-                       (uint32_t)salt, (int64_t*)out);
+    MOSS_CHECK_ARG(sample_args_ok(logits, rows, stride, vocab, temperature, top_k, out));
+    MOSS_CHECK_ARG(seed && position && MOSS_ALIGNED(seed, 8) && MOSS_ALIGNED(position, 8));
+    const SampleRows a{(const uint16_t*)logits, stride, vocab, temperature, top_k, top_p, (uint32_t)salt,
+                       (int64_t*)out};
+    hipLaunchKernelGGL(sample_topk_rows, dim3(rows), dim3(kWave), 0, (hipStream_t)stream, a, (const uint64_t*)seed,
+                       (const int64_t*)position);
+    return moss_launch_status();
+}
+
+MOSS_API int moss_sample_topk_pair(const void* logits_a, int rows_a, int stride_a, int vocab_a, float temperature_a,
+                                   int top_k_a, float top_p_a, int salt_a, void* out_a, const void* logits_b,
+                                   int rows_b, int stride_b, int vocab_b, float temperature_b, int top_k_b,
+                                   float top_p_b, int salt_b, void* out_b, const void* seed, const void* position,
+                                   void* stream) {
+    MOSS_CHECK_ARG(sample_args_ok(logits_a, rows_a, stride_a, vocab_a, temperature_a, top_k_a, out_a));
+    MOSS_CHECK_ARG(sample_args_ok(logits_b, rows_b, stride_b, vocab_b, temperature_b, top_k_b, out_b));
+    MOSS_CHECK_ARG(seed && position && MOSS_ALIGNED(seed, 8) && MOSS_ALIGNED(position, 8));
+    const SampleRows a{(const uint16_t*)logits_a, stride_a, vocab_a, temperature_a, top_k_a, top_p_a,
+                       (uint32_t)salt_a, (int64_t*)out_a};
+    const SampleRows b{(const uint16_t*)logits_b, stride_b, vocab_b, temperature_b, top_k_b, top_p_b,
+                       (uint32_t)salt_b, (int64_t*)out_b};
+    hipLaunchKernelGGL(sample_topk_pair, dim3(rows_a + rows_b), dim3(kWave), 0, (hipStream_t)stream, a, rows_a, b,
+                       (const uint64_t*)seed, (const int64_t*)position);
     return moss_launch_status();
 }
 

@@ -185,11 +185,13 @@ class DecodeStepG32:
         text top-2 at temperature 1.5, audio top-25 / top-p 0.8 at temperature 1.7, or argmax when
         greedy."""
         n_audio = CODEBOOKS * self.audio_stride
-        sampling.sample_topk(logits[n_audio:n_audio + 2], 0.0 if self.greedy else 1.5, 2, 1.0, seed=self.seed_buf,
-                             position=self.position, salt=1, out=self.text_index)
-        sampling.sample_topk(logits[:head_count * self.audio_stride].view(head_count, self.audio_stride),
-                             0.0 if self.greedy else 1.7, 25, 0.8, seed=self.seed_buf, position=self.position, salt=0,
-                             vocab=SAMPLED_CODES, out=self.audio_index[:head_count])
+        sampling.sample_topk_pair(
+            dict(logits=logits[n_audio:n_audio + 2], temperature=0.0 if self.greedy else 1.5, top_k=2, top_p=1.0,
+                 salt=1, out=self.text_index),
+            dict(logits=logits[:head_count * self.audio_stride].view(head_count, self.audio_stride),
+                 temperature=0.0 if self.greedy else 1.7, top_k=25, top_p=0.8, salt=0, vocab=SAMPLED_CODES,
+                 out=self.audio_index[:head_count]),
+            seed=self.seed_buf, position=self.position)
         sampling.compose_next_ids(self.text_index, self.audio_index, self.text_ids, self.audio_length,
                                   self.delay_length, delay_slot_id=int(self.text_ids_host[1]),
                                   audio_end_id=self.audio_end_id, out=self.next_ids)

@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "moss_w4a8_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4a8_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_sample_topk": [_P, _I, _I, _I, _F, _I, _F, _P, _P, _I, _P, _P],
+    "moss_sample_topk_pair": [_P, _I, _I, _I, _F, _I, _F, _I, _P, _P, _I, _I, _I, _F, _I, _F, _I, _P, _P, _P, _P],
     "moss_compose_next_ids": [_P, _P, _P, _P, _P, ctypes.c_longlong, ctypes.c_longlong, _I, ctypes.c_longlong, _P, _P],
     "moss_advance_step": [_P, _P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong,
                           _P],

@@ -66,6 +66,37 @@ def sample_topk(logits: torch.Tensor, temperature: float = 1.7, top_k: int = 25,
     return out
 
 
+def _sample_set(logits, temperature, top_k, top_p, vocab, out):
+    _cuda_contig("logits", logits, torch.bfloat16)
+    rows = 1 if logits.dim() == 1 else logits.shape[0]
+    stride = logits.shape[-1]
+    vocab = stride if vocab is None else int(vocab)
+    _require(0 < vocab <= min(stride, MAX_VOCAB), f"vocab must be in [1, min(stride, {MAX_VOCAB})]")
+    if temperature > 0:
+        _require(1 <= top_k <= min(MAX_TOP_K, vocab), f"top_k must be in [1, min({MAX_TOP_K}, vocab)]")
+    _cuda_contig("out", out, torch.int64, logits.device)
+    _require(out.numel() == rows, f"out must hold {rows} indices")
+    return (native.ptr(logits), rows, stride, vocab, float(temperature), int(top_k), float(top_p))
+
+
+def sample_topk_pair(a: dict, b: dict, *, seed: torch.Tensor, position: torch.Tensor) -> None:
+    """Two :func:`sample_topk` calls sharing ``seed`` and ``position`` in one launch (the decode
+    step's text row and audio rows, ``llm.py:280,284``); each of ``a`` and ``b`` holds ``logits``,
+    ``temperature``, ``top_k``, ``top_p``, ``salt``, ``out`` and optionally ``vocab``.  The outputs
+    equal the two separate calls'."""
+    sets = []
+    for d in (a, b):
+        head = _sample_set(d["logits"], d["temperature"], d["top_k"], d["top_p"], d.get("vocab"), d["out"])
+        _require(d["logits"].device == a["logits"].device, "both sets on one device")
+        sets.append(head + (int(d["salt"]), native.ptr(d["out"])))
+    dev = a["logits"].device
+    for name, t in (("seed", seed), ("position", position)):
+        _cuda_contig(name, t, torch.int64, dev)
+        _require(t.numel() == 1, f"{name} holds one value")
+    native.call("moss_sample_topk_pair", *sets[0], *sets[1], native.ptr(seed), native.ptr(position),
+                native.stream_of(a["logits"]))
+
+
 def compose_next_ids(text_index: torch.Tensor, audio_index: torch.Tensor, text_ids: torch.Tensor,
                      audio_length: torch.Tensor, delay_length: torch.Tensor, *, delay_slot_id: int,
                      audio_end_id: int, pad_code: int = 1024, out: torch.Tensor | None = None) -> torch.Tensor:

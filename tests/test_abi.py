@@ -116,6 +116,12 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_sample_topk(p, 1, 100, 100, f(1.0), 1, f(0.8), null, p, 0, p, null) == 1     # seed buffer
     assert lib.moss_sample_topk(p, 1, 100, 100, f(1.0), 1, f(0.8), ctypes.c_void_p(4100), p, 0, p,
                                 null) == 1                                                        # seed alignment
+    pair_ok = (p, 1, 2, 2, f(1.5), 2, f(1.0), 1, p, p, 32, 1025, 1024, f(1.7), 25, f(0.8), 0, p)
+    bad_vocab = pair_ok[:10] + (32, 4096, 4096) + pair_ok[13:]
+    assert lib.moss_sample_topk_pair(*bad_vocab, p, p, null) == 1                                 # vocab <= 2048
+    bad_k = pair_ok[:5] + (3,) + pair_ok[6:]
+    assert lib.moss_sample_topk_pair(*bad_k, p, p, null) == 1                                     # top_k <= vocab
+    assert lib.moss_sample_topk_pair(*pair_ok, null, p, null) == 1                                # seed buffer
     assert lib.moss_compose_next_ids(p, p, p, p, p, 0, 0, 0, 1024, p, null) == 1                  # channels
     q = ctypes.c_void_p(8192)
     assert lib.moss_w4a8_norm_gemv(p, null, p, null, f(1e-6), p, p, p, p, 12288, 64, 0, null) == 1   # K

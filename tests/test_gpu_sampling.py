@@ -65,6 +65,33 @@ def test_sampling_matches_oracle_draws(dev, temperature, top_k, top_p, rows, str
                             f"pos {position} seed {seed} row {r}")
 
 
+@pytest.mark.parametrize("greedy", [False, True])
+def test_sample_pair_equals_two_calls(dev, greedy):
+    """One launch for two row sets (the decode step's text row and 32 audio rows) returns what the
+    two separate sample_topk calls return, over positions and seeds (the sets restart their row
+    numbers, so each keeps its own random stream)."""
+    from moss_tts._runtime import sampling
+
+    text = _logits(1, 2, 5).to(dev).view(-1)
+    audio = _logits(32, 1025, 6).to(dev)
+    for position in (0, 9, 2047, 2**33 + 5):
+        pos = torch.tensor([position], dtype=torch.int64, device=dev)
+        for seed in (0, 987654321):
+            print(f"sample pair greedy={greedy} position={position} seed={seed}", flush=True)
+            sb = sampling.seed_buffer(seed, dev)
+            t_ref = sampling.sample_topk(text, 0.0 if greedy else 1.5, 2, 1.0, seed=sb, position=pos, salt=1)
+            a_ref = sampling.sample_topk(audio, 0.0 if greedy else 1.7, 25, 0.8, seed=sb, position=pos, salt=0,
+                                         vocab=1024)
+            t_out = torch.full((1,), -1, dtype=torch.int64, device=dev)
+            a_out = torch.full((32,), -1, dtype=torch.int64, device=dev)
+            sampling.sample_topk_pair(
+                dict(logits=text, temperature=0.0 if greedy else 1.5, top_k=2, top_p=1.0, salt=1, out=t_out),
+                dict(logits=audio, temperature=0.0 if greedy else 1.7, top_k=25, top_p=0.8, salt=0, vocab=1024,
+                     out=a_out),
+                seed=sb, position=pos)
+            assert torch.equal(t_out, t_ref) and torch.equal(a_out, a_ref)
+
+
 def _candidate_count(row_logits: np.ndarray, temperature: float, top_k: int) -> int:
     """How many keys the kernel's threshold keeps: those >= the k-th largest per-lane maximum
     (lane l holds indices l + 64 j).  Tells which selection branch a case exercises."""
