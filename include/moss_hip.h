@@ -96,8 +96,10 @@ int moss_w4g32_gateup_silu(const void *x, const void *qw, const void *sc, const 
  * res == NULL:  xn = rmsnorm(x) * norm_w;
  * res != NULL:  s = bf16(x + res) is stored to sum_out (which must not overlap x or res) and
  *               xn = rmsnorm(s) * norm_w.
- * Rounding points and summation order are those of moss_rmsnorm, so the result is bit-identical
- * to moss_rmsnorm followed by moss_w4g32_gemv.  K % 2048 == 0, K <= 8192, M is 1.
+ * Rounding points and summation order are those of moss_rmsnorm, so the normalized row is
+ * bit-identical to moss_rmsnorm's, and for K <= 4096 the result is bit-identical to moss_rmsnorm
+ * followed by moss_w4g32_gemv (at K = 8192 that GEMV splits K over two waves, and the two results
+ * differ only by that fp32 summation order).  K % 2048 == 0, K <= 8192, M is 1.
  * Replaces the fused add+RMSNorm+quant+projection of
  * src/moss_tts/_runtime/dp4a_norm_projection.py:48-166 (and gateup_cluster.py:44-157). */
 int moss_w4g32_norm_gemv(const void *x, const void *res, const void *norm_w, void *sum_out, float eps, const void *qw,

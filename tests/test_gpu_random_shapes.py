@@ -1,7 +1,8 @@
 """GPU parity at seeded random shapes inside the documented limits, beside the hand-picked shapes of
 the other tests: INT4-G32 GEMV and gate||up (both dequant modes, every rows-per-wave choice), the
-INT4 GEMM (small-M streaming, tiles, K splits), the FP8 linear (GEMV and GEMM), and decode and
-prompt attention at random cache lengths, positions and start rows.
+same with the (add-)RMSNorm fused in (bit-identical to norm then projection), the W4A8 integer-dot
+GEMV and gate||up, the INT4 GEMM (small-M streaming, tiles, K splits), the FP8 linear (GEMV and
+GEMM), and decode and prompt attention at random cache lengths, positions and start rows.
 
 Reference: fp32 torch math on the same inputs; for INT4 the weights are the bit-exact dequant
 (itself pinned bit for bit against the oracle in test_gpu_w4g32.py), for FP8 the exact e4m3 -> bf16
@@ -64,7 +65,24 @@ def _prefill_cases(count):
     return out
 
 
+def _norm_cases(count):
+    out = []
+    for _ in range(count):
+        out.append((2048 * _rng.choice((1, 2, 4)), 2 * _rng.randint(1, 3000), _rng.choice((0, 1, 2, 4)),
+                    _rng.random() < 0.5))
+    return out
+
+
+def _w4a8_cases(count):
+    out = []
+    for _ in range(count):
+        out.append((64 * _rng.randint(1, 256), 2 * _rng.randint(1, 3000), _rng.choice((0, 1, 2, 4))))
+    return out
+
+
 GEMV = _gemv_cases(12)
+NORM = _norm_cases(8)
+W4A8 = _w4a8_cases(8)
 GEMM = _gemm_cases(12)
 FP8 = _fp8_cases(12)
 DECODE = _decode_cases(12)
@@ -97,6 +115,54 @@ def test_gemv_random_shape(dev, k, n, rows, mode):
         gate, up = ref[:, :half].bfloat16().float(), ref[:, half:].bfloat16().float()
         want = torch.nn.functional.silu(gate).bfloat16().float() * up
         assert _rel(w4g32.gateup_silu(x, pw, rows_per_wave=rows, dequant=mode), want) < TOL
+
+
+@pytest.mark.parametrize("k,n,rows,residual", NORM)
+def test_fused_norm_random_shape(dev, k, n, rows, residual):
+    """The (add-)RMSNorm fused into the GEMV and the gate||up equals norm then projection bit for bit
+    for K <= 4096; at K = 8192 the plain projection splits K over two waves, so the two agree to the
+    bar instead (same normalized row, different fp32 summation order)."""
+    from moss_tts._runtime import pointwise, w4g32
+
+    print(f"fused norm K={k} N={n} rows={rows} residual={residual}", flush=True)
+    pw, g = _packed(n, k, 7 * k + n, dev)
+    x = torch.randn((1, k), device=dev, generator=g).bfloat16()
+    res = torch.randn((1, k), device=dev, generator=g).bfloat16() if residual else None
+    nw = (1 + 0.01 * torch.randn(k, device=dev, generator=g)).bfloat16()
+    if residual:
+        summed, xn = pointwise.add_rmsnorm(x, res, nw, 1e-6)
+        s2, y = w4g32.norm_gemv(x, nw, 1e-6, pw, residual=res, rows_per_wave=rows)
+        s3, yg = w4g32.norm_gateup_silu(x, nw, 1e-6, pw, residual=res, rows_per_wave=rows)
+        assert torch.equal(s2, summed) and torch.equal(s3, summed)
+    else:
+        xn = pointwise.rmsnorm(x, nw, 1e-6)
+        y = w4g32.norm_gemv(x, nw, 1e-6, pw, rows_per_wave=rows)
+        yg = w4g32.norm_gateup_silu(x, nw, 1e-6, pw, rows_per_wave=rows)
+    y_ref = w4g32.gemv(xn, pw, rows_per_wave=rows)
+    yg_ref = w4g32.gateup_silu(xn, pw, rows_per_wave=rows)
+    if k <= 4096:
+        assert torch.equal(y, y_ref) and torch.equal(yg, yg_ref)
+    else:
+        assert _rel(y, y_ref) < TOL and _rel(yg, yg_ref) < TOL
+
+
+@pytest.mark.parametrize("k,n,rows", W4A8)
+def test_w4a8_random_shape(dev, k, n, rows):
+    """The integer-dot GEMV and gate||up against fp32 math on the same int8 activations (codes times
+    group scales) and the dequantized weights."""
+    from moss_tts._runtime import w4a8, w4g32
+
+    print(f"w4a8 K={k} N={n} rows={rows}", flush=True)
+    pw, g = _packed(n, k, 11 * k + n, dev)
+    x = torch.randn((1, k), device=dev, generator=g).bfloat16()
+    act = w4a8.quantize(x.view(-1))
+    xq = (act.natural().float().view(-1, 32) * act.scales.view(-1, 1)).view(1, k)
+    ref = xq @ w4g32.dequantize(pw).float().t()
+    assert _rel(w4a8.linear(None, pw, prequantized=act, rows_per_wave=rows), ref) < TOL
+    half = n // 2
+    gate, up = ref[:, :half].bfloat16().float(), ref[:, half:].bfloat16().float()
+    want = torch.nn.functional.silu(gate).bfloat16().float() * up
+    assert _rel(w4a8.linear(None, pw, paired=True, prequantized=act, rows_per_wave=rows), want) < TOL
 
 
 @pytest.mark.parametrize("m,k,n", GEMM)
