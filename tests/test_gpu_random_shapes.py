@@ -80,6 +80,22 @@ def _w4a8_cases(count):
     return out
 
 
+def _bf16_cases(count):
+    out = []
+    for _ in range(count):
+        out.append((512 * _rng.choice((1, 2, 3, 4, 5, 6, 7, 8, 12, 16)), _rng.randint(1, 5000),
+                    _rng.choice((0, 1, 2, 4))))
+    return out
+
+
+def _w4a8_norm_cases(count):
+    out = []
+    for _ in range(count):
+        out.append((2048 * _rng.choice((1, 2, 4)), 2 * _rng.randint(1, 3000), _rng.random() < 0.5,
+                    _rng.random() < 0.5, _rng.choice((0, 1, 2, 4))))
+    return out
+
+
 GEMV = _gemv_cases(12)
 NORM = _norm_cases(8)
 W4A8 = _w4a8_cases(8)
@@ -87,6 +103,10 @@ GEMM = _gemm_cases(12)
 FP8 = _fp8_cases(12)
 DECODE = _decode_cases(12)
 PREFILL = _prefill_cases(12)
+BF16 = _bf16_cases(8)
+BF16_NORM = [(2048 * _rng.choice((1, 2, 4)), _rng.randint(1, 5000), _rng.random() < 0.5) for _ in range(6)]
+FP8_GATEUP = [(16 * _rng.randint(1, 512), _rng.randint(1, 3000), _rng.choice((0, 1, 2, 4))) for _ in range(8)]
+W4A8_NORM = _w4a8_norm_cases(8)
 
 
 def _rel(a, b):
@@ -228,3 +248,71 @@ def test_prefill_attention_random_shape(dev, L, n, start):
     y = attention.prefill_attention(q, kc, vc, torch.tensor([start], device=dev)).view(n, 32, 128)
     ref = _attention_ref(q, kc[0], vc[0], start + torch.arange(n, device=dev))
     assert _rel(y, ref) < TOL
+
+
+@pytest.mark.parametrize("k,n,rows", BF16)
+def test_bf16_gemv_random_shape(dev, k, n, rows):
+    from moss_tts._runtime import bf16
+
+    print(f"bf16 gemv K={k} N={n} rows={rows}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(3 * k + n)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).bfloat16()
+    x = torch.randn((1, k), device=dev, generator=g).bfloat16()
+    assert _rel(bf16.gemv(x, w, rows_per_wave=rows), x.float() @ w.float().t()) < TOL
+
+
+@pytest.mark.parametrize("k,n,residual", BF16_NORM)
+def test_bf16_norm_gemv_random_shape(dev, k, n, residual):
+    """The fused (add-)RMSNorm + bf16 GEMV equals the norm then the GEMV bit for bit."""
+    from moss_tts._runtime import bf16, pointwise
+
+    print(f"bf16 norm gemv K={k} N={n} residual={residual}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(5 * k + n)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).bfloat16()
+    x = (torch.randn((1, k), device=dev, generator=g) * 3).bfloat16()
+    nw = (1 + 0.01 * torch.randn(k, device=dev, generator=g)).bfloat16()
+    if residual:
+        r = torch.randn((1, k), device=dev, generator=g).bfloat16()
+        s, y = bf16.norm_gemv(x, nw, 1e-6, w, residual=r)
+        s_ref, h = pointwise.add_rmsnorm(x, r, nw, 1e-6)
+        assert torch.equal(s, s_ref)
+    else:
+        y, h = bf16.norm_gemv(x, nw, 1e-6, w), pointwise.rmsnorm(x, nw, 1e-6)
+    assert torch.equal(y, bf16.gemv(h, w))
+    assert _rel(y, h.float() @ w.float().t()) < TOL
+
+
+@pytest.mark.parametrize("k,n_half,rows", FP8_GATEUP)
+def test_fp8_gateup_random_shape(dev, k, n_half, rows):
+    from moss_tts._runtime import fp8
+
+    print(f"fp8 gate||up K={k} N/2={n_half} rows={rows}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(k + 7 * n_half)
+    wb = torch.randint(0, 256, (2 * n_half, k), device=dev, dtype=torch.uint8, generator=g)
+    wb[(wb & 0x7F) == 0x7F] = 0  # no NaN codes
+    s = torch.rand((2 * n_half,), device=dev, generator=g) * 0.01 + 0.005
+    x = torch.randn((1, k), device=dev, generator=g).bfloat16()
+    ref = (x.float() @ fp8.to_bf16(wb).float().t()) * s
+    gate, up = ref[:, :n_half].bfloat16().float(), ref[:, n_half:].bfloat16().float()
+    want = torch.nn.functional.silu(gate).bfloat16().float() * up
+    assert _rel(fp8.fp8_silu_decode(x, wb, s, rows_per_wave=rows), want) < TOL
+
+
+@pytest.mark.parametrize("k,n,paired,residual,rows", W4A8_NORM)
+def test_w4a8_fused_norm_random_shape(dev, k, n, paired, residual, rows):
+    """(add+)RMSNorm + quantizer + W4A8 projection in one kernel equals norm_quant followed by the
+    projection on its activations, bit for bit."""
+    from moss_tts._runtime import w4a8
+
+    print(f"w4a8 fused norm K={k} N={n} paired={paired} residual={residual} rows={rows}", flush=True)
+    pw, g = _packed(n, k, 13 * k + n, dev)
+    x = (torch.randn((1, k), device=dev, generator=g) * 3).bfloat16()
+    r = torch.randn((1, k), device=dev, generator=g).bfloat16() if residual else None
+    nw = (1 + 0.1 * torch.randn(k, device=dev, generator=g)).bfloat16()
+    summed, _, act = w4a8.norm_quant(x, r, nw, 1e-6, normalized=False)
+    want = w4a8.linear(None, pw, paired=paired, prequantized=act, rows_per_wave=rows)
+    got = w4a8.norm_linear(x, nw, 1e-6, pw, residual=r, paired=paired, rows_per_wave=rows)
+    if residual:
+        got_sum, got = got
+        assert torch.equal(got_sum, summed)
+    assert torch.equal(got.view(-1), want.view(-1))
