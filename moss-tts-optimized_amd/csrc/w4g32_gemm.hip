@@ -11,10 +11,11 @@
 // epilogue (src/moss_tts/_runtime/fused_mlp.py:20-21).  The fp8 MFMA forms are not used:
 // they would round the bf16 activations to e4m3 as well.
 //
-// INT4 takes the register-weight tile (w4g32_gemm_t_kernel) wherever its shape conditions hold
-// (reg_tile_shape): the dequantized weights are the MFMA's A operand straight from the
-// registers that dequantize them, and only the activations are staged in LDS.  FP8, other INT4
-// shapes and misaligned scale or zero-point pointers take the LDS tiles:
+// INT4 takes the register-weight tile wherever its shape conditions hold (reg_tile_shape): the
+// dequantized weights are the MFMA's A operand straight from the registers that dequantize them,
+// and only the activations are staged in LDS (w4g32_gemm_t_kernel up to 64 tokens per tile;
+// w4g32_gemm_tdma_kernel, whose activations go from global memory to LDS without registers, for
+// 128).  FP8, other INT4 shapes and misaligned scale or zero-point pointers take the LDS tiles:
 //
 // LDS tiles: BM x BN outputs (BM, BN in {64, 128}) per 256-thread workgroup, 2 x 2 waves of
 // (BM/2) x (BN/2), K in steps of 64 (two quantization groups).  Pipeline: two LDS buffers and
@@ -30,6 +31,7 @@
 #include "common.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace moss {
 namespace {
@@ -469,6 +471,182 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
     }
 }
 
+// The 128-token register-weight tile (M > 64) with the activations copied from global memory
+// straight into LDS (global_load_lds_dwordx4: lane i of an instruction writes bytes 16 i .. + 15
+// of a 1 KiB span), so no registers stage them and no LDS stores are issued: 150 VGPRs, three
+// workgroups per CU (768 gate||up tiles at M = 512 run in one round instead of 1.5).  Weights,
+// operands, MFMA order and results are those of w4g32_gemm_t_kernel<4, SPLIT>, bit for bit.
+// LDS layout: two buffers of 128 token rows x 128 bytes (one K step), chunk c (8 bf16) of row r
+// stored at position c ^ (r & 7) ^ ((r >> 3) & 1): the 16 lanes that read one chunk of 16
+// consecutive rows in one LDS cycle (64 banks) hit 16 different 16-byte bank groups (r & 7 alone
+// pairs rows r and r + 8 on the same banks: 4 conflict cycles per read, by counters); the eight
+// lanes per row of a copy instruction still read that row's 128 contiguous bytes.  The buffers are distinct variables, which lets the compiler see
+// that reading one does not wait for the copy into the other.
+// Step s: copy step s + 1 into the other buffer, multiply step s, load the codes of step s + kTs
+// (and the next block's scales and zeros after a block's last step), then wait until this wave's
+// copy has landed -- at most the loads issued after it still outstanding (vector memory requests
+// complete in order) -- and meet the other waves at the barrier.  The waits are explicit because
+// the compiler only knows that a copy must land before this wave reads it, not before other waves
+// do.  qw, sc and zp carry no __restrict__, so the compiler barriers (asm memory clobbers) keep
+// those loads in program order around the copies and the waits; the block loop runs in pairs so
+// that every load lands in the register it is read from (a register copy would wait for it).
+__device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt not waited): vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8
+#define MOSS_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+
+template <bool SPLIT>
+__global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t* __restrict__ X, const uint4* qw,
+                                                              const uint16_t* sc, const uint8_t* zp,
+                                                              uint16_t* __restrict__ Y, float* __restrict__ part,
+                                                              int M, int N, int K) {
+    constexpr int BN = 128, BM = 128, JT = 4;
+    __shared__ __attribute__((aligned(1024))) uint16_t Xa[BM * kBK];
+    __shared__ __attribute__((aligned(1024))) uint16_t Xb[BM * kBK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mt = (M + BM - 1) / BM, tiles = gridDim.x;
+    int tile = blockIdx.x;
+    if (tiles % kXcds == 0) tile = (blockIdx.x % kXcds) * (tiles / kXcds) + blockIdx.x / kXcds;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+    const int G = K >> 5, steps = SPLIT ? K / kBK / gridDim.y : K / kBK;
+    const int kbase = SPLIT ? blockIdx.y * steps * kBK : 0;  // a multiple of kTs steps (8 groups)
+    // copy instruction c of wave w fills rows 8 (4 w + c) .. + 7; lane i writes position i & 7 of
+    // row r = 8 (4 w + c) + i / 8, i.e. chunk (i & 7) ^ (r & 7) ^ ((r >> 3) & 1) of it, with
+    // r & 7 = (i >> 3) & 7 and (r >> 3) & 1 = c & 1 (rows past M copy row M - 1; those outputs
+    // are not stored)
+    const uint16_t* xsrc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int r = 8 * (4 * wave + c) + (lane >> 3);
+        xsrc[c] = X + (size_t)min(m0 + r, M - 1) * K + kbase + 8 * ((lane & 7) ^ ((lane >> 3) & 7) ^ (c & 1));
+    }
+    auto copy_x = [&](uint16_t* buf, int k0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) __builtin_amdgcn_global_load_lds(xsrc[c] + k0, buf + 512 * (4 * wave + c), 16, 0, 0);
+    };
+    // operand kk of token tile j: row 32 j + (l & 31), chunk 4 half + kk of the step
+    const int half = lane >> 5;
+    const int swz = (lane & 7) ^ ((lane >> 3) & 1);
+    uint32_t roff[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) roff[kk] = 128u * (uint32_t)(lane & 31) + 16u * (uint32_t)((4 * half + kk) ^ swz);
+    const size_t wrow = (size_t)min(n0 + 32 * wave + (lane & 31), N - 1);
+    auto load_w = [&](uint4& w, int k0) { w = qw[wrow * G + ((kbase + k0) >> 5) + half]; };
+    auto load_blk = [&](TBlock& t, int blk) {
+        const int g = (kbase >> 5) + 8 * blk;
+        int zb;
+        zero_loc(g, G, zb, t.zsh);
+        t.s = *reinterpret_cast<const uint4*>(sc + wrow * G + g);
+        t.z = *reinterpret_cast<const uint2*>(zp + wrow * (G >> 1) + zb);
+    };
+
+    f32x16_t acc[JT];
+#pragma unroll
+    for (int j = 0; j < JT; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+
+    const int blocks = steps / kTs;
+    uint4 cw[kTs];
+    TBlock tb[2];  // block b's scales and zeros in tb[b & 1]
+    copy_x(Xa, 0);
+    cbar();
+    load_blk(tb[0], 0);
+    load_blk(tb[1], min(1, blocks - 1));
+#pragma unroll
+    for (int i = 0; i < kTs; ++i) load_w(cw[i], min(i, steps - 1) * kBK);
+    cbar();
+    MOSS_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+    cbar();
+    uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
+    asm volatile("" : "+v"(mask), "+v"(bias_bits));
+    // I: step within the block, P: which tb holds the block's scales, LAST: the last block, whose
+    // refills are never read (the compiler drops them, so its waits count nothing after the copy)
+    auto step = [&](auto ic, auto pc, auto lc, int blk, const uint16_t* rd, uint16_t* wr) {
+        constexpr int i = decltype(ic)::value, P = decltype(pc)::value;
+        constexpr bool LAST = decltype(lc)::value;
+        const TBlock& cur = tb[P];
+        const int s = blk * kTs + i;
+        copy_x(wr, min(s + 1, steps - 1) * kBK);  // the last step's copy (unread) is drained below
+        cbar();
+        const uint32_t sw = i == 0 ? cur.s.x : i == 1 ? cur.s.y : i == 2 ? cur.s.z : cur.s.w;
+        const uint32_t zw = i < 2 ? cur.z.x : cur.z.y;
+        const uint32_t s_lo = (sw >> (16 * half)) & 0xffffu, s_hi = s_lo << 16;
+        const uint32_t zq = (zw >> (8 * (2 * (i & 1) + half) + cur.zsh)) & 15u;
+        const float bias = -(128.0f + (float)zq) * bf16_bits((uint16_t)s_lo);
+        const char* xs = reinterpret_cast<const char*>(rd);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            bf16x8_t b[JT];
+#pragma unroll
+            for (int j = 0; j < JT; ++j) b[j] = *reinterpret_cast<const bf16x8_t*>(xs + roff[kk] + 4096 * j);
+            const uint32_t wd = kk == 0 ? cw[i].x : kk == 1 ? cw[i].y : kk == 2 ? cw[i].z : cw[i].w;
+            uint32_t wf[4];
+            dequant_word_exact((wd & mask) | bias_bits, ((wd >> 4) & mask) | bias_bits, ((wd >> 8) & mask) | bias_bits,
+                               ((wd >> 12) & mask) | bias_bits, s_lo, s_hi, bias, wf);
+            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{wf[0], wf[1], wf[2], wf[3]});
+#pragma unroll
+            for (int j = 0; j < JT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], acc[j], 0, 0, 0);
+        }
+        pin();
+        // code slot i, and after the block's last step its scales, are free: refill them
+        load_w(cw[i], min(s + kTs, steps - 1) * kBK);
+        if (i == kTs - 1) load_blk(tb[P], min(blk + 2, blocks - 1));
+        cbar();
+        if (LAST) MOSS_WAIT_VM(0);
+        else if (i == kTs - 1) MOSS_WAIT_VM(3);  // one code load, two block loads after the copy
+        else MOSS_WAIT_VM(1);                    // one code load after the copy
+        __builtin_amdgcn_s_barrier();
+        cbar();
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    using No = std::false_type;
+    using Yes = std::true_type;
+    int blk = 0;
+    for (; blk + 1 < blocks; blk += 2) {
+        step(S0{}, S0{}, No{}, blk, Xa, Xb);
+        step(S1{}, S0{}, No{}, blk, Xb, Xa);
+        step(S2{}, S0{}, No{}, blk, Xa, Xb);
+        step(S3{}, S0{}, No{}, blk, Xb, Xa);
+        step(S0{}, S1{}, No{}, blk + 1, Xa, Xb);
+        step(S1{}, S1{}, No{}, blk + 1, Xb, Xa);
+        step(S2{}, S1{}, No{}, blk + 1, Xa, Xb);
+        step(S3{}, S1{}, No{}, blk + 1, Xb, Xa);
+    }
+    if (blk < blocks) {
+        step(S0{}, S0{}, Yes{}, blk, Xa, Xb);
+        step(S1{}, S0{}, Yes{}, blk, Xb, Xa);
+        step(S2{}, S0{}, Yes{}, blk, Xa, Xb);
+        step(S3{}, S0{}, Yes{}, blk, Xb, Xa);
+    }
+    MOSS_WAIT_VM(0);  // every copy has landed before the workgroup's LDS is released
+    // C[n][m] of the 32 x 32 tile (n0 + 32 wave, m0 + 32 j): as in w4g32_gemm_t_kernel
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+        const int m = m0 + 32 * j + (lane & 31);
+        if (m >= M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = n0 + 32 * wave + 8 * q + 4 * (lane >> 5);
+            if (n >= N) continue;
+            const float v0 = acc[j][4 * q], v1 = acc[j][4 * q + 1], v2 = acc[j][4 * q + 2], v3 = acc[j][4 * q + 3];
+            if constexpr (SPLIT) {
+                *reinterpret_cast<float4*>(part + ((size_t)blockIdx.y * M + m) * N + n) = make_float4(v0, v1, v2, v3);
+            } else {
+                uint2 o;
+                o.x = pack_bf16x2(v0, v1);
+                o.y = pack_bf16x2(v2, v3);
+                *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
+            }
+        }
+    }
+}
+
 // y[m, n] = bf16(scale[n] * sum_z part[z, m, n]), z ascending; 4 outputs per thread (N % 4 == 0).
 __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ part, const float* __restrict__ row_scale,
                                                    uint16_t* __restrict__ Y, int MN, int N, int S) {
@@ -715,7 +893,7 @@ bool reg_tile_shape(int K, int N, bool int4) {
 }
 
 // INT4: the register-weight tile, 32, 64 or 128 tokens deep.  M > 64 (MFMA-bound): split K (2..8,
-// >= 2 blocks each) while the doubled workgroup count still fits two per CU.  M <= 64 (bound by
+// >= 2 blocks each) while the doubled workgroup count still fits one per CU.  M <= 64 (bound by
 // the weight stream): split while the workgroups fit two per CU and the fp32 partials (written
 // and read back once) stay below half the weight bytes.  Shapes it does not take use the LDS
 // tiles: 64-row tiles for M <= 64; 128-wide N tiles when they already give >= 256 workgroups; a
@@ -734,7 +912,11 @@ Plan plan_gemm(int M, int K, int N, bool int4) {
         const long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + 127) / 128);
         const int steps = K / kBK;
         const double wbytes = (double)N * K * 0.5625;  // codes, scales, zero points
-        while (p.split < 16 && tiles * p.split * 2 <= 512 && steps % (2 * p.split * kTs) == 0 &&
+        // M > 64 (the LDS-copy tile, three workgroups per CU): split only up to one workgroup per
+        // CU; measured over M = 128 .. 2048, a deeper split costs more in partial sums and their
+        // reduction than the extra workgroups gain
+        const long cap = M <= 64 ? 512 : 256;
+        while (p.split < 16 && tiles * p.split * 2 <= cap && steps % (2 * p.split * kTs) == 0 &&
                (M <= 64 ? 2.0 * p.split * M * N * 4 <= 0.5 * wbytes
                         : (p.split < 8 && steps / (2 * p.split) >= 2 * kTs)))
             p.split *= 2;
@@ -787,6 +969,15 @@ template <int JT>
 void launch_reg(const Plan& p, const void* x, const void* qw, const void* sc, const void* zp, void* y, void* ws,
                 int M, int K, int N, hipStream_t st) {
     const dim3 grid((unsigned)(((M + 32 * JT - 1) / (32 * JT)) * ((N + 127) / 128)), (unsigned)p.split);
+    if constexpr (JT == 4) {
+        if (p.split > 1)
+            hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<true>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
+        else
+            hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<false>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
+        return;
+    }
     if (p.split > 1)
         hipLaunchKernelGGL((w4g32_gemm_t_kernel<JT, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
                            (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);

@@ -61,8 +61,11 @@ def test_host_only_entry_points(lib):
     ws = lib.moss_gemm_workspace_bytes(64, 4096, 4096)                            # M=64: K split over workgroups
     assert ws > 0 and ws % (64 * 4096 * 4) == 0 and ws // (64 * 4096 * 4) in (2, 4, 8)
     assert lib.moss_gemm_workspace_bytes(512, 4096, 24576) == 0                   # prefill tiles fill the GPU
-    assert lib.moss_gemm_workspace_bytes(512, 4096, 6144) == 2 * 512 * 6144 * 4   # 192 INT4 tiles: K split in 2
-    assert lib.moss_gemm_workspace_bytes(512, 12288, 4096) == 4 * 512 * 4096 * 4  # 128 INT4 tiles: K split in 4
+    # INT4 tiles of 128 tokens: the K split doubles while the workgroups fit one per CU
+    assert lib.moss_gemm_workspace_bytes(512, 4096, 6144) == 0                    # 192 tiles: no split
+    assert lib.moss_gemm_workspace_bytes(512, 4096, 4096) == 2 * 512 * 4096 * 4   # 128 tiles: K split in 2
+    assert lib.moss_gemm_workspace_bytes(512, 12288, 4096) == 2 * 512 * 4096 * 4
+    assert lib.moss_gemm_workspace_bytes(128, 12288, 4096) == 8 * 128 * 4096 * 4  # 32 tiles: K split in 8
     # M=16: 32 INT4 tiles of 32 tokens; the split doubles to 16 (512 workgroups) while the partials
     # stay under half the weight bytes
     assert lib.moss_gemm_workspace_bytes(16, 4096, 4096) == 16 * 16 * 4096 * 4

@@ -289,7 +289,7 @@ def test_gemm_parity(dev, m, k, n):
     _assert_rne_or_adjacent(y, ref, abs_sum, k, f"gemm M={m} K={k} N={n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(512, 4096, 6144), (48, 4096, 2056)])
+@pytest.mark.parametrize("m,k,n", [(512, 4096, 4096), (48, 4096, 2056)])
 def test_gemm_fallbacks_match(dev, m, k, n):
     """The C-ABI's fallbacks give the same products: without a workspace the planned K split is
     dropped (one pass over K), and scales or zero points that are not 16 / 8-byte aligned send the
