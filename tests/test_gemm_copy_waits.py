@@ -16,7 +16,10 @@ import pytest
 
 from moss_tts import _build
 
-_VMEM = re.compile(r"^(global_load|global_store|global_atomic|buffer_|scratch_|flat_)")
+# loads only: vector-memory loads complete in order, so a wait that leaves at most N ops
+# outstanding, N = the loads issued after a copy, implies the copy has landed; a store issued after
+# it may complete first and must not be counted
+_VMEM_LOAD = re.compile(r"^(global_load|buffer_load|scratch_load|flat_load)")
 
 
 def _device_asm(tmp_path):
@@ -48,13 +51,14 @@ def _kernel_bodies(lines, needle):
 
 def check_copy_waits(body):
     """Returns the number of barriers checked; raises AssertionError on a barrier (or the end)
-    that a copy of this wave may still be in flight for."""
-    pending = None  # vector-memory instructions issued since the last uncovered copy
+    that a copy of this wave may still be in flight for.  Straight-line scan: the kernel's loop
+    bodies are unrolled and every step ends at a barrier."""
+    pending = None  # vector-memory loads issued since the last uncovered copy
     barriers = 0
     for k, t in enumerate(body):
         if t.startswith("global_load_lds"):
             pending = 0
-        elif _VMEM.match(t):
+        elif _VMEM_LOAD.match(t):
             if pending is not None:
                 pending += 1
         elif t.startswith("s_waitcnt") and "vmcnt" in t:
@@ -75,6 +79,11 @@ def test_check_rejects_a_lax_wait():
         check_copy_waits(body)
     body[2] = "s_waitcnt vmcnt(1)"
     assert check_copy_waits(body) == 1
+    # a store after the copy does not count: vmcnt(1) could pass with the copy still in flight
+    body = ["global_load_lds_dwordx4 v[0:1], off", "scratch_store_dword off, v9, off", "s_waitcnt vmcnt(1)",
+            "s_barrier", "s_endpgm"]
+    with pytest.raises(AssertionError):
+        check_copy_waits(body)
 
 
 def test_copy_tile_waits_cover_every_copy(tmp_path):
