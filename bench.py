@@ -255,6 +255,56 @@ def bf16_heads_bench(torch, dev):
             "bytes": nbytes, "shape": f"K={k}, N={n}"}
 
 
+def pointwise_bench(torch, dev):
+    """The prompt pass's pointwise kernels at 512 tokens: add-RMSNorm (4096 wide), the q/k head
+    RMSNorm + RoPE + KV-cache write, and SiLU*mul (24576 -> 12288).  Inputs are rotated over
+    >= 300 MB of copies so they come from HBM; GB/s counts the bytes each kernel must read and
+    write once."""
+    from moss_tts._runtime import pointwise
+
+    gen = torch.Generator(device=dev).manual_seed(97)
+    n, out = 512, {}
+
+    def copies_for(nbytes):
+        return max(2, -(-300 * 2**20 // nbytes))
+
+    # add-RMSNorm: x and residual in, summed and normalized out
+    nb = 2 * n * HIDDEN * 2
+    xs = [(torch.randn((n, HIDDEN), generator=gen, device=dev)).bfloat16() for _ in range(copies_for(nb))]
+    res = torch.randn((n, HIDDEN), generator=gen, device=dev).bfloat16()
+    nw = (1 + 0.01 * torch.randn(HIDDEN, generator=gen, device=dev)).bfloat16()
+    cases = [("add_rmsnorm_512x4096", [lambda x=x: pointwise.add_rmsnorm(x, res, nw, 1e-6) for x in xs],
+              4 * n * HIDDEN * 2 + 2 * HIDDEN)]
+    # q/k norm + RoPE + KV write: qkv rows in; q, K and V rows out; one cos/sin row per token
+    qkv_w = (pointwise.QH + 2 * pointwise.KH) * pointwise.HD
+    nb = n * qkv_w * 2
+    qkvs = [torch.randn((n, qkv_w), generator=gen, device=dev).bfloat16() for _ in range(copies_for(nb))]
+    qn = (1 + 0.01 * torch.randn(pointwise.HD, generator=gen, device=dev)).bfloat16()
+    kn = (1 + 0.01 * torch.randn(pointwise.HD, generator=gen, device=dev)).bfloat16()
+    ang = torch.arange(n, device=dev, dtype=torch.float32)[:, None] * torch.rand(pointwise.HD, device=dev)
+    cos, sin = ang.cos().bfloat16().contiguous(), ang.sin().bfloat16().contiguous()
+    kc = torch.zeros((1, pointwise.KH, 2048, pointwise.HD), device=dev, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    pos = torch.arange(n, device=dev, dtype=torch.int64)
+    cases.append(("qk_norm_rope_kv_512", [lambda q=q: pointwise.qk_rope(q, qn, kn, cos, sin, kc, vc, pos, 1e-6)
+                                          for q in qkvs],
+                  n * qkv_w * 2 + n * pointwise.QH * pointwise.HD * 2 + 2 * n * pointwise.KH * pointwise.HD * 2
+                  + 2 * n * pointwise.HD * 2))
+    # SiLU*mul: gate||up rows in, the product out
+    nb = n * 2 * INTER * 2
+    gus = [torch.randn((n, 2 * INTER), generator=gen, device=dev).bfloat16() for _ in range(copies_for(nb))]
+    cases.append(("silu_mul_512x12288", [lambda g=g: pointwise.silu_mul(g) for g in gus], nb + n * INTER * 2))
+    for name, fns, nbytes in cases:
+        sec = _per_launch(torch, fns, replays=5)
+        gbs = nbytes / sec / 1e9
+        _log(f"[bench] {name}: {sec * 1e6:.2f} us, {gbs:.0f} GB/s")
+        out[name] = {"us_per_call": round(sec * 1e6, 3), "GB/s": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "copies": len(fns)}
+    del xs, qkvs, gus
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill_bench(torch, dev):
     """INT4-G32 prefill GEMMs at M=512 (QKV N=6144, O N=4096, gate||up N=24576, down K=12288):
     TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak."""
@@ -558,6 +608,7 @@ def main() -> int:
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
     small_m = small_m_bench(torch, dev) if not args.no_extras else None
     heads_bf16 = bf16_heads_bench(torch, dev) if not args.no_extras else None
+    pointwise_lines = pointwise_bench(torch, dev) if not args.no_extras else None
     prefill = prefill_bench(torch, dev) if not args.no_extras else None
     decode = decode_w4a8 = None
     if args.decode_steps > 0:
@@ -630,6 +681,7 @@ def main() -> int:
             "fp8": fp8_lines,
             "int4_small_m": small_m,
             "bf16_heads_k4096_n32770": heads_bf16,
+            "pointwise_512_tokens": pointwise_lines,
             "prefill_gemm": prefill,
         },
     }

@@ -188,6 +188,23 @@ int moss_w4g32_gemm(const void *x, const void *qw, const void *sc, const void *z
 /* Workspace bytes the GEMMs (INT4 and FP8, M > 1) use for an M x K x N problem; 0 = none. */
 long long moss_gemm_workspace_bytes(int M, int K, int N);
 
+/* Prefill gate||up projection with the SiLU*mul epilogue: qw/sc/zp hold 2*N rows (gate rows, then
+ * up rows; N % 4 == 0), y bf16 [M, N] = bf16(bf16(silu(g)) * u) with g, u the bf16 outputs of
+ * moss_w4g32_gemm on those rows -- equal bit for bit to moss_w4g32_gemm (full workspace) followed by
+ * moss_silu_mul.  For M > 64 where the GEMM plan has no K split (Qwen3-8B's gate||up at every
+ * M > 64) the epilogue runs inside the GEMM and no [M, 2N] product is written; otherwise the
+ * product and the GEMM's partial sums go to a caller-owned workspace of
+ * moss_gemm_silu_workspace_bytes(M, K, N) bytes (16-byte aligned; for 16/8-byte aligned sc/zp and
+ * 8-byte aligned y -- otherwise the unfused form runs and needs that workspace too, and a smaller
+ * one is refused with hipErrorInvalidValue).  Replaces F.linear(x, _gate_up) followed by the
+ * prefill SiLU (src/moss_tts/_runtime/llm.py:27-29, prefill_pointwise.py:18-31). */
+int moss_w4g32_gemm_silu(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
+                         void *workspace, long long workspace_bytes, void *stream);
+
+/* Workspace bytes moss_w4g32_gemm_silu needs for an M x K x N problem (N = the SiLU outputs); 0 when
+ * the epilogue runs inside the GEMM. */
+long long moss_gemm_silu_workspace_bytes(int M, int K, int N);
+
 /* moss_w4g32_gemm without a workspace argument and without any allocation: the K-split partial sums
  * go to a 32 MiB device array inside the library (one per GPU, kept until the process ends), which
  * holds every plan's partials, so the result equals moss_w4g32_gemm's with a full workspace bit for

@@ -35,6 +35,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // Round a float through bf16 and back (the "x.to(bf16).to(f32)" step).
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits(f32_to_bf16(f)); }
 
+// The SiLU*mul epilogue on bf16 gate and up values: bf16(silu(g)) * u, rounded by the caller
+// (src/moss_tts/_runtime/prefill_pointwise.py:18-31).  One definition for every kernel that must
+// agree bit for bit.
+__device__ __forceinline__ float silu_mul_bf16(float g, float u) { return round_bf16(g / (1.0f + expf(-g))) * u; }
+
 // Where group g's zero point sits in a row-packed zp row (blocks of 128 groups: for block c with
 // r = min(128, G - 128c) groups, byte 64c + b holds z[128c + b] low and z[128c + r/2 + b] high):
 // byte index and bit shift.  Branch-free, so a byte load through it is not followed by a wait at

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows(const uint32_t* __restrict_
     for (int p = 0; p < 2; ++p) {
         const float gv = p ? bf16_hi(g) : bf16_lo(g);
         const float uv = p ? bf16_hi(u) : bf16_lo(u);
-        r[p] = round_bf16(gv / (1.0f + expf(-gv))) * uv;
+        r[p] = silu_mul_bf16(gv, uv);
     }
     y[row * half + c] = pack_bf16x2(r[0], r[1]);
 }

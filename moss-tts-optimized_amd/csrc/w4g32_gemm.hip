@@ -496,12 +496,17 @@ __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
 // lgkmcnt 11:8
 #define MOSS_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
 
-template <bool SPLIT>
+// SILU (unsplit only): the weights hold 2 N rows, gate rows then up rows, and Y [M, N] receives
+// bf16(bf16(silu(g)) * u): a workgroup takes gate rows n0 .. n0 + 63 (waves 0, 1) and the up rows
+// of the same outputs (waves 2, 3); the up waves hand their bf16 results to the gate waves through
+// LDS.  Equal bit for bit to the unsplit GEMM of all 2 N rows followed by moss_silu_mul.
+template <bool SPLIT, bool SILU = false>
 __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t* __restrict__ X, const uint4* qw,
                                                               const uint16_t* sc, const uint8_t* zp,
                                                               uint16_t* __restrict__ Y, float* __restrict__ part,
                                                               int M, int N, int K) {
-    constexpr int BN = 128, BM = 128, JT = 4;
+    static_assert(!(SPLIT && SILU), "the SiLU epilogue needs whole sums");
+    constexpr int BN = SILU ? 64 : 128, BM = 128, JT = 4;
     __shared__ __attribute__((aligned(1024))) uint16_t Xa[BM * kBK];
     __shared__ __attribute__((aligned(1024))) uint16_t Xb[BM * kBK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -531,7 +536,9 @@ __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t*
     uint32_t roff[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) roff[kk] = 128u * (uint32_t)(lane & 31) + 16u * (uint32_t)((4 * half + kk) ^ swz);
-    const size_t wrow = (size_t)min(n0 + 32 * wave + (lane & 31), N - 1);
+    // this lane's weight row (SILU: waves 2 and 3 take the up rows, N further on)
+    const int wn = SILU ? n0 + 32 * (wave & 1) + (lane & 31) : n0 + 32 * wave + (lane & 31);
+    const size_t wrow = (size_t)min(wn, N - 1) + (SILU && wave >= 2 ? (size_t)N : 0);
     auto load_w = [&](uint4& w, int k0) { w = qw[wrow * G + ((kbase + k0) >> 5) + half]; };
     auto load_blk = [&](TBlock& t, int blk) {
         const int g = (kbase >> 5) + 8 * blk;
@@ -625,6 +632,54 @@ __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t*
         step(S3{}, S0{}, Yes{}, blk, Xb, Xa);
     }
     MOSS_WAIT_VM(0);  // every copy has landed before the workgroup's LDS is released
+    if constexpr (SILU) {
+        // once every wave's copies have landed (each waited for its own above; the barrier makes
+        // that all of them) no wave reads or writes the activation buffers.  Each wave pair hands
+        // half of its bf16 results to the other through them -- the gate waves token tiles 2, 3,
+        // the up waves tiles 0, 1 -- so that all four waves evaluate the SiLU: wave w & 1 of a
+        // pair owns rows 32 (w & 1) .. + 31, the gate waves finish tiles 0, 1, the up waves 2, 3.
+        // Slot: pairs of consecutive elements of one lane per 32-bit word.
+        __syncthreads();
+        uint32_t* xu = reinterpret_cast<uint32_t*>(Xa);  // [from up | from gate] x 2 x 2 tiles x 8 x 64
+        const bool up = wave >= 2;
+        const int rw = wave & 1;
+        auto slot = [&](int from_up, int jj, int pr) { return (((from_up * 2 + rw) * 2 + jj) * 8 + pr) * 64 + lane; };
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+                const int j = up ? jj : jj + 2;  // the tiles the other pair finishes
+                xu[slot(up, jj, e / 2)] = pack_bf16x2(acc[j][e], acc[j][e + 1]);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int j = up ? jj + 2 : jj;
+            const int m = m0 + 32 * j + (lane & 31);
+            if (m >= M) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 32 * rw + 8 * q + 4 * (lane >> 5);
+                if (n >= N) continue;  // N % 4 == 0: the quad is all in range or all out
+                // the other pair's values for this tile: it stored its tile j - 2 (up) / j (gate)
+                // at index jj
+                const uint32_t o01 = xu[slot(!up, jj, 2 * q)], o23 = xu[slot(!up, jj, 2 * q + 1)];
+                const float m0v = round_bf16(acc[j][4 * q]), m1v = round_bf16(acc[j][4 * q + 1]);
+                const float m2v = round_bf16(acc[j][4 * q + 2]), m3v = round_bf16(acc[j][4 * q + 3]);
+                const float x0 = bf16_lo(o01), x1 = bf16_hi(o01), x2 = bf16_lo(o23), x3 = bf16_hi(o23);
+                uint2 o;
+                if (up) {  // own values are up, the others gate
+                    o.x = pack_bf16x2(silu_mul_bf16(x0, m0v), silu_mul_bf16(x1, m1v));
+                    o.y = pack_bf16x2(silu_mul_bf16(x2, m2v), silu_mul_bf16(x3, m3v));
+                } else {
+                    o.x = pack_bf16x2(silu_mul_bf16(m0v, x0), silu_mul_bf16(m1v, x1));
+                    o.y = pack_bf16x2(silu_mul_bf16(m2v, x2), silu_mul_bf16(m3v, x3));
+                }
+                *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
+            }
+        }
+        return;
+    }
     // C[n][m] of the 32 x 32 tile (n0 + 32 wave, m0 + 32 j): as in w4g32_gemm_t_kernel
 #pragma unroll
     for (int j = 0; j < JT; ++j) {
@@ -1025,6 +1080,17 @@ int fp8_gemm_launch(const void* x, const void* w, const float* row_scale, void* 
     return launch_gemm<kFp8E4M3>(x, w, nullptr, nullptr, y, M, K, N, row_scale, ws, ws_bytes, stream);
 }
 
+// The gate||up GEMM with the SiLU*mul epilogue runs fused where moss_w4g32_gemm would run the
+// 128-token copy tile unsplit on all 2 N rows (so the two agree bit for bit): M > 64, the register
+// tile's shapes, no K split in the plan, and the tile's pointer alignment.
+bool silu_fusable_shape(int M, int K, int N) {
+    if (M <= 64 || N % 4) return false;
+    const Plan p = plan_gemm(M, K, 2 * N, true);
+    return p.reg && p.bm == 128 && p.split == 1;
+}
+
+long long align16(long long b) { return (b + 15) & ~15ll; }
+
 // One workspace serves both formats and the LDS-tile fallback: the largest plan's partial sums.
 long long gemm_workspace_bytes(int M, int K, int N) {
     long long bytes = 0;
@@ -1037,6 +1103,8 @@ long long gemm_workspace_bytes(int M, int K, int N) {
 
 using namespace moss;
 
+extern "C" int moss_silu_mul(const void* x, void* y, int rows, int n, void* stream);
+
 MOSS_API long long moss_gemm_workspace_bytes(int M, int K, int N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 64) return 0;
     return gemm_workspace_bytes(M, K, N);
@@ -1048,6 +1116,34 @@ MOSS_API int moss_w4g32_gemm(const void* x, const void* qw, const void* sc, cons
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && workspace_bytes >= 0);
     return launch_gemm<kInt4G32>(x, qw, sc, zp, y, M, K, N, nullptr, workspace, workspace_bytes,
                                  (hipStream_t)stream);
+}
+
+// The unfused form keeps the [M, 2 N] gate||up product in the workspace, followed by the GEMM's own
+// K-split partials.
+MOSS_API long long moss_gemm_silu_workspace_bytes(int M, int K, int N) {
+    if (M <= 0 || K <= 0 || N <= 0 || K % 64 || N % 4) return 0;
+    if (silu_fusable_shape(M, K, N)) return 0;
+    return align16((long long)M * 2 * N * 2) + gemm_workspace_bytes(M, K, 2 * N);
+}
+
+MOSS_API int moss_w4g32_gemm_silu(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
+                                  int N, void* workspace, long long workspace_bytes, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && y && M > 0 && N > 0 && K > 0 && K % 64 == 0 && N % 4 == 0);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && workspace_bytes >= 0);
+    hipStream_t st = (hipStream_t)stream;
+    if (silu_fusable_shape(M, K, N) && MOSS_ALIGNED(y, 8) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8)) {
+        const dim3 grid((unsigned)(((M + 127) / 128) * ((N + 63) / 64)));
+        hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<false, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                           (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)nullptr,
+                           M, N, K);
+        return moss_launch_status();
+    }
+    const long long inter = align16((long long)M * 2 * N * 2);
+    MOSS_CHECK_ARG(workspace && MOSS_ALIGNED(workspace, 16) && workspace_bytes >= inter);
+    char* ws = (char*)workspace;
+    if (int rc = launch_gemm<kInt4G32>(x, qw, sc, zp, ws, M, K, 2 * N, nullptr, ws + inter, workspace_bytes - inter, st))
+        return rc;
+    return moss_silu_mul(ws, y, M, N, stream);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -300,7 +300,7 @@ class DecodeStepG32:
             attn = attention.prefill_attention(qbuf, self.keys[i], self.values[i], start)
             o = w4g32.gemm(attn, layer.o.packed)
             residual, state = pointwise.add_rmsnorm(o, residual, layer.post_norm, eps)
-            act = pointwise.silu_mul(w4g32.gemm(state, layer.gate_up.packed))
+            act = w4g32.gemm_silu(state, layer.gate_up.packed)
             mlp = w4g32.gemm(act, layer.down.packed)
             if i + 1 < len(self.layers):
                 residual, state = pointwise.add_rmsnorm(mlp, residual, self.layers[i + 1].input_norm, eps)

@@ -37,6 +37,8 @@ SIGNATURES: dict[str, list] = {
     "moss_w4g32_gateup_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "moss_w4g32_gemm": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_gemm_workspace_bytes": [_I, _I, _I],
+    "moss_w4g32_gemm_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
+    "moss_gemm_silu_workspace_bytes": [_I, _I, _I],
     "moss_w4g32_gemm_noalloc": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4g32_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_w4g32_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
@@ -66,7 +68,8 @@ SIGNATURES: dict[str, list] = {
     "moss_advance_step": [_P, _P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong,
                           _P],
 }
-_RESTYPES = {"moss_error_string": ctypes.c_char_p, "moss_gemm_workspace_bytes": ctypes.c_longlong}
+_RESTYPES = {"moss_error_string": ctypes.c_char_p, "moss_gemm_workspace_bytes": ctypes.c_longlong,
+             "moss_gemm_silu_workspace_bytes": ctypes.c_longlong}
 
 
 class NativeLibraryMissing(RuntimeError):
@@ -108,6 +111,15 @@ def gemm_workspace(m: int, k: int, n: int, device) -> tuple:
         return None, 0, None
     ws = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
     return ctypes.c_void_p(ws.data_ptr()), nbytes, ws
+
+
+def workspace(nbytes: int, device) -> tuple:
+    """(pointer, bytes, tensor) of a fresh 16-byte aligned device buffer of ``nbytes``, or
+    (None, 0, None) for none; the caller keeps the tensor alive until the launch has run."""
+    if nbytes == 0:
+        return None, 0, None
+    ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+    return ctypes.c_void_p(ws.data_ptr()), int(nbytes), ws
 
 
 def stream_of(t: torch.Tensor) -> ctypes.c_void_p:

@@ -309,6 +309,23 @@ def gemm(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
     return y
 
 
+def gemm_silu(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
+    """Prefill gate||up with the SiLU*mul epilogue: ``w`` holds gate rows then up rows (2 N rows),
+    bf16 ``[..., M, K]`` -> bf16 ``[..., M, N]``, equal bit for bit to ``silu_mul(gemm(x, w))``
+    (``src/moss_tts/_runtime/llm.py:27-29``, ``prefill_pointwise.py:18-31``)."""
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.shape[-1] == w.K, f"x must end in a dimension of {w.K}")
+    _require(_aligned(x, 16), "x must be 16-byte aligned")
+    _require(w.N % 8 == 0, "gate||up weight needs 2 N rows with N % 4 == 0")
+    m, n = x.numel() // w.K, w.N // 2
+    _require(m > 0, "empty input")
+    y = torch.empty((*x.shape[:-1], n), dtype=torch.bfloat16, device=x.device)
+    wp, wb, _keep = native.workspace(int(native.lib().moss_gemm_silu_workspace_bytes(m, w.K, n)), x.device)
+    native.call("moss_w4g32_gemm_silu", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
+                native.ptr(y), m, w.K, n, wp, wb, native.stream_of(x))
+    return y
+
+
 #: bytes of the library's scratch array behind :func:`gemm_noalloc` (every GEMM plan's partials fit)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 

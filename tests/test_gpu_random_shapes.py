@@ -107,6 +107,8 @@ BF16 = _bf16_cases(8)
 BF16_NORM = [(2048 * _rng.choice((1, 2, 4)), _rng.randint(1, 5000), _rng.random() < 0.5) for _ in range(6)]
 FP8_GATEUP = [(16 * _rng.randint(1, 512), _rng.randint(1, 3000), _rng.choice((0, 1, 2, 4))) for _ in range(8)]
 W4A8_NORM = _w4a8_norm_cases(8)
+GEMM_SILU = [(_rng.choice((_rng.randint(2, 64), _rng.randint(65, 700))), 64 * _rng.choice((16, 64, 128, 192)),
+              4 * _rng.randint(1, 3500)) for _ in range(8)]
 
 
 def _rel(a, b):
@@ -316,3 +318,15 @@ def test_w4a8_fused_norm_random_shape(dev, k, n, paired, residual, rows):
         got_sum, got = got
         assert torch.equal(got_sum, summed)
     assert torch.equal(got.view(-1), want.view(-1))
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_SILU)
+def test_gemm_silu_random_shape(dev, m, k, n):
+    """The gate||up GEMM with the SiLU*mul epilogue (fused or through the workspace) equals the GEMM
+    followed by silu_mul bit for bit."""
+    from moss_tts._runtime import native, pointwise, w4g32
+
+    print(f"gemm_silu M={m} K={k} N={n} fused={native.lib().moss_gemm_silu_workspace_bytes(m, k, n) == 0}", flush=True)
+    pw, g = _packed(2 * n, k, 17 * m + k + n, dev)
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    assert torch.equal(w4g32.gemm_silu(x, pw), pointwise.silu_mul(w4g32.gemm(x, pw)))

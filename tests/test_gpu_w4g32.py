@@ -289,6 +289,26 @@ def test_gemm_parity(dev, m, k, n):
     _assert_rne_or_adjacent(y, ref, abs_sum, k, f"gemm M={m} K={k} N={n}")
 
 
+@pytest.mark.parametrize("m,k,n,fused", [(512, 4096, 12288, True), (65, 4096, 12288, True), (200, 4096, 12260, True),
+                                         (64, 4096, 12288, False), (16, 4096, 12288, False), (700, 4096, 256, False),
+                                         (128, 1024, 100, False), (3, 4096, 512, False)])
+def test_gemm_silu_equals_gemm_then_silu(dev, m, k, n, fused):
+    """The gate||up GEMM with the SiLU*mul epilogue equals the GEMM of all 2 N rows followed by
+    silu_mul, bit for bit: fused in the 128-token tile (M > 64 with no K split in the plan) and
+    through the workspace otherwise (64 tokens or fewer, or few enough tiles that K is split)."""
+    from moss_tts._runtime import native, pointwise, w4g32
+
+    print(f"gemm_silu M={m} K={k} N={n} fused={fused}", flush=True)
+    assert (native.lib().moss_gemm_silu_workspace_bytes(m, k, n) == 0) == fused
+    g = torch.Generator(device=dev).manual_seed(m + k + n)
+    pw = w4g32.quantize_minmax(torch.randn((2 * n, k), device=dev, generator=g) * 0.02)
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    want = pointwise.silu_mul(w4g32.gemm(x, pw))
+    got = w4g32.gemm_silu(x, pw)
+    assert got.shape == (m, n)
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("m,k,n", [(512, 4096, 4096), (48, 4096, 2056)])
 def test_gemm_fallbacks_match(dev, m, k, n):
     """The C-ABI's fallbacks give the same products: without a workspace the planned K split is
