@@ -193,13 +193,22 @@ __device__ __forceinline__ void dequant_word_exact(uint32_t d0, uint32_t d1, uin
 // (src/moss_tts/_runtime/kernels.py:142-170): xn = bf16(bf16(x * r) * w); out_l =
 // bf16(bf16(xn_l * cos_l) + bf16(-xn_{l+64} * sin_l)), out_{l+64} = bf16(bf16(xn_{l+64} *
 // cos_{l+64}) + bf16(xn_l * sin_{l+64})), the negation being float negation.
-__device__ __forceinline__ void head_norm_rope(float a, float b, float w0, float w1, float c0, float c1, float s0,
-                                               float s1, float eps, uint16_t& o0, uint16_t& o1) {
-    const float r = rsqrtf(wave_sum(a * a + b * b) / 128.0f + eps);
+// The squares of a dim pair, contracted one way everywhere (kernels that must agree use this).
+__device__ __forceinline__ float head_sq(float a, float b) { return __builtin_fmaf(a, a, b * b); }
+
+// The per-dim part once the head's reciprocal RMS r is known.
+__device__ __forceinline__ void head_rope_apply(float a, float b, float r, float w0, float w1, float c0, float c1,
+                                                float s0, float s1, uint16_t& o0, uint16_t& o1) {
     const float an = round_bf16(round_bf16(a * r) * w0);
     const float bn = round_bf16(round_bf16(b * r) * w1);
     o0 = f32_to_bf16(round_bf16(an * c0) + round_bf16((-bn) * s0));
     o1 = f32_to_bf16(round_bf16(bn * c1) + round_bf16(an * s1));
+}
+
+__device__ __forceinline__ void head_norm_rope(float a, float b, float w0, float w1, float c0, float c1, float s0,
+                                               float s1, float eps, uint16_t& o0, uint16_t& o1) {
+    const float r = rsqrtf(wave_sum(head_sq(a, b)) / 128.0f + eps);
+    head_rope_apply(a, b, r, w0, w1, c0, c1, s0, s1, o0, o1);
 }
 
 }  // namespace moss
