@@ -341,6 +341,30 @@ def prefill_bench(torch, dev):
     return out
 
 
+def prefill_pass_bench(torch, n_layers: int, dev, replays: int = 10):
+    """The 512-token prompt pass alone: the bucket graph run once by ``prefill`` and then replayed
+    ``replays`` times (11 executions in all, for a kernel trace)."""
+    from moss_tts._runtime.decode import DecodeStepG32
+
+    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
+    n = 512
+    eng.capture_prefill((n,))
+    g = torch.Generator().manual_seed(5)
+    ids = torch.cat([torch.randint(0, 151643, (n, 1), generator=g), torch.randint(0, 1024, (n, 32), generator=g)], 1)
+    eng.prefill(ids)
+    graph = eng.prefill_graphs[n][0]
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / replays
+    _log(f"[bench] prefill of {n} tokens through {n_layers} layers: {ms:.3f} ms per replay ({replays} replays)")
+    return ms
+
+
 def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False):
     """The full batch-1 decode step (embedding -> n_layers -> 32 INT4 heads, KV cache of 2048
     rows filled with N(0,1), current position 2047) captured as one graph; ms per step.
@@ -440,6 +464,8 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="skip the FP8 and prefill GEMM lines")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the 36-layer decode step (both arithmetics) and its lines, for a kernel trace")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 36-layer 512-token prompt pass (10 graph replays), for a kernel trace")
     ap.add_argument("--pmc-pass", choices=("gemv", "gemm"), default=None,
                     help="eager launches only, for rocprofv3 --pmc: 'gemv' = a 512 MiB copy of known size, "
                          "then one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy; "
@@ -462,6 +488,10 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     arch = native.device_arch(0)
+    if args.prefill_only:
+        _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); 512-token prompt pass only")
+        prefill_pass_bench(torch, args.decode_layers, dev)
+        return 0
     if args.decode_only:
         _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode step only")
         for w8 in (False, True):
