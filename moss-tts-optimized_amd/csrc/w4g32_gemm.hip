@@ -473,15 +473,16 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
 
 // The 128-token register-weight tile (M > 64) with the activations copied from global memory
 // straight into LDS (global_load_lds_dwordx4: lane i of an instruction writes bytes 16 i .. + 15
-// of a 1 KiB span), so no registers stage them and no LDS stores are issued: 150 VGPRs, three
+// of a 1 KiB span), so no registers stage them and no LDS stores are issued: 150-152 VGPRs, three
 // workgroups per CU (768 gate||up tiles at M = 512 run in one round instead of 1.5).  Weights,
 // operands, MFMA order and results are those of w4g32_gemm_t_kernel<4, SPLIT>, bit for bit.
 // LDS layout: two buffers of 128 token rows x 128 bytes (one K step), chunk c (8 bf16) of row r
 // stored at position c ^ (r & 7) ^ ((r >> 3) & 1): the 16 lanes that read one chunk of 16
 // consecutive rows in one LDS cycle (64 banks) hit 16 different 16-byte bank groups (r & 7 alone
 // pairs rows r and r + 8 on the same banks: 4 conflict cycles per read, by counters); the eight
-// lanes per row of a copy instruction still read that row's 128 contiguous bytes.  The buffers are distinct variables, which lets the compiler see
-// that reading one does not wait for the copy into the other.
+// lanes per row of a copy instruction still read that row's 128 contiguous bytes.  The buffers
+// are distinct variables, which lets the compiler see that reading one does not wait for the copy
+// into the other.
 // Step s: copy step s + 1 into the other buffer, multiply step s, load the codes of step s + kTs
 // (and the next block's scales and zeros after a block's last step), then wait until this wave's
 // copy has landed -- at most the loads issued after it still outstanding (vector memory requests
@@ -498,8 +499,9 @@ __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
 
 // SILU (unsplit only): the weights hold 2 N rows, gate rows then up rows, and Y [M, N] receives
 // bf16(bf16(silu(g)) * u): a workgroup takes gate rows n0 .. n0 + 63 (waves 0, 1) and the up rows
-// of the same outputs (waves 2, 3); the up waves hand their bf16 results to the gate waves through
-// LDS.  Equal bit for bit to the unsplit GEMM of all 2 N rows followed by moss_silu_mul.
+// of the same outputs (waves 2, 3); each wave pair hands half of its bf16 results to the other
+// through LDS, so all four waves evaluate the SiLU.  Equal bit for bit to the unsplit GEMM of all
+// 2 N rows followed by moss_silu_mul.
 template <bool SPLIT, bool SILU = false>
 __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t* __restrict__ X, const uint4* qw,
                                                               const uint16_t* sc, const uint8_t* zp,
