@@ -205,6 +205,18 @@ int moss_w4g32_gemm_silu(const void *x, const void *qw, const void *sc, const vo
  * the epilogue runs inside the GEMM. */
 long long moss_gemm_silu_workspace_bytes(int M, int K, int N);
 
+/* Prefill O / down projection followed by the residual add and RMSNorm: with p = the bf16 product
+ * of moss_w4g32_gemm, summed_out = bf16(p + residual) and y = bf16(bf16(summed * rsqrt(mean(summed^2)
+ * + eps)) * norm_w), both [M, N] (N % 8 == 0, N <= 8192; x, residual, norm_w, summed_out, y 16-byte
+ * aligned) -- equal bit for bit to moss_w4g32_gemm followed by moss_rmsnorm with the residual.  The
+ * workspace is moss_w4g32_gemm's (moss_gemm_workspace_bytes); when the plan splits K, the norm
+ * kernel reduces the partial sums itself (one launch and one [M, N] round trip fewer).  Replaces
+ * o_proj / down_proj and the following add_rmsnorm of the prefill layer loop
+ * (src/moss_tts/_runtime/llm.py:84, prefill_pointwise.py:46-57). */
+int moss_w4g32_gemm_add_rmsnorm(const void *x, const void *qw, const void *sc, const void *zp, const void *residual,
+                                const void *norm_w, float eps, void *summed_out, void *y, int M, int K, int N,
+                                void *workspace, long long workspace_bytes, void *stream);
+
 /* moss_w4g32_gemm without a workspace argument and without any allocation: the K-split partial sums
  * go to a 32 MiB device array inside the library (one per GPU, kept until the process ends), which
  * holds every plan's partials, so the result equals moss_w4g32_gemm's with a full workspace bit for

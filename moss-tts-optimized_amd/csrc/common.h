@@ -223,6 +223,12 @@ __device__ __forceinline__ void head_norm_rope(float a, float b, float w0, float
 
 static inline int moss_launch_status() { return (int)hipGetLastError(); }
 
+namespace moss {
+// norm_rope.hip: the split-K reduction fused with the residual add + RMSNorm after a GEMM.
+int addnorm_from_parts(const float* parts, int S, const void* res, const void* w, void* sum_out, void* y, int rows,
+                       int n, float eps, hipStream_t st);
+}  // namespace moss
+
 // The fused-norm projections: res == NULL normalizes x; otherwise s = bf16(x + res) is normalized
 // and stored to sum_out by one workgroup while the others still read x and res, so sum_out must not
 // overlap either of them (an in-place residual update would race).  K % 2048 == 0, K <= 8192.

@@ -33,7 +33,10 @@ constexpr int kMaxChunks = 4;
 // scales and code sums, as the reference's fused norm + quantizer does
 // (src/moss_tts/_runtime/dp4a_fusions.py:24-40); y may then be null.  A group's 4 chunks
 // belong to the 4 lanes of one DPP quad.
-template <bool RESIDUAL, bool QUANT = false>
+// PARTS: x is not read; each value is formed from S fp32 partial sums of a split-K GEMM,
+// parts[z][row][col] added in z order from 0 and rounded to bf16 -- exactly what gemm_reduce
+// (w4g32_gemm.hip) writes -- so reduce-then-norm takes one launch and no bf16 round trip.
+template <bool RESIDUAL, bool QUANT = false, bool PARTS = false>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ res,
                                                              const uint16_t* __restrict__ w,
@@ -41,7 +44,8 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
                                                              uint16_t* __restrict__ y, int n, float eps,
                                                              uint2* __restrict__ qx = nullptr,
                                                              float* __restrict__ sx = nullptr,
-                                                             int* __restrict__ qsum = nullptr) {
+                                                             int* __restrict__ qsum = nullptr,
+                                                             const float* __restrict__ parts = nullptr, int S = 0) {
     __shared__ float lds[kNormThreads / kWave];
     const size_t row = blockIdx.x;
     const int chunks = n / 8;
@@ -61,7 +65,24 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
     for (int c = 0; c < kMaxChunks; ++c) {
         const int ci = threadIdx.x + c * kNormThreads;
         if (ci < chunks) {
-            const uint4 a = xr[ci];
+            uint4 a;
+            if constexpr (PARTS) {
+                const size_t mn = (size_t)gridDim.x * n;
+                const float* pr = parts + row * n + 8 * ci;
+                float acc[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+                for (int z = 0; z < S; ++z) {
+                    const float4 p0 = reinterpret_cast<const float4*>(pr + z * mn)[0];
+                    const float4 p1 = reinterpret_cast<const float4*>(pr + z * mn)[1];
+                    acc[0] += p0.x, acc[1] += p0.y, acc[2] += p0.z, acc[3] += p0.w;
+                    acc[4] += p1.x, acc[5] += p1.y, acc[6] += p1.z, acc[7] += p1.w;
+                }
+                a = make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
+                               pack_bf16x2(acc[6], acc[7]));
+            } else {
+                a = xr[ci];
+            }
             const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
             uint32_t sw[4];
             if constexpr (RESIDUAL) {
@@ -258,6 +279,17 @@ __global__ __launch_bounds__(256) void silu_mul_rows(const uint32_t* __restrict_
 }
 
 }  // namespace
+
+// The split-K reduction of a GEMM's fp32 partials fused with the residual add and RMSNorm that
+// follow it (rows x n outputs, S partials each; n % 8 == 0, 16-byte aligned buffers).
+int addnorm_from_parts(const float* parts, int S, const void* res, const void* w, void* sum_out, void* y, int rows,
+                       int n, float eps, hipStream_t st) {
+    hipLaunchKernelGGL((rmsnorm_rows<true, false, true>), dim3(rows), dim3(kNormThreads), 0, st,
+                       (const uint16_t*)nullptr, (const uint16_t*)res, (const uint16_t*)w, (uint16_t*)sum_out,
+                       (uint16_t*)y, n, eps, (uint2*)nullptr, (float*)nullptr, (int*)nullptr, parts, S);
+    return moss_launch_status();
+}
+
 }  // namespace moss
 
 using namespace moss;

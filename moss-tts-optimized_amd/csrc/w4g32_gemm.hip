@@ -1043,9 +1043,12 @@ void launch_reg(const Plan& p, const void* x, const void* qw, const void* sc, co
                            (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
 }
 
+// split_out: when non-null, a K-split plan leaves its fp32 partials in ws for the caller to reduce
+// (no gemm_reduce launch) and *split_out receives the split (1: y holds the product).
 template <int FMT>
 int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K, int N,
-                const float* row_scale, void* ws, long long ws_bytes, hipStream_t st) {
+                const float* row_scale, void* ws, long long ws_bytes, hipStream_t st, int* split_out = nullptr) {
+    if (split_out) *split_out = 1;
     if (stream_shape(FMT, M, K, N, x, qw, sc, zp, y)) {
         launch_stream<FMT>(x, qw, sc, zp, row_scale, y, M, K, N, st);
         return moss_launch_status();
@@ -1066,7 +1069,9 @@ int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, v
     else if (p.bm == 64) launch_tile<64, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else if (p.bn == 64) launch_tile<128, 64, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
     else launch_tile<128, 128, FMT>(p, x, qw, sc, zp, y, ws, M, K, N, row_scale, st);
-    if (p.split > 1) {
+    if (p.split > 1 && split_out) {
+        *split_out = p.split;
+    } else if (p.split > 1) {
         const int mn = M * N;
         hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, st, (const float*)ws,
                            FMT == kFp8E4M3 ? row_scale : nullptr, (uint16_t*)y, mn, N, p.split);
@@ -1146,6 +1151,31 @@ MOSS_API int moss_w4g32_gemm_silu(const void* x, const void* qw, const void* sc,
     if (int rc = launch_gemm<kInt4G32>(x, qw, sc, zp, ws, M, K, 2 * N, nullptr, ws + inter, workspace_bytes - inter, st))
         return rc;
     return moss_silu_mul(ws, y, M, N, stream);
+}
+
+extern "C" int moss_rmsnorm(const void* x, const void* res, const void* w, void* sum_out, void* y, int rows, int n,
+                            float eps, void* stream);
+
+// The O / down projection followed by the residual add and RMSNorm of the prompt pass.  A K-split
+// plan's partials go straight into the norm kernel, which reduces them in split order; otherwise
+// the product goes to summed_out and the norm runs in place there (each thread reads a chunk
+// before it writes the same chunk).
+MOSS_API int moss_w4g32_gemm_add_rmsnorm(const void* x, const void* qw, const void* sc, const void* zp,
+                                         const void* residual, const void* norm_w, float eps, void* summed_out,
+                                         void* y, int M, int K, int N, void* workspace, long long workspace_bytes,
+                                         void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && residual && norm_w && summed_out && y && M > 0 && N > 0 && K > 0 &&
+                   K % 64 == 0 && N % 8 == 0 && N <= 8192 && eps >= 0.f);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && MOSS_ALIGNED(residual, 16) &&
+                   MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(summed_out, 16) && MOSS_ALIGNED(y, 16) &&
+                   workspace_bytes >= 0);
+    hipStream_t st = (hipStream_t)stream;
+    int split = 1;
+    if (int rc = launch_gemm<kInt4G32>(x, qw, sc, zp, summed_out, M, K, N, nullptr, workspace, workspace_bytes, st,
+                                       &split))
+        return rc;
+    if (split > 1) return addnorm_from_parts((const float*)workspace, split, residual, norm_w, summed_out, y, M, N, eps, st);
+    return moss_rmsnorm(summed_out, residual, norm_w, summed_out, y, M, N, eps, stream);
 }
 
 // ---------------------------------------------------------------------------------------------

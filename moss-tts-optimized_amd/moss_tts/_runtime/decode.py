@@ -298,12 +298,13 @@ class DecodeStepG32:
             pointwise.qk_rope(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i], self.values[i],
                               positions, eps, cos_by_position=True, out=qbuf)
             attn = attention.prefill_attention(qbuf, self.keys[i], self.values[i], start)
-            o = w4g32.gemm(attn, layer.o.packed)
-            residual, state = pointwise.add_rmsnorm(o, residual, layer.post_norm, eps)
+            residual, state = w4g32.gemm_add_rmsnorm(attn, layer.o.packed, residual, layer.post_norm, eps)
             act = w4g32.gemm_silu(state, layer.gate_up.packed)
-            mlp = w4g32.gemm(act, layer.down.packed)
             if i + 1 < len(self.layers):
-                residual, state = pointwise.add_rmsnorm(mlp, residual, self.layers[i + 1].input_norm, eps)
+                residual, state = w4g32.gemm_add_rmsnorm(act, layer.down.packed, residual,
+                                                         self.layers[i + 1].input_norm, eps)
+            else:
+                mlp = w4g32.gemm(act, layer.down.packed)  # the last layer's add-norm runs with the heads
         return self._heads(mlp.index_select(0, last), residual.index_select(0, last), CODEBOOKS)
 
     def _prefill_inputs(self, ids: torch.Tensor, start: int, rows: int):

@@ -39,6 +39,7 @@ SIGNATURES: dict[str, list] = {
     "moss_gemm_workspace_bytes": [_I, _I, _I],
     "moss_w4g32_gemm_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_gemm_silu_workspace_bytes": [_I, _I, _I],
+    "moss_w4g32_gemm_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_w4g32_gemm_noalloc": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4g32_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "moss_w4g32_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],

@@ -326,6 +326,32 @@ def gemm_silu(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
     return y
 
 
+def gemm_add_rmsnorm(x: torch.Tensor, w: PackedW4G32, residual: torch.Tensor, norm_weight: torch.Tensor,
+                     eps: float) -> tuple:
+    """Prefill projection followed by the residual add and RMSNorm: ``(summed, y)`` with
+    ``summed = bf16(gemm(x, w) + residual)`` and ``y = rmsnorm(summed)``, equal bit for bit to
+    ``pointwise.add_rmsnorm(gemm(x, w), residual, norm_weight, eps)``; a K-split GEMM's partial sums
+    are reduced inside the norm kernel (``src/moss_tts/_runtime/prefill_pointwise.py:46-57``)."""
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.shape[-1] == w.K, f"x must end in a dimension of {w.K}")
+    m = x.numel() // w.K
+    _require(m > 0, "empty input")
+    _require(w.N % 8 == 0 and w.N <= 8192, "the norm needs N % 8 == 0 and N <= 8192")
+    _cuda_contig("residual", residual, torch.bfloat16, w.device)
+    _require(residual.numel() == m * w.N, f"residual must hold {m} x {w.N} values")
+    _cuda_contig("norm_weight", norm_weight, torch.bfloat16, w.device)
+    _require(norm_weight.numel() == w.N, f"norm_weight must hold {w.N} values")
+    for name, t in (("x", x), ("residual", residual), ("norm_weight", norm_weight)):
+        _require(_aligned(t, 16), f"{name} must be 16-byte aligned")
+    summed = torch.empty((*x.shape[:-1], w.N), dtype=torch.bfloat16, device=x.device)
+    y = torch.empty_like(summed)
+    wp, wb, _keep = native.gemm_workspace(m, w.K, w.N, x.device)
+    native.call("moss_w4g32_gemm_add_rmsnorm", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales),
+                native.ptr(w.zeros), native.ptr(residual), native.ptr(norm_weight), float(eps), native.ptr(summed),
+                native.ptr(y), m, w.K, w.N, wp, wb, native.stream_of(x))
+    return summed, y
+
+
 #: bytes of the library's scratch array behind :func:`gemm_noalloc` (every GEMM plan's partials fit)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 

@@ -309,6 +309,26 @@ def test_gemm_silu_equals_gemm_then_silu(dev, m, k, n, fused):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("m,k,n", [(512, 4096, 4096), (512, 12288, 4096), (1024, 4096, 4096), (64, 4096, 4096),
+                                   (16, 4096, 4096), (200, 1024, 512), (3, 4096, 4096)])
+def test_gemm_add_rmsnorm_equals_gemm_then_add_rmsnorm(dev, m, k, n):
+    """The projection followed by the residual add and RMSNorm equals gemm then add_rmsnorm bit for
+    bit, with the split-K reduction inside the norm kernel (M=512 O and down, and the other split
+    plans) and without (M=1024, the streaming kernel)."""
+    from moss_tts._runtime import native, pointwise, w4g32
+
+    split = native.lib().moss_gemm_workspace_bytes(m, k, n) // (m * n * 4)
+    print(f"gemm_add_rmsnorm M={m} K={k} N={n} split={split}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(3 * m + k + n)
+    pw = w4g32.quantize_minmax(torch.randn((n, k), device=dev, generator=g) * 0.02)
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    res = torch.randn((m, n), device=dev, generator=g).bfloat16()
+    nw = (1 + 0.05 * torch.randn(n, device=dev, generator=g)).bfloat16()
+    want_s, want_y = pointwise.add_rmsnorm(w4g32.gemm(x, pw), res, nw, 1e-6)
+    got_s, got_y = w4g32.gemm_add_rmsnorm(x, pw, res, nw, 1e-6)
+    assert torch.equal(got_s, want_s) and torch.equal(got_y, want_y)
+
+
 @pytest.mark.parametrize("m,k,n", [(512, 4096, 4096), (48, 4096, 2056)])
 def test_gemm_fallbacks_match(dev, m, k, n):
     """The C-ABI's fallbacks give the same products: without a workspace the planned K split is
