@@ -126,6 +126,18 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_sample_topk_pair(*bad_k, p, p, null) == 1                                     # top_k <= vocab
     assert lib.moss_sample_topk_pair(*pair_ok, null, p, null) == 1                                # seed buffer
     assert lib.moss_compose_next_ids(p, p, p, p, p, 0, 0, 0, 1024, p, null) == 1                  # channels
+    # the prefill fusions (every call below is refused before any launch)
+    assert lib.moss_w4g32_gemm_silu(p, p, p, p, p, 512, 4096, 12290, null, 0, null) == 1          # N % 4
+    assert lib.moss_w4g32_gemm_silu(odd, p, p, p, p, 512, 4096, 12288, null, 0, null) == 1        # alignment
+    assert lib.moss_w4g32_gemm_silu(p, p, p, p, p, 16, 4096, 12288, null, 0, null) == 1           # unfused: workspace
+    assert lib.moss_gemm_silu_workspace_bytes(512, 4096, 12288) == 0                               # fused in the GEMM
+    assert lib.moss_gemm_silu_workspace_bytes(16, 4096, 12288) >= 16 * 2 * 12288 * 2               # [M, 2N] product
+    assert lib.moss_w4g32_gemm_add_rmsnorm(p, p, p, p, p, p, f(1e-6), p, p, 512, 4096, 4100, null, 0,
+                                           null) == 1                                              # N % 8
+    assert lib.moss_w4g32_gemm_add_rmsnorm(p, p, p, p, p, p, f(1e-6), p, p, 512, 4096, 8200, null, 0,
+                                           null) == 1                                              # N <= 8192
+    assert lib.moss_w4g32_gemm_add_rmsnorm(p, p, p, p, odd, p, f(1e-6), p, p, 512, 4096, 4096, null, 0,
+                                           null) == 1                                              # residual alignment
     q = ctypes.c_void_p(8192)
     assert lib.moss_w4a8_norm_gemv(p, null, p, null, f(1e-6), p, p, p, p, 12288, 64, 0, null) == 1   # K
     assert lib.moss_w4a8_norm_gemv(p, p, p, null, f(1e-6), p, p, p, p, 4096, 64, 0, null) == 1       # sum_out
