@@ -107,6 +107,8 @@ BF16 = _bf16_cases(8)
 BF16_NORM = [(2048 * _rng.choice((1, 2, 4)), _rng.randint(1, 5000), _rng.random() < 0.5) for _ in range(6)]
 FP8_GATEUP = [(16 * _rng.randint(1, 512), _rng.randint(1, 3000), _rng.choice((0, 1, 2, 4))) for _ in range(8)]
 W4A8_NORM = _w4a8_norm_cases(8)
+GEMM_ADDNORM = [(_rng.choice((_rng.randint(2, 64), _rng.randint(65, 1100))), 64 * _rng.choice((16, 64, 192)),
+                 8 * _rng.randint(1, 1024)) for _ in range(8)]
 GEMM_SILU = [(_rng.choice((_rng.randint(2, 64), _rng.randint(65, 700))), 64 * _rng.choice((16, 64, 128, 192)),
               4 * _rng.randint(1, 3500)) for _ in range(8)]
 
@@ -330,3 +332,20 @@ def test_gemm_silu_random_shape(dev, m, k, n):
     pw, g = _packed(2 * n, k, 17 * m + k + n, dev)
     x = torch.randn((m, k), device=dev, generator=g).bfloat16()
     assert torch.equal(w4g32.gemm_silu(x, pw), pointwise.silu_mul(w4g32.gemm(x, pw)))
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_ADDNORM)
+def test_gemm_add_rmsnorm_random_shape(dev, m, k, n):
+    """The projection followed by the residual add and RMSNorm (the split-K reduction inside the
+    norm when the plan splits K) equals gemm then add_rmsnorm bit for bit."""
+    from moss_tts._runtime import native, pointwise, w4g32
+
+    split = native.lib().moss_gemm_workspace_bytes(m, k, n) // (m * n * 4)
+    print(f"gemm_add_rmsnorm M={m} K={k} N={n} split={split}", flush=True)
+    pw, g = _packed(n, k, 19 * m + k + n, dev)
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    res = torch.randn((m, n), device=dev, generator=g).bfloat16()
+    nw = (1 + 0.05 * torch.randn(n, device=dev, generator=g)).bfloat16()
+    want = pointwise.add_rmsnorm(w4g32.gemm(x, pw), res, nw, 1e-6)
+    got = w4g32.gemm_add_rmsnorm(x, pw, res, nw, 1e-6)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
