@@ -1,8 +1,9 @@
 """GPU: the prompt pass (prefill) against the oracle.
 
 * ``moss_prefill_attention`` (MFMA causal GQA attention) against the oracle's fp32 causal attention,
-  |y - ref| <= 1e-2 + 1e-2 |ref| per output, for prompts of 1..512 tokens starting at row 0 or
-  after a cache prefix; every output row covered.
+  |y - ref| <= 1e-2 + 1e-2 |ref| per output, for prompts of 1..700 tokens starting at row 0 or
+  after a cache prefix (both workgroup shapes); every output row covered; NaN in cache rows after
+  the prompt never reaches the output.
 * The composed prompt pass (``DecodeStepG32.prefill``: embedding sum, 2 full-width layers of INT4
   GEMMs, q/k-norm + RoPE + KV write, causal attention, norms, SiLU*mul, then the final norm and the
   heads on the last token) against ``oracle.decode.prefill`` on the same dequantized weights: the
@@ -24,7 +25,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("n,start,L", [(1, 0, 64), (5, 0, 64), (32, 0, 128), (33, 7, 128), (100, 0, 256),
-                                       (128, 300, 1024), (512, 0, 2048), (200, 1777, 2048), (64, 0, 64)])
+                                       (128, 300, 1024), (512, 0, 2048), (200, 1777, 2048), (64, 0, 64),
+                                       (513, 0, 576), (700, 60, 1024)])
 def test_prefill_attention_parity(dev, n, start, L):
     from moss_tts._runtime import attention
 
@@ -36,6 +38,27 @@ def test_prefill_attention_parity(dev, n, start, L):
     st = torch.tensor([start], dtype=torch.int64, device=dev)
     out = attention.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), st)
     torch.cuda.synchronize()
+    ref = oa.prefill_attention(q, kc, vc, start).reshape(n, 4096)
+    _assert_close(out, ref, f"prefill attention n={n} start={start}")
+
+
+@pytest.mark.parametrize("n,start,L", [(37, 5, 2048), (1, 0, 128), (100, 1900, 2048), (600, 0, 1024)])
+def test_prefill_attention_ignores_rows_after_the_prompt(dev, n, start, L):
+    """Cache rows after the last prompt token may never have been written: NaN there must not reach
+    the output, although those rows share a key block with the prompt's last keys."""
+    from moss_tts._runtime import attention
+
+    print(f"prefill attention, NaN rows after the prompt: n={n} start={start} L={L}", flush=True)
+    g = torch.Generator().manual_seed(n + start + L)
+    q = torch.randn((n, 32, 128), generator=g).bfloat16()
+    kc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
+    vc = torch.randn((1, 8, L, 128), generator=g).bfloat16()
+    kc[:, :, start + n:] = float("nan")
+    vc[:, :, start + n:] = float("nan")
+    st = torch.tensor([start], dtype=torch.int64, device=dev)
+    out = attention.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), st)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
     ref = oa.prefill_attention(q, kc, vc, start).reshape(n, 4096)
     _assert_close(out, ref, f"prefill attention n={n} start={start}")
 
