@@ -200,3 +200,21 @@ def test_embedding_sum(dev):
     out = attention.embedding_sum(ids.to(dev), text.to(dev), audio.to(dev))
     ref = oa.embedding_sum(ids[0], text, audio)
     assert torch.equal(out.cpu()[0].view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("T,H,Q", [(37, 4096, 32), (5, 4098, 32), (3, 1000, 40), (2, 8, 2), (4, 12, 1), (3, 1004, 33)])
+def test_embedding_sum_rows(dev, T, H, Q):
+    """Several tokens at once, bit-exact: 16-, 8- and 2-byte loads (H % 8, H % 4, other H), Q beyond
+    one batch of 32 codebooks, a single codebook."""
+    from moss_tts._runtime import attention
+    from oracle import attention as oa
+
+    print(f"embedding sum T={T} H={H} Q={Q}", flush=True)
+    g = torch.Generator().manual_seed(T + H + Q)
+    text = torch.randn((50, H), generator=g).bfloat16()
+    audio = torch.randn((Q, 70, H), generator=g).bfloat16()
+    ids = torch.cat([torch.randint(0, 50, (T, 1), generator=g), torch.randint(0, 70, (T, Q), generator=g)], 1)
+    out = attention.embedding_sum(ids.to(dev), text.to(dev), audio.to(dev)).cpu()
+    for t in range(T):
+        ref = oa.embedding_sum(ids[t], text, audio)
+        assert torch.equal(out[t].view(torch.int16), ref.view(torch.int16)), t
