@@ -205,6 +205,26 @@ int moss_w4g32_gemm_silu(const void *x, const void *qw, const void *sc, const vo
  * the epilogue runs inside the GEMM. */
 long long moss_gemm_silu_workspace_bytes(int M, int K, int N);
 
+/* Prefill QKV projection (N = 6144: 32 query, 8 key, 8 value heads of 128) with the q/k head
+ * RMSNorm + RoPE and the K/V cache write as its epilogue: equal bit for bit to moss_w4g32_gemm
+ * (full workspace) followed by moss_qk_norm_rope_kv(..., cos_by_position = 1).  q_out bf16
+ * [M, 32, 128]; K/V rows positions[t] (int64 [M], clamped into 0 .. L - 1) of the [8, L, 128]
+ * caches; cos/sin [L, 128]; q_weight/k_weight [128].  For M > 64 where the GEMM plan has no K split
+ * (Qwen3-8B at M > 256) the norm, RoPE and cache writes run inside the GEMM and no [M, 6144]
+ * product is written; otherwise the product and the GEMM's partial sums go to a caller-owned
+ * workspace of moss_gemm_qk_rope_workspace_bytes(M, K) bytes (16-byte aligned; also for sc/zp
+ * not 16/8-byte aligned).  x, qw 16-byte aligned; the bf16 vectors, caches, q_out and positions
+ * 8-byte aligned.  Replaces qkv_proj and the prefill q/k-norm + RoPE + cache write
+ * (src/moss_tts/_runtime/llm.py:84, :95-98, prefill_qkv.py:31-53). */
+int moss_w4g32_gemm_qk_rope(const void *x, const void *qw, const void *sc, const void *zp, const void *q_weight,
+                            const void *k_weight, const void *cos, const void *sin, void *q_out, void *k_cache,
+                            void *v_cache, const void *positions, int M, int K, int L, float eps, void *workspace,
+                            long long workspace_bytes, void *stream);
+
+/* Workspace bytes moss_w4g32_gemm_qk_rope needs for M tokens of K inputs; 0 when the epilogue runs
+ * inside the GEMM. */
+long long moss_gemm_qk_rope_workspace_bytes(int M, int K);
+
 /* Prefill O / down projection followed by the residual add and RMSNorm: with p = the bf16 product
  * of moss_w4g32_gemm, summed_out = bf16(p + residual) and y = bf16(bf16(summed * rsqrt(mean(summed^2)
  * + eps)) * norm_w), both [M, N] (N % 8 == 0, N <= 8192; x, residual, norm_w, summed_out, y 16-byte

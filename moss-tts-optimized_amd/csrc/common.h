@@ -211,6 +211,40 @@ __device__ __forceinline__ void head_norm_rope(float a, float b, float w0, float
     head_rope_apply(a, b, r, w0, w1, c0, c1, s0, s1, o0, o1);
 }
 
+// The same for one head held by 16 lanes (lane j of the group: dims 4 j .. + 3 in a, their RoPE
+// partners 64 + 4 j .. + 3 in b, as 8-byte bf16 quads; weights, cos and sin likewise).  The sum of
+// squares follows wave_sum's tree exactly -- pairs and quads inside the lane, then lanes 1 (DPP
+// row half mirror), 3 (row mirror), 4 and 8 apart -- so the outputs equal head_norm_rope's bit
+// for bit.  All 16 lanes of the group must be active.
+__device__ __forceinline__ float xor16(float v, int m) { return __shfl_xor(v, m, 16); }
+__device__ __forceinline__ float bf16_quad(uint2 v, int i) {
+    return i == 0 ? bf16_lo(v.x) : i == 1 ? bf16_hi(v.x) : i == 2 ? bf16_lo(v.y) : bf16_hi(v.y);
+}
+
+__device__ __forceinline__ void head4_norm_rope(uint2 xa, uint2 xb, uint2 wa, uint2 wb, uint2 ca, uint2 cb,
+                                                uint2 sa, uint2 sb, float eps, uint2& lo, uint2& hi) {
+    float a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = bf16_quad(xa, i);
+        b[i] = bf16_quad(xb, i);
+    }
+    // stages 1, 2 of wave_sum (lanes 1 and 2 apart there) are this lane's four pairs
+    float v = (head_sq(a[0], b[0]) + head_sq(a[1], b[1])) + (head_sq(a[2], b[2]) + head_sq(a[3], b[3]));
+    v += xor16(v, 1);  // row_half_mirror: the neighbouring quad
+    v += xor16(v, 3);  // row_mirror: the mirrored quad pair (lanes j ^ 2 and j ^ 3 hold the same value)
+    v += xor16(v, 4);  // readlanes 0 + 16 and 32 + 48
+    v += xor16(v, 8);  // (a + b) + (c + d)
+    const float r = rsqrtf(v / 128.0f + eps);
+    uint16_t o0[4], o1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        head_rope_apply(a[i], b[i], r, bf16_quad(wa, i), bf16_quad(wb, i), bf16_quad(ca, i), bf16_quad(cb, i),
+                        bf16_quad(sa, i), bf16_quad(sb, i), o0[i], o1[i]);
+    lo = make_uint2(o0[0] | ((uint32_t)o0[1] << 16), o0[2] | ((uint32_t)o0[3] << 16));
+    hi = make_uint2(o1[0] | ((uint32_t)o1[1] << 16), o1[2] | ((uint32_t)o1[3] << 16));
+}
+
 }  // namespace moss
 
 // ---------------------------------------------------------------- host-side plumbing

@@ -194,13 +194,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
     }
 }
 
-// The same with 16 lanes per head and four heads per wave: lane j of a head holds dims 4 j .. + 3
-// and their RoPE partners 64 + 4 j .. + 3, moved with 8-byte loads and stores.  The sum of squares
-// follows wave_sum's tree exactly -- pairs and quads inside the lane, then lanes 1 (DPP row half
-// mirror), 3 (row mirror), 4 and 8 apart -- so every output equals qk_norm_rope_kv's bit for bit.
-// Requires 8-byte aligned rows (checked by the caller).
-__device__ __forceinline__ float xor16(float v, int m) { return __shfl_xor(v, m, 16); }
-
+// The same with 16 lanes per head and four heads per wave (head4_norm_rope): lane j of a head holds
+// dims 4 j .. + 3 and their RoPE partners 64 + 4 j .. + 3, moved with 8-byte loads and stores; every
+// output equals qk_norm_rope_kv's bit for bit.  Requires 8-byte aligned rows (checked by the caller).
 __global__ __launch_bounds__(256) void qk_norm_rope_kv4(const uint16_t* __restrict__ qkv,
                                                         const uint16_t* __restrict__ qw,
                                                         const uint16_t* __restrict__ kw,
@@ -217,32 +213,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv4(const uint16_t* __restri
     const size_t base = (size_t)t * ROW + (is_q ? h * D : QH * D + (h - QH) * D);
     const uint16_t* wt = is_q ? qw : kw;
     auto ld4 = [](const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); };
-    auto el = [](uint2 v, int i) { return i == 0 ? bf16_lo(v.x) : i == 1 ? bf16_hi(v.x) : i == 2 ? bf16_lo(v.y) : bf16_hi(v.y); };
     const uint2 xa = ld4(qkv + base + 4 * j), xb = ld4(qkv + base + 64 + 4 * j);
     const int64_t p = min(max(pos[t], (int64_t)0), (int64_t)(L - 1));
     const size_t crow = cos_by_position ? (size_t)p : (size_t)t;
-    const uint2 ca = ld4(cos_t + crow * D + 4 * j), cb = ld4(cos_t + crow * D + 64 + 4 * j);
-    const uint2 sa = ld4(sin_t + crow * D + 4 * j), sb = ld4(sin_t + crow * D + 64 + 4 * j);
-    const uint2 wa = ld4(wt + 4 * j), wb = ld4(wt + 64 + 4 * j);
-    float a[4], b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        a[i] = el(xa, i);
-        b[i] = el(xb, i);
-    }
-    // stages 1, 2 of wave_sum (lanes 1 and 2 apart there) are this lane's four pairs
-    float v = (head_sq(a[0], b[0]) + head_sq(a[1], b[1])) + (head_sq(a[2], b[2]) + head_sq(a[3], b[3]));
-    v += xor16(v, 1);  // row_half_mirror: the neighbouring quad
-    v += xor16(v, 3);  // row_mirror: the mirrored quad pair (lanes j ^ 2 and j ^ 3 hold the same value)
-    v += xor16(v, 4);  // readlanes 0 + 16 and 32 + 48
-    v += xor16(v, 8);  // (a + b) + (c + d)
-    const float r = rsqrtf(v / 128.0f + eps);
-    uint16_t o0[4], o1[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        head_rope_apply(a[i], b[i], r, el(wa, i), el(wb, i), el(ca, i), el(cb, i), el(sa, i), el(sb, i), o0[i], o1[i]);
-    const uint2 lo = make_uint2(o0[0] | ((uint32_t)o0[1] << 16), o0[2] | ((uint32_t)o0[3] << 16));
-    const uint2 hi = make_uint2(o1[0] | ((uint32_t)o1[1] << 16), o1[2] | ((uint32_t)o1[3] << 16));
+    uint2 lo, hi;
+    head4_norm_rope(xa, xb, ld4(wt + 4 * j), ld4(wt + 64 + 4 * j), ld4(cos_t + crow * D + 4 * j),
+                    ld4(cos_t + crow * D + 64 + 4 * j), ld4(sin_t + crow * D + 4 * j), ld4(sin_t + crow * D + 64 + 4 * j),
+                    eps, lo, hi);
     if (is_q) {
         uint16_t* dst = q_out + ((size_t)t * QH + h) * D;
         *reinterpret_cast<uint2*>(dst + 4 * j) = lo;

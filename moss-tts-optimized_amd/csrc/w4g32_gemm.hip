@@ -502,12 +502,28 @@ __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
 // of the same outputs (waves 2, 3); each wave pair hands half of its bf16 results to the other
 // through LDS, so all four waves evaluate the SiLU.  Equal bit for bit to the unsplit GEMM of all
 // 2 N rows followed by moss_silu_mul.
-template <bool SPLIT, bool SILU = false>
+// QKR (unsplit only): the QKV projection of the prompt pass with the q/k head RMSNorm + RoPE and
+// the K/V cache write as its epilogue (N = 48 heads of 128: 32 query, 8 key, 8 value heads, one
+// head per 128-wide tile); Y receives the query heads [M, 32, 128].  Equal bit for bit to the
+// unsplit GEMM followed by moss_qk_norm_rope_kv with cos/sin rows taken by position.
+struct QkRope {
+    const uint16_t* q_weight;  // [128] head RMSNorm weights
+    const uint16_t* k_weight;
+    const uint16_t* cos_t;  // [L, 128], row = position
+    const uint16_t* sin_t;
+    uint16_t* k_cache;  // [8, L, 128]
+    uint16_t* v_cache;
+    const int64_t* positions;  // [M], clamped into 0 .. L - 1
+    int L;
+    float eps;
+};
+
+template <bool SPLIT, bool SILU = false, bool QKR = false>
 __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t* __restrict__ X, const uint4* qw,
                                                               const uint16_t* sc, const uint8_t* zp,
                                                               uint16_t* __restrict__ Y, float* __restrict__ part,
-                                                              int M, int N, int K) {
-    static_assert(!(SPLIT && SILU), "the SiLU epilogue needs whole sums");
+                                                              int M, int N, int K, QkRope qr) {
+    static_assert(!(SPLIT && (SILU || QKR)) && !(SILU && QKR), "the epilogues need whole sums");
     constexpr int BN = SILU ? 64 : 128, BM = 128, JT = 4;
     __shared__ __attribute__((aligned(1024))) uint16_t Xa[BM * kBK];
     __shared__ __attribute__((aligned(1024))) uint16_t Xb[BM * kBK];
@@ -679,6 +695,75 @@ __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t*
                 }
                 *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
             }
+        }
+        return;
+    }
+    if constexpr (QKR) {
+        // The tile is one head of 128 tokens.  Its bf16 products (rounded as the plain store rounds
+        // them) are staged token-major in the activation buffers -- rows 0..63 in Xa, 64..127 in
+        // Xb, 8-byte chunk c of row r at c ^ (r & 31), so the 32 rows of one store hit distinct
+        // banks -- then each token row goes through head4_norm_rope on 16 lanes, 16 rows per pass.
+        constexpr int QH = 32, KH = 8, D = 128;
+        const int head = n0 / D, jl = tid & 15;
+        auto ld4 = [](const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); };
+        // this thread's 8 token rows r = 16 pass + tid / 16: positions first, then (for query and key
+        // heads) the weights and all cos / sin quads, so their latencies overlap the staging
+        int64_t pos[8];
+#pragma unroll
+        for (int pass = 0; pass < 8; ++pass) {
+            const int m = min(m0 + 16 * pass + (tid >> 4), M - 1);
+            pos[pass] = min(max(qr.positions[m], (int64_t)0), (int64_t)(qr.L - 1));
+        }
+        auto chunk = [&](int r, int c) {
+            return reinterpret_cast<uint2*>((r < 64 ? Xa : Xb) + (r & 63) * 128 + 4 * (c ^ (r & 31)));
+        };
+        __syncthreads();  // every wave's copies have landed; no wave reads the buffers any more
+#pragma unroll
+        for (int j = 0; j < JT; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint2 o;
+                o.x = pack_bf16x2(acc[j][4 * q], acc[j][4 * q + 1]);
+                o.y = pack_bf16x2(acc[j][4 * q + 2], acc[j][4 * q + 3]);
+                *chunk(32 * j + (lane & 31), 8 * wave + 2 * q + (lane >> 5)) = o;
+            }
+        if (head >= QH + KH) {  // value heads: the rounded products as they are
+            __syncthreads();
+#pragma unroll
+            for (int pass = 0; pass < 8; ++pass) {
+                const int r = 16 * pass + (tid >> 4);
+                if (m0 + r >= M) continue;
+                uint16_t* vd = qr.v_cache + ((size_t)(head - QH - KH) * qr.L + pos[pass]) * D;
+                *reinterpret_cast<uint2*>(vd + 4 * jl) = *chunk(r, jl);
+                *reinterpret_cast<uint2*>(vd + 64 + 4 * jl) = *chunk(r, 16 + jl);
+            }
+            return;
+        }
+        const uint16_t* wt = head < QH ? qr.q_weight : qr.k_weight;
+        const uint2 wa = ld4(wt + 4 * jl), wb = ld4(wt + 64 + 4 * jl);
+        uint2 cs[8][4];
+#pragma unroll
+        for (int pass = 0; pass < 8; ++pass) {
+            const uint16_t* cr = qr.cos_t + (size_t)pos[pass] * D;
+            const uint16_t* sr = qr.sin_t + (size_t)pos[pass] * D;
+            cs[pass][0] = ld4(cr + 4 * jl);
+            cs[pass][1] = ld4(cr + 64 + 4 * jl);
+            cs[pass][2] = ld4(sr + 4 * jl);
+            cs[pass][3] = ld4(sr + 64 + 4 * jl);
+        }
+        __syncthreads();
+        // each token row through head4_norm_rope on 16 lanes, 16 rows per pass
+#pragma unroll
+        for (int pass = 0; pass < 8; ++pass) {
+            const int r = 16 * pass + (tid >> 4), m = m0 + r;
+            if (m >= M) continue;  // whole 16-lane groups
+            uint2 lo, hi;
+            head4_norm_rope(*chunk(r, jl), *chunk(r, 16 + jl), wa, wb, cs[pass][0], cs[pass][1], cs[pass][2],
+                            cs[pass][3], qr.eps, lo, hi);
+            uint16_t* dst = head < QH ? Y + ((size_t)m * QH + head) * D
+                                      : qr.k_cache + ((size_t)(head - QH) * qr.L + pos[pass]) * D;
+            *reinterpret_cast<uint2*>(dst + 4 * jl) = lo;
+            *reinterpret_cast<uint2*>(dst + 64 + 4 * jl) = hi;
         }
         return;
     }
@@ -1029,10 +1114,12 @@ void launch_reg(const Plan& p, const void* x, const void* qw, const void* sc, co
     if constexpr (JT == 4) {
         if (p.split > 1)
             hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<true>), grid, dim3(256), 0, st, (const uint16_t*)x,
-                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
+                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K,
+                               QkRope{});
         else
             hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<false>), grid, dim3(256), 0, st, (const uint16_t*)x,
-                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K);
+                               (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)ws, M, N, K,
+                               QkRope{});
         return;
     }
     if (p.split > 1)
@@ -1098,6 +1185,14 @@ bool silu_fusable_shape(int M, int K, int N) {
 
 long long align16(long long b) { return (b + 15) & ~15ll; }
 
+// The QKV projection (N = 6144) with the q/k-norm + RoPE epilogue: fused under the same conditions.
+constexpr int kQkvN = 6144;
+bool qk_rope_fusable_shape(int M, int K) {
+    if (M <= 64) return false;
+    const Plan p = plan_gemm(M, K, kQkvN, true);
+    return p.reg && p.bm == 128 && p.split == 1;
+}
+
 // One workspace serves both formats and the LDS-tile fallback: the largest plan's partial sums.
 long long gemm_workspace_bytes(int M, int K, int N) {
     long long bytes = 0;
@@ -1142,7 +1237,7 @@ MOSS_API int moss_w4g32_gemm_silu(const void* x, const void* qw, const void* sc,
         const dim3 grid((unsigned)(((M + 127) / 128) * ((N + 63) / 64)));
         hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<false, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
                            (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (float*)nullptr,
-                           M, N, K);
+                           M, N, K, QkRope{});
         return moss_launch_status();
     }
     const long long inter = align16((long long)M * 2 * N * 2);
@@ -1155,6 +1250,48 @@ MOSS_API int moss_w4g32_gemm_silu(const void* x, const void* qw, const void* sc,
 
 extern "C" int moss_rmsnorm(const void* x, const void* res, const void* w, void* sum_out, void* y, int rows, int n,
                             float eps, void* stream);
+extern "C" int moss_qk_norm_rope_kv(const void* qkv, const void* q_weight, const void* k_weight, const void* cos,
+                                    const void* sin, void* q_out, void* k_cache, void* v_cache, const void* positions,
+                                    int L, int ntok, float eps, int cos_by_position, void* stream);
+
+// The unfused form keeps the [M, 6144] QKV product in the workspace, followed by the GEMM's own
+// K-split partials.
+MOSS_API long long moss_gemm_qk_rope_workspace_bytes(int M, int K) {
+    if (M <= 0 || K <= 0 || K % 64) return 0;
+    if (qk_rope_fusable_shape(M, K)) return 0;
+    return align16((long long)M * kQkvN * 2) + gemm_workspace_bytes(M, K, kQkvN);
+}
+
+MOSS_API int moss_w4g32_gemm_qk_rope(const void* x, const void* qw, const void* sc, const void* zp,
+                                     const void* q_weight, const void* k_weight, const void* cos, const void* sin,
+                                     void* q_out, void* k_cache, void* v_cache, const void* positions, int M, int K,
+                                     int L, float eps, void* workspace, long long workspace_bytes, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && q_weight && k_weight && cos && sin && q_out && k_cache && v_cache &&
+                   positions && M > 0 && K > 0 && K % 64 == 0 && L > 0 && eps >= 0.f && workspace_bytes >= 0);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && MOSS_ALIGNED(q_weight, 8) &&
+                   MOSS_ALIGNED(k_weight, 8) && MOSS_ALIGNED(cos, 8) && MOSS_ALIGNED(sin, 8) &&
+                   MOSS_ALIGNED(q_out, 8) && MOSS_ALIGNED(k_cache, 8) && MOSS_ALIGNED(v_cache, 8) &&
+                   MOSS_ALIGNED(positions, 8));
+    hipStream_t st = (hipStream_t)stream;
+    if (qk_rope_fusable_shape(M, K) && MOSS_ALIGNED(sc, 16) && MOSS_ALIGNED(zp, 8)) {
+        const QkRope qr{(const uint16_t*)q_weight, (const uint16_t*)k_weight, (const uint16_t*)cos,
+                        (const uint16_t*)sin, (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)positions, L,
+                        eps};
+        const dim3 grid((unsigned)(((M + 127) / 128) * (kQkvN / 128)));
+        hipLaunchKernelGGL((w4g32_gemm_tdma_kernel<false, false, true>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                           (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)q_out,
+                           (float*)nullptr, M, kQkvN, K, qr);
+        return moss_launch_status();
+    }
+    const long long inter = align16((long long)M * kQkvN * 2);
+    MOSS_CHECK_ARG(workspace && MOSS_ALIGNED(workspace, 16) && workspace_bytes >= inter);
+    char* ws = (char*)workspace;
+    if (int rc = launch_gemm<kInt4G32>(x, qw, sc, zp, ws, M, K, kQkvN, nullptr, ws + inter, workspace_bytes - inter,
+                                       st))
+        return rc;
+    return moss_qk_norm_rope_kv(ws, q_weight, k_weight, cos, sin, q_out, k_cache, v_cache, positions, L, M, eps, 1,
+                                stream);
+}
 
 // The O / down projection followed by the residual add and RMSNorm of the prompt pass.  A K-split
 // plan's partials go straight into the norm kernel, which reduces them in split order; otherwise

@@ -294,9 +294,8 @@ class DecodeStepG32:
         qbuf = torch.empty((n, QH, HD), device=self.device, dtype=torch.bfloat16)
         mlp = None
         for i, layer in enumerate(self.layers):
-            qkv = w4g32.gemm(state, layer.qkv.packed)
-            pointwise.qk_rope(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i], self.values[i],
-                              positions, eps, cos_by_position=True, out=qbuf)
+            w4g32.gemm_qk_rope(state, layer.qkv.packed, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
+                               self.values[i], positions, eps, out=qbuf)
             attn = attention.prefill_attention(qbuf, self.keys[i], self.values[i], start)
             residual, state = w4g32.gemm_add_rmsnorm(attn, layer.o.packed, residual, layer.post_norm, eps)
             act = w4g32.gemm_silu(state, layer.gate_up.packed)

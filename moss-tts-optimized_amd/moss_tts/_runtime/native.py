@@ -39,6 +39,9 @@ SIGNATURES: dict[str, list] = {
     "moss_gemm_workspace_bytes": [_I, _I, _I],
     "moss_w4g32_gemm_silu": [_P, _P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_gemm_silu_workspace_bytes": [_I, _I, _I],
+    "moss_w4g32_gemm_qk_rope": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P,
+                                ctypes.c_longlong, _P],
+    "moss_gemm_qk_rope_workspace_bytes": [_I, _I],
     "moss_w4g32_gemm_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P, ctypes.c_longlong, _P],
     "moss_w4g32_gemm_noalloc": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4g32_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
@@ -70,7 +73,8 @@ SIGNATURES: dict[str, list] = {
                           _P],
 }
 _RESTYPES = {"moss_error_string": ctypes.c_char_p, "moss_gemm_workspace_bytes": ctypes.c_longlong,
-             "moss_gemm_silu_workspace_bytes": ctypes.c_longlong}
+             "moss_gemm_silu_workspace_bytes": ctypes.c_longlong,
+             "moss_gemm_qk_rope_workspace_bytes": ctypes.c_longlong}
 
 
 class NativeLibraryMissing(RuntimeError):

@@ -326,6 +326,53 @@ def gemm_silu(x: torch.Tensor, w: PackedW4G32) -> torch.Tensor:
     return y
 
 
+def gemm_qk_rope(x: torch.Tensor, w: PackedW4G32, q_weight: torch.Tensor, k_weight: torch.Tensor, cos: torch.Tensor,
+                 sin: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, positions: torch.Tensor, eps: float, *,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill QKV projection with the q/k head RMSNorm + RoPE and the K/V cache write as its
+    epilogue: equal bit for bit to ``pointwise.qk_rope(gemm(x, w), q_weight, k_weight, cos, sin, keys,
+    values, positions, eps, cos_by_position=True, out=out)`` (``src/moss_tts/_runtime/prefill_qkv.py:31-53``).
+    ``w`` holds the 6144 QKV rows; ``cos``/``sin`` are ``[L, 128]`` tables indexed by each token's
+    device-side position (clamped into the cache).  Returns ``q`` as ``[1, 32, n, 128]`` (a
+    transposed view of ``[1, n, 32, 128]``), like ``qk_rope``."""
+    from . import pointwise
+
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    _require(x.shape[-1] == w.K, f"x must end in a dimension of {w.K}")
+    _require(_aligned(x, 16), "x must be 16-byte aligned")
+    _require(w.N == pointwise.QKV, f"the QKV weight must hold {pointwise.QKV} rows")
+    n = x.numel() // w.K
+    _require(n > 0, "empty input")
+    dev = x.device
+    _require(keys.ndim == 4 and keys.shape == values.shape and tuple(keys.shape[:2]) == (1, pointwise.KH)
+             and keys.shape[3] == pointwise.HD, "matching [1, 8, L, 128] KV buffers required")
+    L = keys.shape[2]
+    for name, t in (("keys", keys), ("values", values), ("cos", cos), ("sin", sin), ("q_weight", q_weight),
+                    ("k_weight", k_weight)):
+        _cuda_contig(name, t, torch.bfloat16, dev)
+        _require(_aligned(t, 8), f"{name} must be 8-byte aligned")
+    for name, t in (("cos", cos), ("sin", sin)):
+        _require(t.numel() == L * pointwise.HD, f"{name} must hold {L} rows of {pointwise.HD}")
+    for name, t in (("q_weight", q_weight), ("k_weight", k_weight)):
+        _require(t.numel() == pointwise.HD, f"{name} must hold {pointwise.HD} values")
+    _cuda_contig("positions", positions, torch.int64, dev)
+    _require(positions.numel() == n, "one int64 position per token required")
+    _require(n <= L, "more tokens than KV rows")
+    if out is not None:
+        _cuda_contig("out", out, torch.bfloat16, dev)
+        _require(out.numel() == n * pointwise.QH * pointwise.HD, f"out must hold {n * pointwise.QH * pointwise.HD} values")
+        q = out.view(1, n, pointwise.QH, pointwise.HD)
+    else:
+        q = torch.empty((1, n, pointwise.QH, pointwise.HD), device=dev, dtype=torch.bfloat16)
+    _require(_aligned(q, 8), "out must be 8-byte aligned")
+    wp, wb, _keep = native.workspace(int(native.lib().moss_gemm_qk_rope_workspace_bytes(n, w.K)), dev)
+    native.call("moss_w4g32_gemm_qk_rope", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
+                native.ptr(q_weight), native.ptr(k_weight), native.ptr(cos), native.ptr(sin), native.ptr(q),
+                native.ptr(keys), native.ptr(values), native.ptr(positions), n, w.K, L, float(eps), wp, wb,
+                native.stream_of(x))
+    return q.transpose(1, 2)
+
+
 def gemm_add_rmsnorm(x: torch.Tensor, w: PackedW4G32, residual: torch.Tensor, norm_weight: torch.Tensor,
                      eps: float) -> tuple:
     """Prefill projection followed by the residual add and RMSNorm: ``(summed, y)`` with

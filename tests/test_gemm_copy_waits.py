@@ -88,7 +88,7 @@ def test_check_rejects_a_lax_wait():
 
 def test_copy_tile_waits_cover_every_copy(tmp_path):
     bodies = _kernel_bodies(_device_asm(tmp_path), "w4g32_gemm_tdma_kernel")
-    assert len(bodies) == 3, sorted(bodies)  # split, unsplit, unsplit with the SiLU epilogue
+    assert len(bodies) == 4, sorted(bodies)  # split, unsplit, unsplit with the SiLU or the q/k-norm + RoPE epilogue
     for name, body in bodies.items():
         assert any(t.startswith("global_load_lds_dwordx4") for t in body), name
         # prologue + 8 steps of the paired-block loop + 4 steps of the last block

@@ -309,6 +309,39 @@ def test_gemm_silu_equals_gemm_then_silu(dev, m, k, n, fused):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("m,fused", [(512, True), (600, True), (257, True), (128, False), (37, False), (2, False)])
+def test_gemm_qk_rope_equals_gemm_then_qk_rope(dev, m, fused):
+    """The QKV projection with the q/k-norm + RoPE + KV write epilogue equals the GEMM followed by
+    ``qk_rope`` bit for bit: the query heads, every K/V row written and every row left alone (token
+    positions scattered over the cache, one clamped from past its end)."""
+    from moss_tts._runtime import native, pointwise, w4g32
+
+    print(f"gemm + qk rope M={m} fused={fused}", flush=True)
+    assert (native.lib().moss_gemm_qk_rope_workspace_bytes(m, 4096) == 0) == fused
+    g = torch.Generator(device=dev).manual_seed(m)
+    L = 1024
+    w = w4g32.quantize_minmax(torch.randn((6144, 4096), device=dev, generator=g) * 0.02)
+    x = torch.randn((m, 4096), device=dev, generator=g).bfloat16()
+    qn = (1 + 0.1 * torch.randn(128, device=dev, generator=g)).bfloat16()
+    kn = (1 + 0.1 * torch.randn(128, device=dev, generator=g)).bfloat16()
+    ang = torch.arange(L, device=dev)[:, None] * (1e-3 * torch.arange(1, 129, device=dev))[None, :]
+    cos, sin = ang.cos().bfloat16().contiguous(), ang.sin().bfloat16().contiguous()
+    pos = torch.randperm(L - 1, device=dev, generator=g)[:m].to(torch.int64)
+    pos[0] = L + 5  # clamped to row L - 1
+    base_k = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    base_v = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    k1, v1, k2, v2 = base_k.clone(), base_v.clone(), base_k.clone(), base_v.clone()
+    q1 = w4g32.gemm_qk_rope(x, w, qn, kn, cos, sin, k1, v1, pos, 1e-6)
+    q2 = pointwise.qk_rope(w4g32.gemm(x, w), qn, kn, cos, sin, k2, v2, pos, 1e-6, cos_by_position=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q1.contiguous().view(torch.int16), q2.contiguous().view(torch.int16))
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
+    assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
+    untouched = torch.ones(L, dtype=torch.bool, device=dev)
+    untouched[pos.clamp(0, L - 1)] = False
+    assert torch.equal(k1[:, :, untouched].view(torch.int16), base_k[:, :, untouched].view(torch.int16))
+
+
 @pytest.mark.parametrize("m,k,n", [(512, 4096, 4096), (512, 12288, 4096), (1024, 4096, 4096), (64, 4096, 4096),
                                    (16, 4096, 4096), (200, 1024, 512), (3, 4096, 4096)])
 def test_gemm_add_rmsnorm_equals_gemm_then_add_rmsnorm(dev, m, k, n):
