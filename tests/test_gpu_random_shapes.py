@@ -111,6 +111,7 @@ GEMM_ADDNORM = [(_rng.choice((_rng.randint(2, 64), _rng.randint(65, 1100))), 64 
                  8 * _rng.randint(1, 1024)) for _ in range(8)]
 GEMM_SILU = [(_rng.choice((_rng.randint(2, 64), _rng.randint(65, 700))), 64 * _rng.choice((16, 64, 128, 192)),
               4 * _rng.randint(1, 3500)) for _ in range(8)]
+GEMM_QK_ROPE = [(_rng.randint(1, 1100), 64 * _rng.choice((16, 64, 128)), 64 * _rng.randint(18, 40)) for _ in range(6)]
 
 
 def _rel(a, b):
@@ -349,3 +350,28 @@ def test_gemm_add_rmsnorm_random_shape(dev, m, k, n):
     want = pointwise.add_rmsnorm(w4g32.gemm(x, pw), res, nw, 1e-6)
     got = w4g32.gemm_add_rmsnorm(x, pw, res, nw, 1e-6)
     assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+@pytest.mark.parametrize("m,k,L", GEMM_QK_ROPE)
+def test_gemm_qk_rope_random_shape(dev, m, k, L):
+    """The QKV GEMM with the q/k-norm + RoPE + KV write epilogue (fused above 256 tokens, through
+    the workspace otherwise) equals the GEMM followed by qk_rope bit for bit, caches included."""
+    from moss_tts._runtime import pointwise, w4g32
+
+    print(f"gemm_qk_rope M={m} K={k} L={L}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(m + k + L)
+    w = w4g32.quantize_minmax(torch.randn((6144, k), device=dev, generator=g) * 0.02)
+    x = torch.randn((m, k), device=dev, generator=g).bfloat16()
+    qn = (1 + 0.1 * torch.randn(128, device=dev, generator=g)).bfloat16()
+    kn = (1 + 0.1 * torch.randn(128, device=dev, generator=g)).bfloat16()
+    cos = torch.randn((L, 128), device=dev, generator=g).bfloat16()
+    sin = torch.randn((L, 128), device=dev, generator=g).bfloat16()
+    pos = torch.randperm(L, device=dev, generator=g)[:m].to(torch.int64)
+    k1 = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    v1 = torch.randn((1, 8, L, 128), device=dev, generator=g).bfloat16()
+    k2, v2 = k1.clone(), v1.clone()
+    q1 = w4g32.gemm_qk_rope(x, w, qn, kn, cos, sin, k1, v1, pos, 1e-6)
+    q2 = pointwise.qk_rope(w4g32.gemm(x, w), qn, kn, cos, sin, k2, v2, pos, 1e-6, cos_by_position=True)
+    assert torch.equal(q1.contiguous().view(torch.int16), q2.contiguous().view(torch.int16))
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
+    assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
