@@ -211,9 +211,10 @@ long long moss_gemm_silu_workspace_bytes(int M, int K, int N);
  * [M, 32, 128]; K/V rows positions[t] (int64 [M], clamped into 0 .. L - 1) of the [8, L, 128]
  * caches; cos/sin [L, 128]; q_weight/k_weight [128].  For M > 64 where the GEMM plan has no K split
  * (Qwen3-8B at M > 256) the norm, RoPE and cache writes run inside the GEMM and no [M, 6144]
- * product is written; otherwise the product and the GEMM's partial sums go to a caller-owned
- * workspace of moss_gemm_qk_rope_workspace_bytes(M, K) bytes (16-byte aligned; also for sc/zp
- * not 16/8-byte aligned).  x, qw 16-byte aligned; the bf16 vectors, caches, q_out and positions
+ * product is written; otherwise the GEMM's output goes to a caller-owned workspace of
+ * moss_gemm_qk_rope_workspace_bytes(M, K) bytes (16-byte aligned; also for sc/zp not 16/8-byte
+ * aligned), and a K-split plan's fp32 partials are reduced by the RoPE kernel itself, in split
+ * order.  x, qw 16-byte aligned; the bf16 vectors, caches, q_out and positions
  * 8-byte aligned.  Replaces qkv_proj and the prefill q/k-norm + RoPE + cache write
  * (src/moss_tts/_runtime/llm.py:84, :95-98, prefill_qkv.py:31-53). */
 int moss_w4g32_gemm_qk_rope(const void *x, const void *qw, const void *sc, const void *zp, const void *q_weight,

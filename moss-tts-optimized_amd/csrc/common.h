@@ -259,6 +259,11 @@ static inline int moss_launch_status() { return (int)hipGetLastError(); }
 
 namespace moss {
 // norm_rope.hip: the split-K reduction fused with the residual add + RMSNorm after a GEMM.
+// The split-K reduction of the QKV GEMM's fp32 partials fused with the q/k-norm + RoPE + KV write
+// (cos/sin by position; 8-byte aligned vectors, 16-byte aligned partials).
+int qk_rope_from_parts(const float* parts, int S, const void* q_weight, const void* k_weight, const void* cos,
+                       const void* sin, void* q_out, void* k_cache, void* v_cache, const void* positions, int L,
+                       int ntok, float eps, hipStream_t st);
 int addnorm_from_parts(const float* parts, int S, const void* res, const void* w, void* sum_out, void* y, int rows,
                        int n, float eps, hipStream_t st);
 }  // namespace moss

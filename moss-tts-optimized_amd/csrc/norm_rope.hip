@@ -197,6 +197,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv(const uint16_t* __restric
 // The same with 16 lanes per head and four heads per wave (head4_norm_rope): lane j of a head holds
 // dims 4 j .. + 3 and their RoPE partners 64 + 4 j .. + 3, moved with 8-byte loads and stores; every
 // output equals qk_norm_rope_kv's bit for bit.  Requires 8-byte aligned rows (checked by the caller).
+// PARTS: the QKV rows are a K-split GEMM's S fp32 partials [S, ntok, 6144] (16-byte aligned), summed
+// in split order and rounded to bf16 as gemm_reduce does, so the outputs equal gemm_reduce followed
+// by the plain form bit for bit.
+template <bool PARTS = false>
 __global__ __launch_bounds__(256) void qk_norm_rope_kv4(const uint16_t* __restrict__ qkv,
                                                         const uint16_t* __restrict__ qw,
                                                         const uint16_t* __restrict__ kw,
@@ -204,7 +208,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv4(const uint16_t* __restri
                                                         const uint16_t* __restrict__ sin_t,
                                                         uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
                                                         uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
-                                                        int L, int ntok, float eps, int cos_by_position) {
+                                                        int L, int ntok, float eps, int cos_by_position,
+                                                        const float* __restrict__ parts = nullptr, int S = 0) {
     constexpr int QH = 32, KH = 8, D = 128, ROW = (QH + 2 * KH) * D;  // 6144
     const int g = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);  // (token, head); 16-lane aligned
     if (g >= ntok * (QH + KH)) return;                                    // whole 16-lane groups only
@@ -213,7 +218,30 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv4(const uint16_t* __restri
     const size_t base = (size_t)t * ROW + (is_q ? h * D : QH * D + (h - QH) * D);
     const uint16_t* wt = is_q ? qw : kw;
     auto ld4 = [](const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); };
-    const uint2 xa = ld4(qkv + base + 4 * j), xb = ld4(qkv + base + 64 + 4 * j);
+    auto row4 = [&](size_t off) {  // QKV elements off .. off + 3
+        if constexpr (PARTS) {
+            // partials loaded 8 at a time before they are added, in split order
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int z0 = 0; z0 < S; z0 += 8) {
+                float4 v[8];
+#pragma unroll
+                for (int z = 0; z < 8; ++z)
+                    if (z0 + z < S) v[z] = *reinterpret_cast<const float4*>(parts + (size_t)(z0 + z) * ntok * ROW + off);
+#pragma unroll
+                for (int z = 0; z < 8; ++z)
+                    if (z0 + z < S) {
+                        acc.x += v[z].x;
+                        acc.y += v[z].y;
+                        acc.z += v[z].z;
+                        acc.w += v[z].w;
+                    }
+            }
+            return make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
+        } else {
+            return ld4(qkv + off);
+        }
+    };
+    const uint2 xa = row4(base + 4 * j), xb = row4(base + 64 + 4 * j);
     const int64_t p = min(max(pos[t], (int64_t)0), (int64_t)(L - 1));
     const size_t crow = cos_by_position ? (size_t)p : (size_t)t;
     uint2 lo, hi;
@@ -231,8 +259,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv4(const uint16_t* __restri
         *reinterpret_cast<uint2*>(kd + 4 * j) = lo;
         *reinterpret_cast<uint2*>(kd + 64 + 4 * j) = hi;
         const size_t vb = (size_t)t * ROW + (QH + KH) * D + kh * D;
-        *reinterpret_cast<uint2*>(vd + 4 * j) = ld4(qkv + vb + 4 * j);
-        *reinterpret_cast<uint2*>(vd + 64 + 4 * j) = ld4(qkv + vb + 64 + 4 * j);
+        *reinterpret_cast<uint2*>(vd + 4 * j) = row4(vb + 4 * j);
+        *reinterpret_cast<uint2*>(vd + 64 + 4 * j) = row4(vb + 64 + 4 * j);
     }
 }
 
@@ -259,6 +287,18 @@ __global__ __launch_bounds__(256) void silu_mul_rows(const uint32_t* __restrict_
 
 // The split-K reduction of a GEMM's fp32 partials fused with the residual add and RMSNorm that
 // follow it (rows x n outputs, S partials each; n % 8 == 0, 16-byte aligned buffers).
+int qk_rope_from_parts(const float* parts, int S, const void* q_weight, const void* k_weight, const void* cos,
+                       const void* sin, void* q_out, void* k_cache, void* v_cache, const void* positions, int L,
+                       int ntok, float eps, hipStream_t st) {
+    if (S < 1) return (int)hipErrorInvalidValue;
+    const int waves = ntok * 40;
+    hipLaunchKernelGGL(qk_norm_rope_kv4<true>, dim3((waves + 15) / 16), dim3(256), 0, st, (const uint16_t*)nullptr,
+                       (const uint16_t*)q_weight, (const uint16_t*)k_weight, (const uint16_t*)cos, (const uint16_t*)sin,
+                       (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)positions, L, ntok,
+                       eps, 1, parts, S);
+    return moss_launch_status();
+}
+
 int addnorm_from_parts(const float* parts, int S, const void* res, const void* w, void* sum_out, void* y, int rows,
                        int n, float eps, hipStream_t st) {
     hipLaunchKernelGGL((rmsnorm_rows<true, false, true>), dim3(rows), dim3(kNormThreads), 0, st,
@@ -313,7 +353,7 @@ MOSS_API int moss_qk_norm_rope_kv(const void* qkv, const void* q_weight, const v
     const int waves = ntok * 40;
     if (MOSS_ALIGNED(qkv, 8) && MOSS_ALIGNED(q_weight, 8) && MOSS_ALIGNED(k_weight, 8) && MOSS_ALIGNED(cos, 8) &&
         MOSS_ALIGNED(sin, 8) && MOSS_ALIGNED(q_out, 8) && MOSS_ALIGNED(k_cache, 8) && MOSS_ALIGNED(v_cache, 8)) {
-        hipLaunchKernelGGL(qk_norm_rope_kv4, dim3((waves + 15) / 16), dim3(256), 0, (hipStream_t)stream,
+        hipLaunchKernelGGL(qk_norm_rope_kv4<false>, dim3((waves + 15) / 16), dim3(256), 0, (hipStream_t)stream,
                            (const uint16_t*)qkv, (const uint16_t*)q_weight, (const uint16_t*)k_weight,
                            (const uint16_t*)cos, (const uint16_t*)sin, (uint16_t*)q_out, (uint16_t*)k_cache,
                            (uint16_t*)v_cache, (const int64_t*)positions, L, ntok, eps, cos_by_position);

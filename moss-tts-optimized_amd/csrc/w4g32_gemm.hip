@@ -1286,9 +1286,13 @@ MOSS_API int moss_w4g32_gemm_qk_rope(const void* x, const void* qw, const void* 
     const long long inter = align16((long long)M * kQkvN * 2);
     MOSS_CHECK_ARG(workspace && MOSS_ALIGNED(workspace, 16) && workspace_bytes >= inter);
     char* ws = (char*)workspace;
+    int split = 1;
     if (int rc = launch_gemm<kInt4G32>(x, qw, sc, zp, ws, M, K, kQkvN, nullptr, ws + inter, workspace_bytes - inter,
-                                       st))
+                                       st, &split))
         return rc;
+    if (split > 1)  // the RoPE kernel reduces the partials itself, in split order
+        return qk_rope_from_parts((const float*)(ws + inter), split, q_weight, k_weight, cos, sin, q_out, k_cache,
+                                  v_cache, positions, L, M, eps, st);
     return moss_qk_norm_rope_kv(ws, q_weight, k_weight, cos, sin, q_out, k_cache, v_cache, positions, L, M, eps, 1,
                                 stream);
 }
