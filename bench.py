@@ -426,13 +426,17 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False)
         end.record()
         torch.cuda.synchronize()
         pms = start.elapsed_time(end) / 5
-        proj = 2 * n * (HIDDEN * 6144 + HIDDEN * HIDDEN + HIDDEN * 2 * INTER + INTER * HIDDEN) * n_layers
-        attn = n_layers * 32 * 2 * 2 * 128 * n * (n + 1) // 2
+        # the flop the pass performs: every layer's QKV for all n tokens; attention, O and the MLP for
+        # all n tokens in the first n_layers - 1 layers and for the last token alone in the last one
+        rest = HIDDEN * HIDDEN + HIDDEN * 2 * INTER + INTER * HIDDEN
+        proj = 2 * HIDDEN * 6144 * n * n_layers + 2 * rest * (n * (n_layers - 1) + 1)
+        attn = (n_layers - 1) * 32 * 2 * 2 * 128 * n * (n + 1) // 2 + 32 * 2 * 2 * 128 * n
         tf = (proj + attn) / pms / 1e9
         prefill = {"tokens": n, "layers": n_layers, "ms": round(pms, 3), "TFLOP/s": round(tf, 1),
                    "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flop": proj + attn,
                    "parts": "embedding, per layer: norms, INT4 GEMMs, q/k-norm + RoPE + KV write, causal attention, "
-                            "SiLU*mul; final norm + heads on the last token"}
+                            "SiLU*mul (the last layer's attention, O and MLP for the last token only, whose logits "
+                            "the pass returns); final norm + heads on the last token"}
         _log(f"[bench] prefill of {n} tokens through {n_layers} layers: {pms:.3f} ms, {tf:.0f} TFLOP/s")
         eng.prefill_graphs.clear()
     nbytes = eng.step_bytes(2047)

@@ -284,7 +284,9 @@ class DecodeStepG32:
         GEMM -> q/k head-norm + RoPE with the K/V rows written at ``positions``
         (``prefill_qkv.py:31-53``) -> causal attention over cache rows ``0 .. position``
         (``llm.py:116-128``) -> O GEMM -> add-RMSNorm -> gate||up GEMM -> SiLU*mul -> down GEMM ->
-        add-RMSNorm into the next layer; then the final add-RMSNorm + heads on the token ``last``.
+        add-RMSNorm into the next layer; the last layer writes every token's K/V rows and runs its
+        attention, O projection and MLP for the token ``last`` alone (only its logits are returned),
+        then the final add-RMSNorm + heads on it.
         ``ids`` int64 ``[n, 33]``, ``positions`` int64 ``[n]`` (= start + arange(n)), ``start`` and
         ``last`` int64 ``[1]``, all on the device.  Returns logits as ``forward`` does."""
         n, eps = ids.shape[0], self.eps
@@ -292,19 +294,28 @@ class DecodeStepG32:
         residual = x
         state = pointwise.rmsnorm(x, self.layers[0].input_norm, eps)
         qbuf = torch.empty((n, QH, HD), device=self.device, dtype=torch.bfloat16)
-        mlp = None
         for i, layer in enumerate(self.layers):
             w4g32.gemm_qk_rope(state, layer.qkv.packed, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
                                self.values[i], positions, eps, out=qbuf)
+            if i + 1 == len(self.layers):
+                break
             attn = attention.prefill_attention(qbuf, self.keys[i], self.values[i], start)
             residual, state = w4g32.gemm_add_rmsnorm(attn, layer.o.packed, residual, layer.post_norm, eps)
             act = w4g32.gemm_silu(state, layer.gate_up.packed)
-            if i + 1 < len(self.layers):
-                residual, state = w4g32.gemm_add_rmsnorm(act, layer.down.packed, residual,
-                                                         self.layers[i + 1].input_norm, eps)
-            else:
-                mlp = w4g32.gemm(act, layer.down.packed)  # the last layer's add-norm runs with the heads
-        return self._heads(mlp.index_select(0, last), residual.index_select(0, last), CODEBOOKS)
+            residual, state = w4g32.gemm_add_rmsnorm(act, layer.down.packed, residual, self.layers[i + 1].input_norm,
+                                                     eps)
+        # Only the last token's hidden state reaches the logits, so after the last layer's K/V rows
+        # are written for every token, its attention, O projection and MLP run for that token alone
+        # (the decode step's kernels, exact dequant as the GEMMs): per-row math equal to the full
+        # pass up to fp32 summation order.
+        layer, i = self.layers[-1], len(self.layers) - 1
+        attn = attention.decode_attention(qbuf.index_select(0, last), self.keys[i], self.values[i],
+                                          positions.index_select(0, last), ws=self.ws)
+        o = w4g32.gemv(attn.view(1, HIDDEN), layer.o.packed)
+        residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
+                                               residual=residual.index_select(0, last))
+        mlp = w4g32.gemv(act, layer.down.packed)
+        return self._heads(mlp, residual, CODEBOOKS)
 
     def _prefill_inputs(self, ids: torch.Tensor, start: int, rows: int):
         n = ids.shape[0]
