@@ -341,13 +341,13 @@ def prefill_bench(torch, dev):
     return out
 
 
-def prefill_pass_bench(torch, n_layers: int, dev, replays: int = 10):
-    """The 512-token prompt pass alone: the bucket graph run once by ``prefill`` and then replayed
-    ``replays`` times (11 executions in all, for a kernel trace)."""
+def prefill_pass_bench(torch, n_layers: int, dev, replays: int = 10, n: int = 512):
+    """The n-token prompt pass alone (a bucket of 128, 256 or 512 tokens): the bucket graph run once
+    by ``prefill`` and then replayed ``replays`` times (13 executions in all, with the two eager
+    warm-ups before capture, for a kernel trace)."""
     from moss_tts._runtime.decode import DecodeStepG32
 
     eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
-    n = 512
     eng.capture_prefill((n,))
     g = torch.Generator().manual_seed(5)
     ids = torch.cat([torch.randint(0, 151643, (n, 1), generator=g), torch.randint(0, 1024, (n, 32), generator=g)], 1)
@@ -469,7 +469,9 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the 36-layer decode step (both arithmetics) and its lines, for a kernel trace")
     ap.add_argument("--prefill-only", action="store_true",
-                    help="only the 36-layer 512-token prompt pass (10 graph replays), for a kernel trace")
+                    help="only the 36-layer prompt pass (10 graph replays), for a kernel trace")
+    ap.add_argument("--prefill-tokens", type=int, choices=(128, 256, 512), default=512,
+                    help="prompt length (a bucket size) for --prefill-only")
     ap.add_argument("--pmc-pass", choices=("gemv", "gemm"), default=None,
                     help="eager launches only, for rocprofv3 --pmc: 'gemv' = a 512 MiB copy of known size, "
                          "then one fused gate||up GEMV and one K=4096 N=12288 GEMV per weight copy; "
@@ -493,8 +495,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     arch = native.device_arch(0)
     if args.prefill_only:
-        _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); 512-token prompt pass only")
-        prefill_pass_bench(torch, args.decode_layers, dev)
+        _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); {args.prefill_tokens}-token prompt pass only")
+        prefill_pass_bench(torch, args.decode_layers, dev, n=args.prefill_tokens)
         return 0
     if args.decode_only:
         _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode step only")

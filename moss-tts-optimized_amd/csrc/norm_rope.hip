@@ -72,11 +72,31 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
                 float acc[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) acc[k] = 0.f;
-                for (int z = 0; z < S; ++z) {
-                    const float4 p0 = reinterpret_cast<const float4*>(pr + z * mn)[0];
-                    const float4 p1 = reinterpret_cast<const float4*>(pr + z * mn)[1];
-                    acc[0] += p0.x, acc[1] += p0.y, acc[2] += p0.z, acc[3] += p0.w;
-                    acc[4] += p1.x, acc[5] += p1.y, acc[6] += p1.z, acc[7] += p1.w;
+                if (S <= 2) {
+                    for (int z = 0; z < S; ++z) {
+                        const float4 p0 = reinterpret_cast<const float4*>(pr + z * mn)[0];
+                        const float4 p1 = reinterpret_cast<const float4*>(pr + z * mn)[1];
+                        acc[0] += p0.x, acc[1] += p0.y, acc[2] += p0.z, acc[3] += p0.w;
+                        acc[4] += p1.x, acc[5] += p1.y, acc[6] += p1.z, acc[7] += p1.w;
+                    }
+                } else {
+                    // deeper splits (short prompts): 4 partials loaded before they are added, so the
+                    // loads of a row do not wait on each other; the same split-order sum
+                    for (int z0 = 0; z0 < S; z0 += 4) {
+                        float4 p[4][2];
+#pragma unroll
+                        for (int z = 0; z < 4; ++z)
+                            if (z0 + z < S) {
+                                p[z][0] = reinterpret_cast<const float4*>(pr + (z0 + z) * mn)[0];
+                                p[z][1] = reinterpret_cast<const float4*>(pr + (z0 + z) * mn)[1];
+                            }
+#pragma unroll
+                        for (int z = 0; z < 4; ++z)
+                            if (z0 + z < S) {
+                                acc[0] += p[z][0].x, acc[1] += p[z][0].y, acc[2] += p[z][0].z, acc[3] += p[z][0].w;
+                                acc[4] += p[z][1].x, acc[5] += p[z][1].y, acc[6] += p[z][1].z, acc[7] += p[z][1].w;
+                            }
+                    }
                 }
                 a = make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
                                pack_bf16x2(acc[6], acc[7]));
