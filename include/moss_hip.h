@@ -201,8 +201,9 @@ long long moss_gemm_workspace_bytes(int M, int K, int N);
 int moss_w4g32_gemm_silu(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
                          void *workspace, long long workspace_bytes, void *stream);
 
-/* Workspace bytes moss_w4g32_gemm_silu needs for an M x K x N problem (N = the SiLU outputs); 0 when
- * the epilogue runs inside the GEMM. */
+/* Workspace bytes that always suffice for moss_w4g32_gemm_silu on an M x K x N problem (N = the SiLU
+ * outputs): the unfused form's, since whether the fused tile runs also depends on the pointers'
+ * alignment, which this query does not see. */
 long long moss_gemm_silu_workspace_bytes(int M, int K, int N);
 
 /* Prefill QKV projection (N = 6144: 32 query, 8 key, 8 value heads of 128) with the q/k head
@@ -222,8 +223,8 @@ int moss_w4g32_gemm_qk_rope(const void *x, const void *qw, const void *sc, const
                             void *v_cache, const void *positions, int M, int K, int L, float eps, void *workspace,
                             long long workspace_bytes, void *stream);
 
-/* Workspace bytes moss_w4g32_gemm_qk_rope needs for M tokens of K inputs; 0 when the epilogue runs
- * inside the GEMM. */
+/* Workspace bytes that always suffice for moss_w4g32_gemm_qk_rope on M tokens of K inputs (the
+ * unfused form's, as for moss_gemm_silu_workspace_bytes). */
 long long moss_gemm_qk_rope_workspace_bytes(int M, int K);
 
 /* Prefill O / down projection followed by the residual add and RMSNorm: with p = the bf16 product
@@ -231,9 +232,10 @@ long long moss_gemm_qk_rope_workspace_bytes(int M, int K);
  * + eps)) * norm_w), both [M, N] (N % 8 == 0, N <= 8192; x, residual, norm_w, summed_out, y 16-byte
  * aligned) -- equal bit for bit to moss_w4g32_gemm followed by moss_rmsnorm with the residual.  The
  * workspace is moss_w4g32_gemm's (moss_gemm_workspace_bytes); when the plan splits K, the norm
- * kernel reduces the partial sums itself (one launch and one [M, N] round trip fewer).  Replaces
- * o_proj / down_proj and the following add_rmsnorm of the prefill layer loop
- * (src/moss_tts/_runtime/llm.py:84, prefill_pointwise.py:46-57). */
+ * kernel reduces the partial sums itself (one launch and one [M, N] round trip fewer).  summed_out
+ * and y must not overlap x, residual or each other (an in-place residual update is refused with
+ * hipErrorInvalidValue).  Replaces o_proj / down_proj and the following add_rmsnorm of the prefill
+ * layer loop (src/moss_tts/_runtime/llm.py:84, prefill_pointwise.py:46-57). */
 int moss_w4g32_gemm_add_rmsnorm(const void *x, const void *qw, const void *sc, const void *zp, const void *residual,
                                 const void *norm_w, float eps, void *summed_out, void *y, int M, int K, int N,
                                 void *workspace, long long workspace_bytes, void *stream);
@@ -365,6 +367,11 @@ int moss_sample_topk_pair(const void *logits_a, int rows_a, int stride_a, int vo
                           int stride_b, int vocab_b, float temperature_b, int top_k_b, float top_p_b, int salt_b,
                           void *out_b, const void *seed, const void *position, void *stream);
 
+/* next_ids int64 [1 + channels] from the sampled text index (int64 [1], into text_ids int64 [2]) and
+ * audio indices (int64 [channels]): the text token becomes delay_slot_id while *delay_length >= 0 and
+ * audio_end_id at *delay_length == 32; audio code c is kept when c < *audio_length and
+ * (*delay_length < 0 or c >= *delay_length), else pad_code.  Replaces the token logic of _decode,
+ * src/moss_tts/_runtime/llm.py:280-287. */
 int moss_compose_next_ids(const void *text_index, const void *audio_index, const void *text_ids,
                           const void *audio_length, const void *delay_length, long long delay_slot_id,
                           long long audio_end_id, int channels, long long pad_code, void *next_ids, void *stream);

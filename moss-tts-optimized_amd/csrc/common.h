@@ -40,6 +40,12 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_bits(f32_to_b
 // agree bit for bit.
 __device__ __forceinline__ float silu_mul_bf16(float g, float u) { return round_bf16(g / (1.0f + expf(-g))) * u; }
 
+// The same from the fp32 gate and up projection outputs of the decode GEMVs, each rounded to bf16
+// first: the bf16 bits of bf16(bf16(silu(bf16(gate))) * bf16(up)) (src/moss_tts/_runtime/dp4a_scaled.py:65-68).
+__device__ __forceinline__ uint16_t silu_mul_rounded_bits(float gate, float up) {
+    return f32_to_bf16(silu_mul_bf16(round_bf16(gate), round_bf16(up)));
+}
+
 // Where group g's zero point sits in a row-packed zp row (blocks of 128 groups: for block c with
 // r = min(128, G - 128c) groups, byte 64c + b holds z[128c + b] low and z[128c + r/2 + b] high):
 // byte index and bit shift.  Branch-free, so a byte load through it is not followed by a wait at
@@ -266,7 +272,17 @@ int qk_rope_from_parts(const float* parts, int S, const void* q_weight, const vo
                        int ntok, float eps, hipStream_t st);
 int addnorm_from_parts(const float* parts, int S, const void* res, const void* w, void* sum_out, void* y, int rows,
                        int n, float eps, hipStream_t st);
+// add-RMSNorm of rows x n values in place: xs = bf16(xs + res), y = rmsnorm(xs) (y must not
+// overlap xs or res).
+int add_rmsnorm_inplace(void* xs, const void* res, const void* w, void* y, int rows, int n, float eps,
+                        hipStream_t st);
 }  // namespace moss
+
+// true when the byte ranges [a, a + an) and [b, b + bn) share an address
+static inline bool moss_overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+    return pa < pb + bn && pb < pa + an;
+}
 
 // The fused-norm projections: res == NULL normalizes x; otherwise s = bf16(x + res) is normalized
 // and stored to sum_out by one workgroup while the others still read x and res, so sum_out must not

@@ -42,13 +42,6 @@ __device__ __forceinline__ float slab_dot(const uint4& w, const uint32_t* xv, fl
     return acc;
 }
 
-__device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
-    const float g = round_bf16(gate);
-    const float u = round_bf16(up);
-    const float a = round_bf16(g / (1.0f + expf(-g)));
-    return f32_to_bf16(a * u);
-}
-
 // KC = ceil(K / 1024) slabs per lane; FULL: K == 1024 KC (no per-lane bound checks).
 template <int KC, int R, bool PAIRED, bool FULL>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
@@ -107,7 +100,7 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(const uint16_t* __restric
             const float a = out[r] * (scale ? scale[n] : 1.0f);
             if constexpr (PAIRED) {
                 const float b = out[R + r] * (scale ? scale[n + n_out] : 1.0f);
-                y[n] = silu_mul_bf16(a, b);
+                y[n] = silu_mul_rounded_bits(a, b);
             } else {
                 y[n] = f32_to_bf16(a);
             }

@@ -36,16 +36,11 @@ constexpr int kMaxChunks = 4;
 // PARTS: x is not read; each value is formed from S fp32 partial sums of a split-K GEMM,
 // parts[z][row][col] added in z order from 0 and rounded to bf16 -- exactly what gemm_reduce
 // (w4g32_gemm.hip) writes -- so reduce-then-norm takes one launch and no bf16 round trip.
-template <bool RESIDUAL, bool QUANT = false, bool PARTS = false>
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __restrict__ x,
-                                                             const uint16_t* __restrict__ res,
-                                                             const uint16_t* __restrict__ w,
-                                                             uint16_t* __restrict__ sum_out,
-                                                             uint16_t* __restrict__ y, int n, float eps,
-                                                             uint2* __restrict__ qx = nullptr,
-                                                             float* __restrict__ sx = nullptr,
-                                                             int* __restrict__ qsum = nullptr,
-                                                             const float* __restrict__ parts = nullptr, int S = 0) {
+// The body carries no aliasing promises; the kernels below state them.
+template <bool RESIDUAL, bool QUANT, bool PARTS>
+__device__ __forceinline__ void rmsnorm_row_body(const uint16_t* x, const uint16_t* res, const uint16_t* w,
+                                                 uint16_t* sum_out, uint16_t* y, int n, float eps, uint2* qx,
+                                                 float* sx, int* qsum, const float* parts, int S) {
     __shared__ float lds[kNormThreads / kWave];
     const size_t row = blockIdx.x;
     const int chunks = n / 8;
@@ -168,6 +163,29 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __r
             }
         }
     }
+}
+
+template <bool RESIDUAL, bool QUANT = false, bool PARTS = false>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ res,
+                                                             const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ sum_out,
+                                                             uint16_t* __restrict__ y, int n, float eps,
+                                                             uint2* __restrict__ qx = nullptr,
+                                                             float* __restrict__ sx = nullptr,
+                                                             int* __restrict__ qsum = nullptr,
+                                                             const float* __restrict__ parts = nullptr, int S = 0) {
+    rmsnorm_row_body<RESIDUAL, QUANT, PARTS>(x, res, w, sum_out, y, n, eps, qx, sx, qsum, parts, S);
+}
+
+// add-RMSNorm with sum_out == x allowed (x and sum_out carry no __restrict__): each thread reads
+// its chunks of x before it writes the same chunks of sum_out, and no thread touches another's.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_rows_inplace(const uint16_t* x,
+                                                                         const uint16_t* __restrict__ res,
+                                                                         const uint16_t* __restrict__ w,
+                                                                         uint16_t* sum_out,
+                                                                         uint16_t* __restrict__ y, int n, float eps) {
+    rmsnorm_row_body<true, false, false>(x, res, w, sum_out, y, n, eps, nullptr, nullptr, nullptr, nullptr, 0);
 }
 
 // One wave per (token, head); lane l owns dims l and l + 64, which are each other's RoPE
@@ -316,6 +334,12 @@ int qk_rope_from_parts(const float* parts, int S, const void* q_weight, const vo
                        (const uint16_t*)q_weight, (const uint16_t*)k_weight, (const uint16_t*)cos, (const uint16_t*)sin,
                        (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)positions, L, ntok,
                        eps, 1, parts, S);
+    return moss_launch_status();
+}
+
+int add_rmsnorm_inplace(void* xs, const void* res, const void* w, void* y, int rows, int n, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(add_rmsnorm_rows_inplace, dim3(rows), dim3(kNormThreads), 0, st, (const uint16_t*)xs,
+                       (const uint16_t*)res, (const uint16_t*)w, (uint16_t*)xs, (uint16_t*)y, n, eps);
     return moss_launch_status();
 }
 

@@ -47,13 +47,6 @@ __global__ __launch_bounds__(256) void int8_quantize_g32(const uint16_t* __restr
     }
 }
 
-__device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
-    const float g = round_bf16(gate);
-    const float u = round_bf16(up);
-    const float a = round_bf16(g / (1.0f + expf(-g)));
-    return f32_to_bf16(a * u);
-}
-
 // The fused normalization in front of a W4A8 projection (ACT 1: RMSNorm, ACT 2: add-RMSNorm;
 // src/moss_tts/_runtime/dp4a_norm_projection.py:48-96, dp4a_fusions.py:24-61): every
 // 256-thread workgroup recomputes y = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * w) of the one
@@ -236,7 +229,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
     }
     uint16_t val[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) val[r] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
+    for (int r = 0; r < R; ++r) val[r] = PAIRED ? silu_mul_rounded_bits(out[r], out[R + r]) : f32_to_bf16(out[r]);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)

@@ -1221,10 +1221,11 @@ MOSS_API int moss_w4g32_gemm(const void* x, const void* qw, const void* sc, cons
 }
 
 // The unfused form keeps the [M, 2 N] gate||up product in the workspace, followed by the GEMM's own
-// K-split partials.
+// K-split partials.  The fused tile needs none, but it depends on the alignment of sc, zp and y,
+// which the size query does not see: the query returns the unfused form's size for every shape, so
+// a workspace of that size always suffices.
 MOSS_API long long moss_gemm_silu_workspace_bytes(int M, int K, int N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 64 || N % 4) return 0;
-    if (silu_fusable_shape(M, K, N)) return 0;
     return align16((long long)M * 2 * N * 2) + gemm_workspace_bytes(M, K, 2 * N);
 }
 
@@ -1255,10 +1256,9 @@ extern "C" int moss_qk_norm_rope_kv(const void* qkv, const void* q_weight, const
                                     int L, int ntok, float eps, int cos_by_position, void* stream);
 
 // The unfused form keeps the [M, 6144] QKV product in the workspace, followed by the GEMM's own
-// K-split partials.
+// K-split partials; returned for every shape, as for moss_gemm_silu_workspace_bytes.
 MOSS_API long long moss_gemm_qk_rope_workspace_bytes(int M, int K) {
     if (M <= 0 || K <= 0 || K % 64) return 0;
-    if (qk_rope_fusable_shape(M, K)) return 0;
     return align16((long long)M * kQkvN * 2) + gemm_workspace_bytes(M, K, kQkvN);
 }
 
@@ -1299,8 +1299,9 @@ MOSS_API int moss_w4g32_gemm_qk_rope(const void* x, const void* qw, const void* 
 
 // The O / down projection followed by the residual add and RMSNorm of the prompt pass.  A K-split
 // plan's partials go straight into the norm kernel, which reduces them in split order; otherwise
-// the product goes to summed_out and the norm runs in place there (each thread reads a chunk
-// before it writes the same chunk).
+// the product goes to summed_out and the in-place add-RMSNorm kernel runs there (each thread reads
+// a chunk before it writes the same chunk).  summed_out and y may not overlap x, residual or each
+// other: such calls are refused.
 MOSS_API int moss_w4g32_gemm_add_rmsnorm(const void* x, const void* qw, const void* sc, const void* zp,
                                          const void* residual, const void* norm_w, float eps, void* summed_out,
                                          void* y, int M, int K, int N, void* workspace, long long workspace_bytes,
@@ -1310,13 +1311,17 @@ MOSS_API int moss_w4g32_gemm_add_rmsnorm(const void* x, const void* qw, const vo
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16) && MOSS_ALIGNED(residual, 16) &&
                    MOSS_ALIGNED(norm_w, 16) && MOSS_ALIGNED(summed_out, 16) && MOSS_ALIGNED(y, 16) &&
                    workspace_bytes >= 0);
+    const size_t xb = (size_t)M * K * 2, ob = (size_t)M * N * 2;
+    MOSS_CHECK_ARG(!moss_overlaps(summed_out, ob, x, xb) && !moss_overlaps(summed_out, ob, residual, ob) &&
+                   !moss_overlaps(y, ob, x, xb) && !moss_overlaps(y, ob, residual, ob) &&
+                   !moss_overlaps(y, ob, summed_out, ob));
     hipStream_t st = (hipStream_t)stream;
     int split = 1;
     if (int rc = launch_gemm<kInt4G32>(x, qw, sc, zp, summed_out, M, K, N, nullptr, workspace, workspace_bytes, st,
                                        &split))
         return rc;
     if (split > 1) return addnorm_from_parts((const float*)workspace, split, residual, norm_w, summed_out, y, M, N, eps, st);
-    return moss_rmsnorm(summed_out, residual, norm_w, summed_out, y, M, N, eps, stream);
+    return add_rmsnorm_inplace(summed_out, residual, norm_w, y, M, N, eps, st);
 }
 
 // ---------------------------------------------------------------------------------------------

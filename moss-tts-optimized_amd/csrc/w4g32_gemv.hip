@@ -162,13 +162,6 @@ __device__ __forceinline__ float row_partial_exact(const XSlice<KG>& xs, const R
     return acc;
 }
 
-__device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
-    const float g = round_bf16(gate);
-    const float u = round_bf16(up);
-    const float a = round_bf16(g / (1.0f + expf(-g)));
-    return f32_to_bf16(a * u);
-}
-
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Non-temporal loads: every weight byte is read once.
@@ -254,7 +247,7 @@ __device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const 
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int n = row0 + r;
-            if (n < n_out) y[n] = PAIRED ? silu_mul_bf16(out[r], out[R + r]) : f32_to_bf16(out[r]);
+            if (n < n_out) y[n] = PAIRED ? silu_mul_rounded_bits(out[r], out[R + r]) : f32_to_bf16(out[r]);
         }
     }
 }
@@ -324,7 +317,7 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
                 a += part[w][lane];
                 if constexpr (PAIRED) b += part[w][R + lane];
             }
-            y[n] = PAIRED ? silu_mul_bf16(a, b) : f32_to_bf16(a);
+            y[n] = PAIRED ? silu_mul_rounded_bits(a, b) : f32_to_bf16(a);
         }
     }
 }

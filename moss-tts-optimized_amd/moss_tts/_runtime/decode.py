@@ -20,6 +20,10 @@ logits and the delay-pattern composition of the next 33 ids.
 Static input buffers (ids, position, audio/delay lengths) make the step graph-capturable;
 ``decode()`` copies new inputs into them and replays the graph, as ``FastLLM.step`` does
 (``src/moss_tts/_runtime/llm.py:327-338``); ``step()`` returns the logits of the same graph.
+The text phase before the audio starts reads the whole text head (``lm_heads[0]``, bf16 as the
+reference keeps it): ``prefill_logits`` returns the prompt's last-token text logits and its audio
+logits (``FastLLM.prefill``, ``llm.py:204-207,303-318``) and ``full_step`` runs the layers and the
+text head alone (``FastLLM.full_step``, ``llm.py:321-325``), captured as a graph of its own.
 """
 from __future__ import annotations
 
@@ -37,7 +41,7 @@ SAMPLED_CODES = 1024                      # audio codes a head can emit (1024 is
 # MossTTSDelay token ids (the reference model config's defaults)
 GEN_SLOT_ID, DELAY_SLOT_ID, AUDIO_START_ID, AUDIO_END_ID = 151656, 151662, 151652, 151653
 PAD_ID = 151643                           # the text pad token of the prompt buckets
-PREFILL_BUCKETS = (128, 256, 512)         # prompt lengths captured as graphs (presets.py:45)
+PREFILL_BUCKETS = (128, 160, 256, 512)    # prompt lengths captured as graphs for gptq (presets.py:45)
 
 
 @dataclass
@@ -75,7 +79,8 @@ class DecodeStepG32:
                  text_embedding: torch.Tensor, audio_embedding: torch.Tensor, *, max_length: int,
                  eps: float = 1e-6, theta: float = 1e6, w4a8: bool = False, audio_stride: int = AUDIO_VOCAB,
                  greedy: bool = False, seed: int = 0, text_ids=(GEN_SLOT_ID, DELAY_SLOT_ID),
-                 audio_end_id: int = AUDIO_END_ID, audio_start_id: int = AUDIO_START_ID):
+                 audio_end_id: int = AUDIO_END_ID, audio_start_id: int = AUDIO_START_ID,
+                 text_head: Bf16Linear | None = None):
         _require(len(layers) > 0, "at least one layer")
         dev = final_norm.device
         _require(dev.type == "cuda", "the decode step runs on a HIP device")
@@ -83,9 +88,13 @@ class DecodeStepG32:
         _require(heads.in_features == HIDDEN, "heads must read the 4096-wide hidden state")
         _require(audio_stride >= SAMPLED_CODES and heads.out_features == CODEBOOKS * audio_stride + 2,
                  "heads must hold 32 audio heads of audio_stride rows, then the 2 text-head rows")
+        _require(text_head is None or (isinstance(text_head, Bf16Linear) and text_head.in_features == HIDDEN
+                                       and text_head.weight.device == dev),
+                 "text_head must be a bf16 [V, 4096] head on the step's device")
         self.layers = layers
         self.final_norm = final_norm
         self.heads = heads
+        self.text_head = text_head
         self.text_embedding = text_embedding
         self.audio_embedding = audio_embedding
         self.max_length = max_length
@@ -113,8 +122,11 @@ class DecodeStepG32:
         self.next_ids = torch.zeros(CODEBOOKS + 1, device=dev, dtype=torch.int64)
         self.graph = None
         self.logits = None
+        self.text_graph = None
+        self.text_out = None
         self.pad_id = PAD_ID
         self.prefill_graphs = {}
+        self.last_prefill_bucket = None           # the bucket graph the last prompt replayed (None: eager)
 
     # ------------------------------------------------------------------ forward
     def forward(self, head_count: int = CODEBOOKS, trace: list | None = None) -> torch.Tensor:
@@ -130,9 +142,17 @@ class DecodeStepG32:
         ``mlp_in``) and of its intermediates (``qkv``, ``attn``, ``o``, ``act``, ``mlp``, ``residual``),
         for layer-by-layer checks."""
         _require(head_count in (8, 16, 24, CODEBOOKS), "head_count must be 8, 16, 24 or 32")
+        mlp, residual = self._layers(trace)
+        logits = self._heads(mlp, residual, head_count)
+        self._sample(logits, head_count)
+        return logits
+
+    def _layers(self, trace: list | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """The embedding sum and every layer from the static ``ids``/``position`` buffers -> the last
+        layer's MLP output and the residual stream (bf16 ``[1, 4096]`` each), before the final norm."""
         if self.w4a8:
             _require(trace is None, "trace is available in the W4A16 step")
-            return self._forward_w4a8(head_count)
+            return self._layers_w4a8()
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
@@ -153,9 +173,14 @@ class DecodeStepG32:
             if trace is not None:
                 trace.append(dict(residual_in=state[0], mlp_in=state[1], qkv=qkv.clone(), attn=attn.clone(),
                                   o=o.clone(), act=act.clone(), mlp=mlp.clone(), residual=residual.clone()))
-        logits = self._heads(mlp, residual, head_count)
-        self._sample(logits, head_count)
-        return logits
+        return mlp, residual
+
+    def _text_logits(self, mlp: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """Final add-RMSNorm + the whole text head (``F.linear(h, lm_heads[0].weight)``,
+        ``src/moss_tts/_runtime/llm.py:207,318,325``) -> bf16 ``[1, V]``."""
+        _require(self.text_head is not None, "the text phase needs the model's text head (lm_heads[0])")
+        return bf16.norm_gemv(mlp, self.final_norm, self.eps, self.text_head.weight,
+                              residual=residual)[1].view(1, -1)
 
     def _heads(self, mlp: torch.Tensor, residual: torch.Tensor, head_count: int) -> torch.Tensor:
         """Final add-RMSNorm + the heads (bf16 as the reference keeps them, or INT4-G32): all rows,
@@ -196,7 +221,7 @@ class DecodeStepG32:
                                   self.delay_length, delay_slot_id=int(self.text_ids_host[1]),
                                   audio_end_id=self.audio_end_id, out=self.next_ids)
 
-    def _forward_w4a8(self, head_count: int = CODEBOOKS) -> torch.Tensor:
+    def _layers_w4a8(self) -> tuple[torch.Tensor, torch.Tensor]:
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
@@ -220,9 +245,7 @@ class DecodeStepG32:
             residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
             hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
-        logits = self._heads(mlp, residual, head_count)
-        self._sample(logits, head_count)
-        return logits
+        return mlp, residual
 
     @torch.inference_mode()
     def capture(self) -> None:
@@ -276,6 +299,45 @@ class DecodeStepG32:
         self.step(ids, position)
         return self.next_ids.clone().view(1, 1, CODEBOOKS + 1)
 
+    # ------------------------------------------------------------------ text phase
+    def _text_forward(self) -> torch.Tensor:
+        mlp, residual = self._layers()
+        return self._text_logits(mlp, residual)
+
+    @torch.inference_mode()
+    def capture_text(self) -> None:
+        """Capture the text-phase step (every layer, then the final norm and the whole text head) as
+        a graph of its own.  The reference runs ``full_step`` eagerly (``llm.py:321-325``); the graph
+        gives the same result without a host launch per kernel."""
+        _require(self.text_head is not None, "the text phase needs the model's text head (lm_heads[0])")
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._text_forward()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = self._text_forward()
+        torch.cuda.synchronize(self.device)
+        self.text_graph, self.text_out = graph, out
+
+    @torch.inference_mode()
+    def full_step(self, ids: torch.Tensor, position: int) -> torch.Tensor:
+        """The text-phase step (``FastLLM.full_step``, ``src/moss_tts/_runtime/llm.py:321-325``): ``ids``
+        int64 ``[1, 1, 33]`` (or ``[1, 33]``) at cache row ``position``, K/V written there; returns the
+        text logits bf16 ``[1, V]`` over the whole text head (a view of the graph's output buffer once
+        ``capture_text`` has run, valid until the next text step)."""
+        if not 0 <= position < self.max_length:
+            raise ValueError("KV capacity exceeded")
+        self.ids.copy_(ids.reshape(1, CODEBOOKS + 1))
+        self.position.fill_(position)
+        if self.text_graph is None:
+            return self._text_forward()
+        self.text_graph.replay()
+        return self.text_out
+
     # ------------------------------------------------------------------ prefill
     def _prefill_body(self, ids: torch.Tensor, positions: torch.Tensor, start: torch.Tensor,
                       last: torch.Tensor) -> torch.Tensor:
@@ -288,7 +350,8 @@ class DecodeStepG32:
         attention, O projection and MLP for the token ``last`` alone (only its logits are returned),
         then the final add-RMSNorm + heads on it.
         ``ids`` int64 ``[n, 33]``, ``positions`` int64 ``[n]`` (= start + arange(n)), ``start`` and
-        ``last`` int64 ``[1]``, all on the device.  Returns logits as ``forward`` does."""
+        ``last`` int64 ``[1]``, all on the device.  Returns the head logits as ``forward`` does and,
+        when the step holds the text head, the text logits ``[1, V]`` (else None)."""
         n, eps = ids.shape[0], self.eps
         x = attention.embedding_sum(ids, self.text_embedding, self.audio_embedding)
         residual = x
@@ -315,7 +378,8 @@ class DecodeStepG32:
         residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
                                                residual=residual.index_select(0, last))
         mlp = w4g32.gemv(act, layer.down.packed)
-        return self._heads(mlp, residual, CODEBOOKS)
+        logits = self._heads(mlp, residual, CODEBOOKS)
+        return logits, (self._text_logits(mlp, residual) if self.text_head is not None else None)
 
     def _prefill_inputs(self, ids: torch.Tensor, start: int, rows: int):
         n = ids.shape[0]
@@ -352,11 +416,26 @@ class DecodeStepG32:
 
     @torch.inference_mode()
     def prefill(self, ids: torch.Tensor, start: int = 0) -> torch.Tensor:
-        """The prompt pass (``FastLLM.prefill``, ``src/moss_tts/_runtime/llm.py:303-318``): ``ids`` int64
-        ``[1, n, 33]`` (or ``[n, 33]``) at cache rows ``start .. start + n - 1``; writes those K/V rows of
-        every layer and returns the last token's logits in the layout of ``step`` (32 audio heads, then
-        the 2 text-head rows).  A captured bucket serves the prompt when one fits, else it runs
-        eagerly."""
+        """The prompt pass (``src/moss_tts/_runtime/llm.py:303-318``) in the layout of ``step``: ``ids``
+        int64 ``[1, n, 33]`` (or ``[n, 33]``) at cache rows ``start .. start + n - 1``; writes those K/V
+        rows of every layer and returns the last token's head logits (32 audio heads, then the 2
+        text-head rows).  ``prefill_logits`` returns the same pass in the reference's layout."""
+        return self._prefill(ids, start)[0]
+
+    @torch.inference_mode()
+    def prefill_logits(self, ids: torch.Tensor, start: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+        """The prompt pass with ``FastLLM.prefill``'s result (``src/moss_tts/_runtime/llm.py:204-207,
+        318``): the last token's text logits over the whole text head, bf16 ``[1, V]``, and its audio
+        logits ``[32, 1024]`` (rows ``[:1024]`` of each codebook head).  Both are views of the bucket
+        graph's output buffers when a bucket serves the prompt, valid until the next prompt."""
+        _require(self.text_head is not None, "the text phase needs the model's text head (lm_heads[0])")
+        logits, text = self._prefill(ids, start)
+        audio = logits[:CODEBOOKS * self.audio_stride].view(CODEBOOKS, self.audio_stride)[:, :SAMPLED_CODES]
+        return text, audio
+
+    def _prefill(self, ids: torch.Tensor, start: int):
+        """A captured bucket serves the prompt when one fits (the smallest bucket ``>= n``), else
+        it runs eagerly."""
         ids = ids.reshape(-1, CODEBOOKS + 1)
         n = ids.shape[0]
         if n < 1 or start < 0 or start + n > self.max_length:
@@ -372,7 +451,9 @@ class DecodeStepG32:
             s_start.fill_(start)
             s_last.fill_(n - 1)
             graph.replay()
+            self.last_prefill_bucket = b
             return out
+        self.last_prefill_bucket = None
         return self._prefill_body(*self._prefill_inputs(ids.to(self.device), start, n))
 
     @property
@@ -419,23 +500,26 @@ class DecodeStepG32:
         text_rows = text_head[torch.tensor([int(t) for t in cfg_ids], device=text_head.device)]
         heads = Bf16Linear(torch.cat([h.weight[:SAMPLED_CODES] for h in model.lm_heads[1:]] + [text_rows], 0)
                            .bfloat16().contiguous())
+        # the whole text head for the text phase (prefill's text logits and full_step): held as given
+        full_text = Bf16Linear(text_head) if text_head.dtype == torch.bfloat16 else None
         audio = torch.stack([e.weight for e in model.emb_ext]).contiguous()
         return cls(layers, lm.norm.weight, heads, lm.embed_tokens.weight.contiguous(), audio,
                    max_length=max_length, eps=eps, theta=float(theta) if theta is not None else 1e6, w4a8=w4a8,
                    audio_stride=SAMPLED_CODES, text_ids=cfg_ids,
                    audio_end_id=getattr(cfg, "audio_end_token_id", AUDIO_END_ID),
-                   audio_start_id=getattr(cfg, "audio_start_token_id", AUDIO_START_ID))
+                   audio_start_id=getattr(cfg, "audio_start_token_id", AUDIO_START_ID), text_head=full_text)
 
     # -------------------------------------------------------------- synthetic model
     @classmethod
     @torch.inference_mode()
     def random(cls, n_layers: int, *, max_length: int, device, seed: int = 0, text_vocab: int = 151936,
                kv_fill: bool = True, dequant: int = w4g32.EXACT, w4a8: bool = False, greedy: bool = False,
-               sample_seed: int = 0, bf16_heads: bool = False) -> "DecodeStepG32":
+               sample_seed: int = 0, bf16_heads: bool = False, text_head: bool = False) -> "DecodeStepG32":
         """Random-init Qwen3-8B-shaped weights (N(0, 0.02), min-max INT4-G32 quantized on the
         device), norm weights 1 + N(0, 0.01), embeddings N(0, 1), KV caches N(0, 1).  The heads are
         INT4-G32 (32 x 1025 + 2 rows), or with ``bf16_heads`` bf16 N(0, 0.02) as an installed model
-        has them (32 x 1024 + 2 rows)."""
+        has them (32 x 1024 + 2 rows).  ``text_head`` adds a bf16 N(0, 0.02) text head of
+        ``text_vocab`` rows for the text phase (``prefill_logits``, ``full_step``)."""
         dev = torch.device(device)
         gen = torch.Generator(device=dev).manual_seed(seed)
 
@@ -460,8 +544,11 @@ class DecodeStepG32:
             heads = q(CODEBOOKS * stride + 2, HIDDEN)  # 32 audio heads of 1025 rows, then the 2 text rows
         text = torch.randn((text_vocab, HIDDEN), generator=gen, device=dev).bfloat16()
         audio = torch.randn((CODEBOOKS, AUDIO_VOCAB, HIDDEN), generator=gen, device=dev).bfloat16()
+        full_text = None
+        if text_head:
+            full_text = Bf16Linear((torch.randn((text_vocab, HIDDEN), generator=gen, device=dev) * 0.02).bfloat16())
         eng = cls(layers, norm(HIDDEN), heads, text, audio, max_length=max_length, w4a8=w4a8, greedy=greedy,
-                  seed=sample_seed, audio_stride=stride)
+                  seed=sample_seed, audio_stride=stride, text_head=full_text)
         if kv_fill:
             for t in eng.keys + eng.values:
                 t.copy_(torch.randn(t.shape, generator=gen, device=dev))

@@ -5,8 +5,9 @@ follow the reference (``src/moss_tts/api.py:36-99``; its checks are pinned by
 ``tests/test_api.py:101-114``).  The SM90 / Triton / nvcc checks of the reference
 (``api.py:79-82,99``) become a gfx950 device check and a check that ``libmoss_hip.so`` loads.
 What this library provides after loading is the INT4-G32 path: the model's projections swapped
-for quantized modules (``install_gptq``), the prompt pass captured per bucket length (``prefill``)
-and the batch-1 decode step captured as one HIP graph (``step``).  The streaming product loop,
+for quantized modules (``install_gptq``), the prompt pass captured per bucket length (``prefill``),
+the text-phase step over the whole text head (``full_step``) and the batch-1 decode step captured
+as one HIP graph (``step``).  The streaming product loop,
 codec and voice cloning of the reference are not part of it.
 """
 from __future__ import annotations
@@ -33,12 +34,23 @@ class GptqEngine:
         return self.decode.graph
 
     def warmup(self) -> None:
-        """Capture the prompt-pass buckets and the decode step (``llm.py:209-225,289-301``)."""
+        """Capture the prompt-pass buckets, the decode step and the text-phase step
+        (``llm.py:209-225,289-301``; buckets ``presets.py:45``)."""
         self.decode.capture_prefill()
         self.decode.capture()
+        if self.decode.text_head is not None:
+            self.decode.capture_text()
 
     def prefill(self, ids, start: int = 0):
+        """``(text logits [1, V], audio logits [32, 1024])`` of the prompt's last token."""
+        return self.decode.prefill_logits(ids, start)
+
+    def prefill_heads(self, ids, start: int = 0):
+        """The same pass with the head logits in the decode step's layout."""
         return self.decode.prefill(ids, start)
+
+    def full_step(self, ids, position: int):
+        return self.decode.full_step(ids, position)
 
     def step(self, ids, position: int):
         return self.decode.step(ids, position)
@@ -151,12 +163,20 @@ class MossTTS:
             self._lock.release()
 
     def prefill(self, ids, start: int = 0):
-        """The prompt pass (``FastLLM.prefill``, ``src/moss_tts/_runtime/llm.py:303-318``): ``ids``
-        int64 ``[1, n, 33]`` written into the KV cache at rows ``start .. start + n - 1``; returns the
-        last token's head logits (32 audio heads, then the 2 text-head rows; a view of the bucket
-        graph's output buffer, valid until the next prompt)."""
+        """The prompt pass (``FastLLM.prefill``, ``src/moss_tts/_runtime/llm.py:204-207,303-318``):
+        ``ids`` int64 ``[1, n, 33]`` written into the KV cache at rows ``start .. start + n - 1``;
+        returns the last token's text logits over the whole text head ``[1, V]`` and its audio logits
+        ``[32, 1024]`` (views of the bucket graph's output buffers, valid until the next prompt).
+        Prompts of up to 128, 160, 256 or 512 tokens replay that bucket's graph."""
         with self._request():
             return self._engine.prefill(ids, start)
+
+    def full_step(self, ids, position: int):
+        """The text-phase step (``FastLLM.full_step``, ``src/moss_tts/_runtime/llm.py:321-325``): ``ids``
+        int64 ``[1, 1, 33]`` at cache row ``position`` -> the text logits ``[1, V]`` over the whole
+        text head (a view of the text graph's output buffer, valid until the next text step)."""
+        with self._request():
+            return self._engine.full_step(ids, position)
 
     def step(self, ids, position: int):
         """One batch-1 decode step: ``ids`` int64 ``[1, 33]`` (text token, 32 codebook codes) at

@@ -111,3 +111,71 @@ def write_export(folder, weights, *, n_layers, revision=None, complete=True, rec
     assert n_layers * 4 == len(weights)
     (folder / "config.json").write_text(json.dumps(config))
     return out
+
+
+def moss_model(dev, seed=0, *, text_vocab=512, token_ids=(100, 101, 102)):
+    """A one-layer, full-width MOSS-TTS-shaped model built from transformers' own Qwen3 modules
+    (hidden 4096, 32 query / 8 KV heads of 128, MLP 12288), with the reference's module names:
+    ``language_model``, 32 audio embeddings ``emb_ext`` and ``lm_heads`` (the text head of
+    ``text_vocab`` rows, then 32 codebook heads of 1025 rows).  Weights N(0, 0.02), norm weights
+    1 + N(0, 0.01), text embeddings N(0, 1).  ``token_ids``: gen slot, delay slot and audio end ids,
+    which must lie inside the text head."""
+    from types import SimpleNamespace
+
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3Model
+
+    cfg = Qwen3Config(hidden_size=4096, intermediate_size=12288, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, num_hidden_layers=1, vocab_size=text_vocab, rms_norm_eps=1e-6, rope_theta=1e6)
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        lm = Qwen3Model(cfg).bfloat16()
+        for p in lm.parameters():
+            torch.nn.init.normal_(p, 0.0, 0.02)
+        for norm in (lm.norm, lm.layers[0].input_layernorm, lm.layers[0].post_attention_layernorm,
+                     lm.layers[0].self_attn.q_norm, lm.layers[0].self_attn.k_norm):
+            norm.weight.data = (1 + 0.01 * torch.randn_like(norm.weight.float())).bfloat16()
+        lm.embed_tokens.weight.data.normal_(0, 1)
+        model = torch.nn.Module()
+        model.language_model = lm
+        model.emb_ext = torch.nn.ModuleList(torch.nn.Embedding(1025, 4096).bfloat16() for _ in range(32))
+        model.lm_heads = torch.nn.ModuleList([torch.nn.Linear(4096, text_vocab, bias=False).bfloat16()] +
+                                             [torch.nn.Linear(4096, 1025, bias=False).bfloat16() for _ in range(32)])
+        for h in model.lm_heads:
+            torch.nn.init.normal_(h.weight, 0.0, 0.02)
+    gen, delay, end = token_ids
+    model.config = SimpleNamespace(language_config=cfg, audio_assistant_gen_slot_token_id=gen,
+                                   audio_assistant_delay_slot_token_id=delay, audio_end_token_id=end)
+    return model
+
+
+def export_model(model, folder):
+    """Export the one-layer model's projections in the reference's calibrated format (layer 0's files
+    linked for layers 1..35, which the public entry point checks for); returns the reference's
+    dequantization of each exported projection (bf16)."""
+    import os
+
+    layer = model.language_model.layers[0]
+    a, m = layer.self_attn, layer.mlp
+    weights = {
+        (0, "qkv"): torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]).float().cpu(),
+        (0, "out"): a.o_proj.weight.float().cpu(),
+        (0, "up"): torch.cat([m.gate_proj.weight, m.up_proj.weight]).float().cpu(),
+        (0, "down"): m.down_proj.weight.float().cpu(),
+    }
+    written = write_export(folder, weights, n_layers=1)
+    for i in range(1, 36):
+        for p in ("qkv", "out", "up", "down"):
+            os.symlink(folder / f"00_{p}.pt", folder / f"{i:02d}_{p}.pt")
+    return {name: o.dequantize_signed(*written[0, name]) for name in ("qkv", "out", "up", "down")}
+
+
+def model_layer_cpu(model, deq):
+    """The oracle's layer dict of the one-layer model: the exported projections' dequantization and
+    the model's own norm weights."""
+    layer = model.language_model.layers[0]
+    a = layer.self_attn
+    return dict(qkv=deq["qkv"], o=deq["out"], gate_up=deq["up"], down=deq["down"],
+                input_norm=layer.input_layernorm.weight.detach().cpu(),
+                post_norm=layer.post_attention_layernorm.weight.detach().cpu(),
+                q_norm=a.q_norm.weight.detach().cpu(), k_norm=a.k_norm.weight.detach().cpu())

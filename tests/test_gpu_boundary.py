@@ -8,62 +8,14 @@ own (rebound) MLP forward at M=1 (GEMV) and M=64 (GEMM) meets 1e-2 atol + 1e-2 r
 dequant-then-matmul; the captured decode step's logits are within 2e-2 relative L2 of the
 oracle's composed step (the same bound as the synthetic decode test), whose heads are the model's
 own bf16 head rows."""
-import os
-from types import SimpleNamespace
-
 import pytest
 import torch
 
-from helpers import _assert_close, write_export
+from helpers import _assert_close, export_model, model_layer_cpu, moss_model
 from oracle import decode as od
 from oracle import w4g32 as o
 
 pytestmark = pytest.mark.gpu
-
-
-def _model(dev, seed=0):
-    from transformers import Qwen3Config
-    from transformers.models.qwen3.modeling_qwen3 import Qwen3Model
-
-    cfg = Qwen3Config(hidden_size=4096, intermediate_size=12288, num_attention_heads=32, num_key_value_heads=8,
-                      head_dim=128, num_hidden_layers=1, vocab_size=512, rms_norm_eps=1e-6, rope_theta=1e6)
-    torch.manual_seed(seed)
-    with torch.device(dev):
-        lm = Qwen3Model(cfg).bfloat16()
-        for p in lm.parameters():
-            torch.nn.init.normal_(p, 0.0, 0.02)
-        for norm in (lm.norm, lm.layers[0].input_layernorm, lm.layers[0].post_attention_layernorm,
-                     lm.layers[0].self_attn.q_norm, lm.layers[0].self_attn.k_norm):
-            norm.weight.data = (1 + 0.01 * torch.randn_like(norm.weight.float())).bfloat16()
-        lm.embed_tokens.weight.data.normal_(0, 1)
-        model = torch.nn.Module()
-        model.language_model = lm
-        model.emb_ext = torch.nn.ModuleList(torch.nn.Embedding(1025, 4096).bfloat16() for _ in range(32))
-        model.lm_heads = torch.nn.ModuleList([torch.nn.Linear(4096, 512, bias=False).bfloat16()] +
-                                             [torch.nn.Linear(4096, 1025, bias=False).bfloat16() for _ in range(32)])
-        for h in model.lm_heads:
-            torch.nn.init.normal_(h.weight, 0.0, 0.02)
-    # the text head of this small model has 512 rows: special token ids inside it
-    model.config = SimpleNamespace(language_config=cfg, audio_assistant_gen_slot_token_id=100,
-                                   audio_assistant_delay_slot_token_id=101, audio_end_token_id=102)
-    return model
-
-
-def _export(model, folder):
-    layer = model.language_model.layers[0]
-    a, m = layer.self_attn, layer.mlp
-    weights = {
-        (0, "qkv"): torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]).float().cpu(),
-        (0, "out"): a.o_proj.weight.float().cpu(),
-        (0, "up"): torch.cat([m.gate_proj.weight, m.up_proj.weight]).float().cpu(),
-        (0, "down"): m.down_proj.weight.float().cpu(),
-    }
-    written = write_export(folder, weights, n_layers=1)
-    # the public entry point checks all 36 layers' files exist; the model has one layer
-    for i in range(1, 36):
-        for p in ("qkv", "out", "up", "down"):
-            os.symlink(folder / f"00_{p}.pt", folder / f"{i:02d}_{p}.pt")
-    return {name: o.dequantize_signed(*written[0, name]) for name in ("qkv", "out", "up", "down")}
 
 
 def test_from_pretrained_install_and_decode(dev, tmp_path):
@@ -73,8 +25,8 @@ def test_from_pretrained_install_and_decode(dev, tmp_path):
     from moss_tts._runtime.presets import install_gptq
 
     print("boundary: building the one-layer model", flush=True)
-    model = _model(dev)
-    deq = _export(model, tmp_path)
+    model = moss_model(dev)
+    deq = export_model(model, tmp_path)
     print("boundary: from_pretrained", flush=True)
     tts = MossTTS.from_pretrained(preset="gptq", calibration_path=tmp_path, device="cuda:0", model=model)
     layer = model.language_model.layers[0]
@@ -111,10 +63,7 @@ def test_from_pretrained_install_and_decode(dev, tmp_path):
     heads = torch.cat([h.weight[:1024] for h in model.lm_heads[1:]] +
                       [model.lm_heads[0].weight[[100, 101]]]).detach().cpu()
     assert isinstance(eng.heads, Bf16Linear) and torch.equal(eng.heads.weight.cpu(), heads)
-    L0 = dict(qkv=deq["qkv"], o=deq["out"], gate_up=deq["up"], down=deq["down"],
-              input_norm=layer.input_layernorm.weight.detach().cpu(),
-              post_norm=layer.post_attention_layernorm.weight.detach().cpu(),
-              q_norm=a.q_norm.weight.detach().cpu(), k_norm=a.k_norm.weight.detach().cpu())
+    L0 = model_layer_cpu(model, deq)
     ref = od.decode_step([L0], model.language_model.norm.weight.detach().cpu(), heads,
                          eng.text_embedding.detach().cpu(), eng.audio_embedding.detach().cpu(), ids, position,
                          keys0, values0, eng.cos.cpu(), eng.sin.cpu()).float()

@@ -295,11 +295,11 @@ def test_gemm_parity(dev, m, k, n):
 def test_gemm_silu_equals_gemm_then_silu(dev, m, k, n, fused):
     """The gate||up GEMM with the SiLU*mul epilogue equals the GEMM of all 2 N rows followed by
     silu_mul, bit for bit: fused in the 128-token tile (M > 64 with no K split in the plan) and
-    through the workspace otherwise (64 tokens or fewer, or few enough tiles that K is split)."""
+    through the workspace otherwise (64 tokens or fewer, or few enough tiles that K is split).  The
+    fused tile is the one that runs without any workspace; the other shapes refuse that call."""
     from moss_tts._runtime import native, pointwise, w4g32
 
     print(f"gemm_silu M={m} K={k} N={n} fused={fused}", flush=True)
-    assert (native.lib().moss_gemm_silu_workspace_bytes(m, k, n) == 0) == fused
     g = torch.Generator(device=dev).manual_seed(m + k + n)
     pw = w4g32.quantize_minmax(torch.randn((2 * n, k), device=dev, generator=g) * 0.02)
     x = torch.randn((m, k), device=dev, generator=g).bfloat16()
@@ -307,6 +307,13 @@ def test_gemm_silu_equals_gemm_then_silu(dev, m, k, n, fused):
     got = w4g32.gemm_silu(x, pw)
     assert got.shape == (m, n)
     assert torch.equal(got, want)
+    bare = torch.full_like(got, float("nan"))
+    rc = native.lib().moss_w4g32_gemm_silu(native.ptr(x), native.ptr(pw.qw), native.ptr(pw.scales),
+                                           native.ptr(pw.zeros), native.ptr(bare), m, k, n, None, 0,
+                                           native.stream_of(x))
+    assert (rc == 0) == fused and (rc == 0 or rc == 1)
+    if fused:
+        assert torch.equal(bare, want)
 
 
 @pytest.mark.parametrize("m,fused", [(512, True), (600, True), (257, True), (128, False), (37, False), (2, False)])
@@ -317,7 +324,6 @@ def test_gemm_qk_rope_equals_gemm_then_qk_rope(dev, m, fused):
     from moss_tts._runtime import native, pointwise, w4g32
 
     print(f"gemm + qk rope M={m} fused={fused}", flush=True)
-    assert (native.lib().moss_gemm_qk_rope_workspace_bytes(m, 4096) == 0) == fused
     g = torch.Generator(device=dev).manual_seed(m)
     L = 1024
     w = w4g32.quantize_minmax(torch.randn((6144, 4096), device=dev, generator=g) * 0.02)
@@ -340,6 +346,19 @@ def test_gemm_qk_rope_equals_gemm_then_qk_rope(dev, m, fused):
     untouched = torch.ones(L, dtype=torch.bool, device=dev)
     untouched[pos.clamp(0, L - 1)] = False
     assert torch.equal(k1[:, :, untouched].view(torch.int16), base_k[:, :, untouched].view(torch.int16))
+    # the fused tile is the form that runs without any workspace; the other shapes refuse that call
+    k3, v3 = base_k.clone(), base_v.clone()
+    q3 = torch.empty((m, 32, 128), device=dev, dtype=torch.bfloat16)
+    lib = native.lib()
+    rc = lib.moss_w4g32_gemm_qk_rope(native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
+                                     native.ptr(qn), native.ptr(kn), native.ptr(cos), native.ptr(sin), native.ptr(q3),
+                                     native.ptr(k3), native.ptr(v3), native.ptr(pos), m, 4096, L, 1e-6, None, 0,
+                                     native.stream_of(x))
+    assert (rc == 0) == fused and (rc == 0 or rc == 1)
+    if fused:
+        torch.cuda.synchronize()
+        assert torch.equal(q3.view(torch.int16), q2.transpose(1, 2).contiguous().view(m, 32, 128).view(torch.int16))
+        assert torch.equal(k3.view(torch.int16), k2.view(torch.int16))
 
 
 @pytest.mark.parametrize("m,k,n", [(512, 4096, 4096), (512, 12288, 4096), (1024, 4096, 4096), (64, 4096, 4096),

@@ -2,9 +2,10 @@
 a caller workspace (``moss_w4g32_gemm``), through the C-ABI.
 
 Both take the same plan (the scratch array holds every plan's partials), so the outputs must be equal
-bit for bit.  Two calls in a row, the second smaller, show that the scratch contents left by the first
-call do not leak into the second; a shape with no K split runs too, and the Python wrapper gives the
-same result into a caller-owned output."""
+bit for bit.  Two K-split calls in a row, the second smaller (4 MiB of partials against the first's
+16 MiB, written over the first call's), show that the scratch contents left by one call do not leak
+into the next; a shape with no K split runs too, and the Python wrapper gives the same result into a
+caller-owned output."""
 import ctypes
 
 import pytest
@@ -26,10 +27,10 @@ def test_gemm_noalloc_matches_workspace_entry(dev):
 
     fn = _fn()
     g = torch.Generator(device=dev).manual_seed(31)
-    for m, k, n in ((512, 12288, 4096), (16, 4096, 4096), (512, 4096, 24576)):
+    for (m, k, n), split in (((512, 12288, 4096), True), ((64, 4096, 4096), True), ((512, 4096, 24576), False)):
         print(f"gemm noalloc M={m} K={k} N={n}", flush=True)
         need = native.lib().moss_gemm_workspace_bytes(m, k, n)
-        assert need <= SCRATCH
+        assert need <= SCRATCH and (need > 0) == split
         pw = w4g32.quantize_minmax((torch.randn((n, k), device=dev, generator=g) * 0.02).contiguous())
         x = torch.randn((m, k), device=dev, generator=g).bfloat16()
         ref = w4g32.gemm(x, pw)
