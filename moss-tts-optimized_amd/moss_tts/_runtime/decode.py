@@ -151,8 +151,7 @@ class DecodeStepG32:
         """The embedding sum and every layer from the static ``ids``/``position`` buffers -> the last
         layer's MLP output and the residual stream (bf16 ``[1, 4096]`` each), before the final norm."""
         if self.w4a8:
-            _require(trace is None, "trace is available in the W4A16 step")
-            return self._layers_w4a8()
+            return self._layers_w4a8(trace)
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
@@ -221,12 +220,13 @@ class DecodeStepG32:
                                   self.delay_length, delay_slot_id=int(self.text_ids_host[1]),
                                   audio_end_id=self.audio_end_id, out=self.next_ids)
 
-    def _layers_w4a8(self) -> tuple[torch.Tensor, torch.Tensor]:
+    def _layers_w4a8(self, trace: list | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         eps = self.eps
         x = attention.embedding_sum(self.ids, self.text_embedding, self.audio_embedding).view(1, HIDDEN)
         residual = x
         mlp = None
         for i, layer in enumerate(self.layers):
+            state = (residual.clone(), None if mlp is None else mlp.clone()) if trace is not None else None
             # add-RMSNorm + quantizer + q||k||v in one kernel, two rows per wave (fewer workgroups
             # repeat the normalization); measured faster than the separate norm_quant here
             if i == 0:
@@ -234,9 +234,9 @@ class DecodeStepG32:
             else:
                 residual, qkv = w4a8.norm_linear(mlp, layer.input_norm, eps, layer.qkv.packed, residual=residual,
                                                  rows_per_wave=2)
-            _, act = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
-                                                    self.keys[i], self.values[i], self.position, eps, ws=self.ws,
-                                                    quantize=True)
+            attn, act = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
+                                                       self.keys[i], self.values[i], self.position, eps, ws=self.ws,
+                                                       quantize=True)
             o = w4a8.linear(None, layer.o.packed, prequantized=act)
             # gate/up: the separate add-RMSNorm + quantizer is faster than the fused form here
             # (3072 workgroups would each repeat the normalization); the SiLU*mul output is
@@ -245,6 +245,9 @@ class DecodeStepG32:
             residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
             hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
+            if trace is not None:
+                trace.append(dict(residual_in=state[0], mlp_in=state[1], qkv=qkv.clone(), attn=attn.clone(),
+                                  o=o.clone(), act=hidden.clone(), mlp=mlp.clone(), residual=residual.clone()))
         return mlp, residual
 
     @torch.inference_mode()
@@ -340,7 +343,7 @@ class DecodeStepG32:
 
     # ------------------------------------------------------------------ prefill
     def _prefill_body(self, ids: torch.Tensor, positions: torch.Tensor, start: torch.Tensor,
-                      last: torch.Tensor) -> torch.Tensor:
+                      last: torch.Tensor, trace: list | None = None) -> torch.Tensor:
         """The prompt pass over ``n`` tokens (``src/moss_tts/_runtime/llm.py:204-207``; layer loop
         ``src/moss_tts/_runtime/prefill_pointwise.py:46-57``): embedding sum -> per layer the q||k||v
         GEMM -> q/k head-norm + RoPE with the K/V rows written at ``positions``
@@ -351,22 +354,36 @@ class DecodeStepG32:
         then the final add-RMSNorm + heads on it.
         ``ids`` int64 ``[n, 33]``, ``positions`` int64 ``[n]`` (= start + arange(n)), ``start`` and
         ``last`` int64 ``[1]``, all on the device.  Returns the head logits as ``forward`` does and,
-        when the step holds the text head, the text logits ``[1, V]`` (else None)."""
+        when the step holds the text head, the text logits ``[1, V]`` (else None).
+        ``trace`` (eager runs only): a list that receives, per layer, copies of the stream state it
+        starts from (``residual_in``, its normalized form ``state_in``) and of its outputs: the
+        RoPE'd queries ``q``, ``attn``, the residual and normalized state after the O projection
+        (``residual_mid``, ``state_mid``), ``act`` and the state after the MLP (``residual_out``,
+        ``state_out``, normalized with the next layer's input norm); the last layer's attention,
+        O and MLP outputs are the last token's, and it records ``mlp`` instead of the state after it."""
         n, eps = ids.shape[0], self.eps
         x = attention.embedding_sum(ids, self.text_embedding, self.audio_embedding)
         residual = x
         state = pointwise.rmsnorm(x, self.layers[0].input_norm, eps)
         qbuf = torch.empty((n, QH, HD), device=self.device, dtype=torch.bfloat16)
         for i, layer in enumerate(self.layers):
+            rec = dict(residual_in=residual.clone(), state_in=state.clone()) if trace is not None else None
             w4g32.gemm_qk_rope(state, layer.qkv.packed, layer.q_norm, layer.k_norm, self.cos, self.sin, self.keys[i],
                                self.values[i], positions, eps, out=qbuf)
+            if rec is not None:
+                rec["q"] = qbuf.clone()
+                trace.append(rec)
             if i + 1 == len(self.layers):
                 break
             attn = attention.prefill_attention(qbuf, self.keys[i], self.values[i], start)
             residual, state = w4g32.gemm_add_rmsnorm(attn, layer.o.packed, residual, layer.post_norm, eps)
             act = w4g32.gemm_silu(state, layer.gate_up.packed)
+            if rec is not None:
+                rec.update(attn=attn.clone(), residual_mid=residual.clone(), state_mid=state.clone(), act=act.clone())
             residual, state = w4g32.gemm_add_rmsnorm(act, layer.down.packed, residual, self.layers[i + 1].input_norm,
                                                      eps)
+            if rec is not None:
+                rec.update(residual_out=residual.clone(), state_out=state.clone())
         # Only the last token's hidden state reaches the logits, so after the last layer's K/V rows
         # are written for every token, its attention, O projection and MLP run for that token alone
         # (the decode step's kernels, exact dequant as the GEMMs): per-row math equal to the full
@@ -378,6 +395,9 @@ class DecodeStepG32:
         residual, act = w4g32.norm_gateup_silu(o, layer.post_norm, eps, layer.gate_up.packed,
                                                residual=residual.index_select(0, last))
         mlp = w4g32.gemv(act, layer.down.packed)
+        if trace is not None:
+            trace[-1].update(attn=attn.clone().view(1, HIDDEN), o=o.clone(), residual_mid=residual.clone(),
+                             act=act.clone(), mlp=mlp.clone())
         logits = self._heads(mlp, residual, CODEBOOKS)
         return logits, (self._text_logits(mlp, residual) if self.text_head is not None else None)
 

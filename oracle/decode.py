@@ -70,60 +70,81 @@ def reversed_linear(h: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(h.float().flip(-1), w.float().flip(-1))
 
 
-def decode_step_w4a8(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):
-    """The same step with the four layer projections in the W4A8 arithmetic
-    (``oracle.w4a8``; order ``src/moss_tts/_runtime/llm.py:29-56,71-92``): ``layers`` dicts hold
-    ``(q, z, s)`` code triples for ``qkv``, ``o``, ``gate_up``, ``down``; the heads stay
-    dequant-then-matmul on ``heads_w``."""
+def decode_layer_w4a8(L, i, residual, mlp, position, keys, values, cos, sin, eps=1e-6, reverse_f32=False):
+    """One layer of the step in the W4A8 arithmetic (``oracle.w4a8``; order
+    ``src/moss_tts/_runtime/llm.py:29-56,71-92``) from the stream state ``(residual, mlp)`` as in
+    ``decode_layer``: ``L`` holds ``(q, z, s)`` code triples for ``qkv``, ``o``, ``gate_up``,
+    ``down``.  Returns ``qkv, attn, o, act, mlp`` and the new ``residual``.  ``reverse_f32``: every
+    projection's group combine in float32 in reverse group order (``oracle.w4a8._combine``)."""
     p = int(position)
-    x = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
-    residual = x
-    h = op.rmsnorm(x, layers[0]["input_norm"], eps)
+    r = reverse_f32
+    if mlp is None:
+        h = op.rmsnorm(residual, L["input_norm"], eps)
+    else:
+        residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
+    qkv = o8.w4a8_linear(h.view(-1), *L["qkv"], reverse_f32=r)[0].view(1, -1)
+    q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],
+                           torch.tensor([p]), eps)
+    attn = oa.decode_attention(q, keys[i], values[i], p).bfloat16().view(1, -1)
+    o = o8.w4a8_linear(attn.view(-1), *L["o"], reverse_f32=r)[0].view(1, -1)
+    residual, h = op.add_rmsnorm(o, residual, L["post_norm"], eps)
+    n = L["gate_up"][0].shape[0] // 2
+    act = o8.w4a8_gateup_silu(h.view(-1), *L["gate_up"], n, reverse_f32=r)[0].view(1, -1)
+    mlp = o8.w4a8_linear(act.view(-1), *L["down"], reverse_f32=r)[0].view(1, -1)
+    return dict(qkv=qkv, attn=attn, o=o, act=act, mlp=mlp, residual=residual)
+
+
+def decode_step_w4a8(layers, final_norm, heads_w, text, audio, ids, position, keys, values, cos, sin, eps=1e-6):
+    """The same step with the four layer projections in the W4A8 arithmetic (``decode_layer_w4a8``);
+    the heads stay dequant-then-matmul on ``heads_w``.  ``layers`` is consumed once, in order."""
+    residual = oa.embedding_sum(ids.view(-1), text, audio).view(1, -1)
     mlp = None
     for i, L in enumerate(layers):
-        if i > 0:
-            residual, h = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
-        qkv = o8.w4a8_linear(h.view(-1), *L["qkv"])[0].view(1, -1)
-        q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[p:p + 1], sin[p:p + 1], keys[i], values[i],
-                               torch.tensor([p]), eps)
-        attn = oa.decode_attention(q, keys[i], values[i], p).bfloat16().view(-1)
-        o = o8.w4a8_linear(attn, *L["o"])[0].view(1, -1)
-        residual, h = op.add_rmsnorm(o, residual, L["post_norm"], eps)
-        n = L["gate_up"][0].shape[0] // 2
-        a = o8.w4a8_gateup_silu(h.view(-1), *L["gate_up"], n)[0]
-        mlp = o8.w4a8_linear(a, *L["down"])[0].view(1, -1)
+        out = decode_layer_w4a8(L, i, residual, mlp, position, keys, values, cos, sin, eps)
+        residual, mlp = out["residual"], out["mlp"]
     _, h = op.add_rmsnorm(mlp, residual, final_norm, eps)
     return ow.linear(h, heads_w).bfloat16().view(-1)
+
+
+def prefill_layer(L, i, residual, state, start, keys, values, cos, sin, eps=1e-6, linear=None):
+    """One layer of the prompt pass (layer loop ``src/moss_tts/_runtime/prefill_pointwise.py:46-57``)
+    from the stream state entering it: ``residual`` bf16 ``[n, 4096]`` and ``state``, its
+    normalization with the layer's input norm.  q||k||v -> q/k head-norm + RoPE, K/V rows written
+    at positions ``start .. start + n - 1`` of ``keys[i]``/``values[i]`` (``prefill_qkv.py:7-28``)
+    -> causal attention over cache rows ``0 .. position`` (``llm.py:116-128``) -> O -> add-RMSNorm
+    -> gate||up -> SiLU*mul -> down, all projections dequant-then-matmul rounded to bf16.  Returns
+    ``q`` (after RoPE), ``attn``, ``o``, ``residual_mid``, ``state_mid`` (after the O projection's
+    add-RMSNorm), ``act`` and ``mlp``."""
+    lin = linear or ow.linear
+    n = state.shape[0]
+    pos = torch.arange(int(start), int(start) + n)
+    qkv = lin(state, L["qkv"]).bfloat16()
+    q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[pos], sin[pos], keys[i], values[i], pos, eps)
+    attn = oa.prefill_attention(q, keys[i], values[i], int(start)).bfloat16().view(n, -1)
+    o = lin(attn, L["o"]).bfloat16()
+    residual_mid, state_mid = op.add_rmsnorm(o, residual, L["post_norm"], eps)
+    y = lin(state_mid, L["gate_up"])
+    h = y.shape[1] // 2
+    act = ow.silu_mul_rounded(y[:, :h], y[:, h:])
+    mlp = lin(act, L["down"]).bfloat16()
+    return dict(q=q, attn=attn, o=o, residual_mid=residual_mid, state_mid=state_mid, act=act, mlp=mlp)
 
 
 def prefill(layers, final_norm, heads_w, text, audio, ids, start, keys, values, cos, sin, eps=1e-6,
             linear=None):
     """The prompt pass (``src/moss_tts/_runtime/llm.py:204-207``, layer loop
     ``src/moss_tts/_runtime/prefill_pointwise.py:46-57``): ``ids [n, 33]`` at absolute positions
-    ``start .. start + n - 1``; per layer q||k||v -> q/k head-norm + RoPE, K/V rows written at the
-    positions (``prefill_qkv.py:7-28``) -> causal attention over cache rows ``0 .. position``
-    (``llm.py:116-128``) -> O -> add-RMSNorm -> gate||up -> SiLU*mul -> down -> add-RMSNorm, all
-    projections dequant-then-matmul rounded to bf16.  ``layers`` is consumed once, in order.  Returns
-    the bf16 logits of the last token through the final norm and the heads (``llm.py:206-207``)."""
-    lin = linear or ow.linear
-    n = ids.shape[0]
-    pos = torch.arange(int(start), int(start) + n)
+    ``start .. start + n - 1``; per layer ``prefill_layer``, the next layer's input norm applied to
+    the residual sum ``mlp + residual``.  ``layers`` is consumed once, in order.  Returns the bf16
+    logits of the last token through the final norm and the heads (``llm.py:206-207``)."""
     x = oa.embedding_sum(ids, text, audio)
-    residual, state = x, None
-    mlp = None
+    residual, mlp = x, None
     for i, L in enumerate(layers):
         if i == 0:
             state = op.rmsnorm(x, L["input_norm"], eps)
         else:
             residual, state = op.add_rmsnorm(mlp, residual, L["input_norm"], eps)
-        qkv = lin(state, L["qkv"]).bfloat16()
-        q = op.qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], cos[pos], sin[pos], keys[i], values[i], pos, eps)
-        attn = oa.prefill_attention(q, keys[i], values[i], int(start)).bfloat16().view(n, -1)
-        o = lin(attn, L["o"]).bfloat16()
-        residual, state = op.add_rmsnorm(o, residual, L["post_norm"], eps)
-        y = lin(state, L["gate_up"])
-        h = y.shape[1] // 2
-        act = ow.silu_mul_rounded(y[:, :h], y[:, h:])
-        mlp = lin(act, L["down"]).bfloat16()
+        out = prefill_layer(L, i, residual, state, start, keys, values, cos, sin, eps, linear)
+        residual, mlp = out["residual_mid"], out["mlp"]
     _, h = op.add_rmsnorm(mlp[-1:], residual[-1:], final_norm, eps)
-    return lin(h, heads_w).bfloat16().view(-1)
+    return (linear or ow.linear)(h, heads_w).bfloat16().view(-1)

@@ -80,36 +80,53 @@ def from_dot4_order(b: np.ndarray) -> np.ndarray:
 
 
 def group_isums(q_w: torch.Tensor, z: torch.Tensor, qx: np.ndarray) -> np.ndarray:
-    """isum[n, g] = sum_{k in g} (q_w[n, k] - z[n, g]) * qx[k], int64 [N, G] (exact)."""
-    w = q_w.cpu().numpy().astype(np.int64) - np.repeat(z.cpu().numpy().astype(np.int64), GROUP, axis=1)
+    """isum[n, g] = sum_{k in g} (q_w[n, k] - z[n, g]) * qx[k], int64 [N, G] (exact).
+
+    Computed as sum_k q_w qx - z sum_k qx, the first term as a float32 contraction: codes are at
+    most 15 and |qx| at most 127, so every product and every partial sum of a group's 32 products is
+    an integer below 2^24, which float32 holds exactly in any summation order."""
+    w = q_w.cpu()
     n, k = w.shape
-    prod = w * np.asarray(qx).astype(np.int64)[None, :]
-    return prod.reshape(n, k // GROUP, GROUP).sum(-1)
+    g = k // GROUP
+    xq = torch.from_numpy(np.asarray(qx).astype(np.float32)).view(g, GROUP)
+    s1 = torch.einsum("ngt,gt->ng", w.to(torch.float32).view(n, g, GROUP), xq).to(torch.int64).numpy()
+    return s1 - z.cpu().numpy().astype(np.int64) * code_sums(qx).astype(np.int64)[None, :]
+
+
+def _combine(isum: np.ndarray, sx: np.ndarray, s, reverse_f32: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    """(sum_g f32(isum) * f32(f32(s) * sx) in float64, sum of the terms' magnitudes).  With
+    ``reverse_f32`` the terms are added in float32 from the last group to the first: another fp32
+    order the reference's unrestated reduction could have used, for measuring how far summation
+    order alone moves a composed result."""
+    terms = (isum.astype(np.float32).astype(np.float64) *
+             (s.cpu().float().numpy() * np.asarray(sx, dtype=np.float32)[None, :]).astype(np.float32)
+             .astype(np.float64))
+    if reverse_f32:
+        t32 = terms.astype(np.float32)[:, ::-1]
+        acc = np.zeros(t32.shape[0], dtype=np.float32)
+        for gi in range(t32.shape[1]):
+            acc = (acc + t32[:, gi]).astype(np.float32)
+        return acc.astype(np.float64), np.abs(terms).sum(-1)
+    return terms.sum(-1), np.abs(terms).sum(-1)
 
 
 def w4a8_f64(qx: np.ndarray, sx: np.ndarray, q_w, z, s) -> np.ndarray:
     """Pre-rounding output in float64: sum_g f32(isum) * f32(f32(s) * sx) (``dp4a_scaled.py:53-57``)."""
-    isum = group_isums(q_w, z, qx).astype(np.float32).astype(np.float64)
-    sw = s.cpu().float().numpy()
-    prod = (sw * np.asarray(sx, dtype=np.float32)[None, :]).astype(np.float32).astype(np.float64)
-    return (isum * prod).sum(-1)
+    return _combine(group_isums(q_w, z, qx), sx, s)[0]
 
 
-def w4a8_linear(x: torch.Tensor, q_w, z, s) -> tuple[torch.Tensor, np.ndarray, np.ndarray]:
+def w4a8_linear(x: torch.Tensor, q_w, z, s, reverse_f32: bool = False) -> tuple[torch.Tensor, np.ndarray, np.ndarray]:
     """bf16 x [K] -> (y bf16 [N], the float64 pre-rounding sums, per-row sum of |terms|)."""
     qx, sx = quantize_g32(x)
-    y64 = w4a8_f64(qx, sx, q_w, z, s)
-    isum = group_isums(q_w, z, qx).astype(np.float64)
-    prod = (s.cpu().float().numpy() * sx[None, :]).astype(np.float32).astype(np.float64)
-    mag = np.abs(isum * prod).sum(-1)
+    y64, mag = _combine(group_isums(q_w, z, qx), sx, s, reverse_f32)
     y = bits_to_bf16(f32_to_bf16_bits(y64.astype(np.float32)))
     return y, y64, mag
 
 
-def w4a8_gateup_silu(x: torch.Tensor, q_w, z, s, n_half: int):
+def w4a8_gateup_silu(x: torch.Tensor, q_w, z, s, n_half: int, reverse_f32: bool = False):
     """Paired form (``dp4a_scaled.py:64-68``): returns (y bf16 [n_half], gate64, up64)."""
     qx, sx = quantize_g32(x)
-    y64 = w4a8_f64(qx, sx, q_w, z, s)
+    y64 = _combine(group_isums(q_w, z, qx), sx, s, reverse_f32)[0]
     gate64, up64 = y64[:n_half], y64[n_half:]
     g = torch.from_numpy(gate64.astype(np.float32))
     u = torch.from_numpy(up64.astype(np.float32))

@@ -200,3 +200,88 @@ def test_decode_step_w4a8_two_layers(dev):
     replay = eng.step(ids, position).clone()
     torch.cuda.synchronize()
     assert torch.equal(eager, replay)
+
+
+def test_decode_step_w4a8_full_size(dev):
+    """The benchmarked W4A8 step itself: 36 layers, KV capacity 2048 filled with N(0,1), the token at
+    position 2047, run as the captured graph, against the oracle in the same arithmetic
+    (``oracle.decode.decode_layer_w4a8``: int8 activations per group of 32, exact integer group sums,
+    the fp32 group combine).
+
+    * The graph's logits and K/V rows equal an eager run of the same step bit for bit.
+    * Layer by layer (teacher forcing from the GPU's own stream state): q||k||v, attention, O,
+      SiLU*mul, down and the residual within relative L2 1e-2 of the oracle's, the K/V row too, and
+      the heads' logits from the GPU's final state.
+    * End to end: the free-running GPU logits within max(2e-2, 1.5x the oracle's distance to itself
+      with every group combine summed in float32 in reverse group order), a bar that must stay at or
+      below 5e-2."""
+    import time
+
+    from moss_tts._runtime.decode import DecodeStepG32
+    from oracle import pointwise as op
+
+    print("decode step w4a8: 36 layers, L=2048, p=2047 (graph replay)", flush=True)
+    L, position, n_layers = 2048, 2047, 36
+    eng = DecodeStepG32.random(n_layers, max_length=L, device=dev, seed=4242, w4a8=True)
+    eng.capture()
+    keys0 = [k.cpu() for k in eng.keys]
+    values0 = [v.cpu() for v in eng.values]
+    ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
+    logits = eng.step(ids, position).float().cpu()
+    kv_graph = [(eng.keys[i][:, :, position].cpu(), eng.values[i][:, :, position].cpu()) for i in range(n_layers)]
+    trace = []
+    with torch.inference_mode():
+        eager = eng.forward(trace=trace).float().cpu()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, logits), "graph replay differs from the eager step"
+    for i in range(n_layers):
+        assert torch.equal(eng.keys[i][:, :, position].cpu(), kv_graph[i][0])
+        assert torch.equal(eng.values[i][:, :, position].cpu(), kv_graph[i][1])
+    print("GPU step done; oracle layer by layer", flush=True)
+
+    def rel(a, b):
+        a, b = a.float().flatten(), b.float().flatten()
+        return float((a - b).norm() / b.norm())
+
+    cos, sin, eps = eng.cos.cpu(), eng.sin.cpu(), eng.eps
+    caches = {m: ([k.clone() for k in keys0], [v.clone() for v in values0]) for m in ("tf", "free", "rev")}
+    x0 = oa.embedding_sum(ids.view(-1), eng.text_embedding.cpu(), eng.audio_embedding.cpu()).view(1, -1)
+    assert torch.equal(trace[0]["residual_in"].cpu(), x0)
+    state = {"free": (x0, None), "rev": (x0, None)}
+    worst, t0 = 0.0, time.time()
+    for i, l in enumerate(eng.layers):
+        lw = dict(qkv=_codes_cpu(l.qkv.packed), o=_codes_cpu(l.o.packed), gate_up=_codes_cpu(l.gate_up.packed),
+                  down=_codes_cpu(l.down.packed), input_norm=l.input_norm.cpu(), post_norm=l.post_norm.cpu(),
+                  q_norm=l.q_norm.cpu(), k_norm=l.k_norm.cpu())
+        t = trace[i]
+        mlp_in = None if t["mlp_in"] is None else t["mlp_in"].cpu()
+        ref = od.decode_layer_w4a8(lw, i, t["residual_in"].cpu(), mlp_in, position, *caches["tf"], cos, sin, eps)
+        for key in ("qkv", "attn", "o", "act", "mlp", "residual"):
+            err = rel(t[key].cpu(), ref[key])
+            worst = max(worst, err)
+            assert err < 1e-2, f"layer {i} {key}: relative L2 {err:.3e}"
+        for got, want in ((kv_graph[i][0], caches["tf"][0][i]), (kv_graph[i][1], caches["tf"][1][i])):
+            err = rel(got, want[:, :, position])
+            assert err < 1e-2, f"layer {i} KV row: relative L2 {err:.3e}"
+        for mode, rev in (("free", False), ("rev", True)):
+            out = od.decode_layer_w4a8(lw, i, *state[mode], position, *caches[mode], cos, sin, eps, reverse_f32=rev)
+            state[mode] = (out["residual"], out["mlp"])
+        if i % 6 == 5:
+            print(f"  oracle layer {i + 1}/{n_layers} ({time.time() - t0:.1f} s); worst layer error {worst:.2e}",
+                  flush=True)
+    heads_w = _dequant_cpu(eng.heads)
+    final = eng.final_norm.cpu()
+
+    def head(res, mlp):
+        _, h = op.add_rmsnorm(mlp, res, final, eps)
+        return o.linear(h, heads_w).bfloat16().float().view(-1)
+
+    err = rel(logits, head(trace[-1]["residual"].cpu(), trace[-1]["mlp"].cpu()))
+    print(f"heads from the GPU's final state: relative L2 {err:.3e}", flush=True)
+    assert err < 1e-2
+    free, rev = head(*state["free"]), head(*state["rev"])
+    e2e, self_dist = rel(logits, free), rel(rev, free)
+    bar = max(2e-2, 1.5 * self_dist)
+    print(f"end to end: GPU vs oracle {e2e:.3e}; oracle vs reversed-order oracle {self_dist:.3e}; bar {bar:.3e}; "
+          f"worst layer error {worst:.3e}", flush=True)
+    assert e2e < bar and bar <= 5e-2

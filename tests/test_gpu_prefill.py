@@ -135,3 +135,112 @@ def test_prefill_graph_equals_eager(dev):
     assert torch.equal(eng.keys[0][:, :, :128], k_e)
     with pytest.raises(ValueError, match="KV capacity"):
         eng.prefill(ids, start=400)
+
+
+def test_prefill_full_depth(dev):
+    """The benchmarked prompt pass at full depth: 36 layers, a 128-token prompt through its bucket
+    graph (KV capacity 1024).
+
+    * The graph's logits and K/V rows equal an eager run of the same pass bit for bit.
+    * Layer by layer (teacher forcing): each oracle layer (``oracle.decode.prefill_layer``) starts from
+      the GPU's own stream state entering that layer (the residual sum and its normalization, whose
+      normalization is checked too); the RoPE'd queries, attention, the state after the O projection,
+      SiLU*mul, the state after the MLP (normalized with the next layer's input norm) and every K/V
+      row written are within relative L2 1e-2 of the GPU's; the last layer's attention, O and MLP,
+      which run for the last token alone, against the oracle's last row; then the heads' logits from
+      the GPU's final state.
+    * End to end: the free-running GPU logits within max(2e-2, 1.5x the oracle's distance to itself
+      with every product's K axis summed in reverse) of the free-running oracle, as for the decode
+      step; the bar must stay at or below 5e-2."""
+    import time
+
+    from moss_tts._runtime.decode import DecodeStepG32
+    from oracle import pointwise as op
+
+    n, L, n_layers = 128, 1024, 36
+    print(f"prefill full depth: {n_layers} layers, {n} tokens (bucket graph)", flush=True)
+    eng = DecodeStepG32.random(n_layers, max_length=L, device=dev, seed=77)
+    eng.capture_prefill((n,))
+    keys0 = [k.cpu() for k in eng.keys]
+    values0 = [v.cpu() for v in eng.values]
+    g = torch.Generator().manual_seed(3)
+    ids = torch.cat([torch.randint(0, 151643, (n, 1), generator=g), torch.randint(0, 1024, (n, 32), generator=g)], 1)
+    logits = eng.prefill(ids).float().cpu()
+    assert eng.last_prefill_bucket == n
+    kv_graph = [(eng.keys[i][:, :, :n].cpu(), eng.values[i][:, :, :n].cpu()) for i in range(n_layers)]
+    trace = []
+    with torch.inference_mode():
+        eager = eng._prefill_body(*eng._prefill_inputs(ids.to(dev), 0, n), trace=trace)[0].float().cpu()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, logits), "graph replay differs from the eager pass"
+    for i in range(n_layers):
+        assert torch.equal(eng.keys[i][:, :, :n].cpu(), kv_graph[i][0])
+        assert torch.equal(eng.values[i][:, :, :n].cpu(), kv_graph[i][1])
+    print("GPU pass done; oracle layer by layer", flush=True)
+
+    bufs = {}
+
+    def deq(name, m):
+        if name not in bufs:
+            bufs[name] = torch.empty(m.N * m.K)
+        return o.dequantize_rowpack_f32(m.qw.cpu(), m.scales.cpu(), m.zeros.cpu(), out=bufs[name])
+
+    cos, sin, eps = eng.cos.cpu(), eng.sin.cpu(), eng.eps
+    caches = {m: ([k.clone() for k in keys0], [v.clone() for v in values0]) for m in ("tf", "free", "rev")}
+    x0 = oa.embedding_sum(ids, eng.text_embedding.cpu(), eng.audio_embedding.cpu())
+    assert torch.equal(trace[0]["residual_in"].cpu(), x0)
+    state = {m: (x0, None) for m in ("free", "rev")}
+    worst, t0 = 0.0, time.time()
+
+    def check(key, got, want, i):
+        nonlocal worst
+        err = _rel(got, want)
+        worst = max(worst, err)
+        assert err < 1e-2, f"layer {i} {key}: relative L2 {err:.3e}"
+
+    for i, l in enumerate(eng.layers):
+        lw = dict(qkv=deq("qkv", l.qkv.packed), o=deq("o", l.o.packed), gate_up=deq("gate_up", l.gate_up.packed),
+                  down=deq("down", l.down.packed), input_norm=l.input_norm.cpu(), post_norm=l.post_norm.cpu(),
+                  q_norm=l.q_norm.cpu(), k_norm=l.k_norm.cpu())
+        t = {k: v.cpu() for k, v in trace[i].items()}
+        check("state_in", t["state_in"], op.rmsnorm(t["residual_in"], lw["input_norm"], eps), i)
+        ref = od.prefill_layer(lw, i, t["residual_in"], t["state_in"], 0, *caches["tf"], cos, sin, eps)
+        check("q", t["q"], ref["q"].reshape(n, -1), i)
+        for kv in (0, 1):
+            check("K/V rows", kv_graph[i][kv], caches["tf"][kv][i][:, :, :n], i)
+        last = i + 1 == n_layers
+        rows = slice(n - 1, n) if last else slice(0, n)
+        for key in ("attn", "residual_mid", "act") + (("o", "mlp") if last else ("state_mid",)):
+            check(key, t[key], ref[key][rows], i)
+        if not last:
+            res_out, st_out = op.add_rmsnorm(ref["mlp"], ref["residual_mid"], eng.layers[i + 1].input_norm.cpu(), eps)
+            check("residual_out", t["residual_out"], res_out, i)
+            check("state_out", t["state_out"], st_out, i)
+        for mode, lin in (("free", None), ("rev", od.reversed_linear)):
+            res, mlp = state[mode]
+            if mlp is None:
+                st = op.rmsnorm(res, lw["input_norm"], eps)
+            else:
+                res, st = op.add_rmsnorm(mlp, res, lw["input_norm"], eps)
+            out = od.prefill_layer(lw, i, res, st, 0, *caches[mode], cos, sin, eps, lin)
+            state[mode] = (out["residual_mid"], out["mlp"])
+        if i % 6 == 5:
+            print(f"  oracle layer {i + 1}/{n_layers} ({time.time() - t0:.1f} s); worst layer error {worst:.2e}",
+                  flush=True)
+    heads_w = deq("heads", eng.heads.packed)
+    final = eng.final_norm.cpu()
+
+    def head(res, mlp, lin=o.linear):
+        _, h = op.add_rmsnorm(mlp[-1:], res[-1:], final, eps)
+        return lin(h, heads_w).bfloat16().float().view(-1)
+
+    err = _rel(logits, head(trace[-1]["residual_mid"].cpu(), trace[-1]["mlp"].cpu()))
+    print(f"heads from the GPU's final state: relative L2 {err:.3e}", flush=True)
+    assert err < 1e-2
+    free = head(*state["free"])
+    rev = head(*state["rev"], od.reversed_linear)
+    e2e, self_dist = _rel(logits, free), _rel(rev, free)
+    bar = max(2e-2, 1.5 * self_dist)
+    print(f"end to end: GPU vs oracle {e2e:.3e}; oracle vs reversed-order oracle {self_dist:.3e}; bar {bar:.3e}; "
+          f"worst layer error {worst:.3e}", flush=True)
+    assert e2e < bar and bar <= 5e-2
