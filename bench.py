@@ -503,6 +503,79 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False)
     return out
 
 
+def decode_budget(torch, n_layers: int, steps: int, dev) -> dict:
+    """Per-kernel budget of the W4A16 decode step measured inside the step itself, untraced: for each
+    kernel family, a graph of the step in which every launch of that family runs twice (the
+    launches are idempotent: same inputs, same outputs) is timed against the plain step graph; the
+    difference is what that family's launches cost in the step, dispatch gaps included.  The
+    families' costs sum to about the step time, unlike traced kernel durations."""
+    import contextlib
+
+    from moss_tts._runtime import attention, sampling, w4g32
+    from moss_tts._runtime.decode import DecodeStepG32
+
+    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
+    ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
+
+    def time_step() -> float:
+        eng.graph = None
+        eng.capture()
+        eng.step(ids, 2047)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            eng.graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps * 1e3
+
+    @contextlib.contextmanager
+    def doubled(module, name, pick):
+        orig = getattr(module, name)
+
+        def twice(*a, **kw):
+            if pick(*a, **kw):
+                orig(*a, **kw)
+            return orig(*a, **kw)
+
+        setattr(module, name, twice)
+        try:
+            yield
+        finally:
+            setattr(module, name, orig)
+
+    def width(a, kw):
+        return a[3].N if len(a) > 3 else kw["w"].N
+
+    families = [
+        ("embedding sum", attention, "embedding_sum", lambda *a, **kw: True, 1),
+        ("add-RMSNorm + q||k||v GEMV", w4g32, "norm_gemv", lambda *a, **kw: width(a, kw) == 6144, n_layers),
+        ("q/k-norm + RoPE + KV write + attention split + merge", attention, "decode_attention_qkv",
+         lambda *a, **kw: True, n_layers),
+        ("O GEMV (K=4096)", w4g32, "gemv", lambda *a, **kw: a[1].K == 4096, n_layers),
+        ("add-RMSNorm + gate||up GEMV + SiLU*mul", w4g32, "norm_gateup_silu", lambda *a, **kw: True, n_layers),
+        ("down GEMV (K=12288)", w4g32, "gemv", lambda *a, **kw: a[1].K == 12288, n_layers),
+        ("final add-RMSNorm + heads GEMV", w4g32, "norm_gemv", lambda *a, **kw: width(a, kw) > 6144, 1),
+        ("sampling (text and audio rows)", sampling, "sample_topk_pair", lambda *a, **kw: True, 1),
+        ("next-id composition", sampling, "compose_next_ids", lambda *a, **kw: True, 1),
+    ]
+    base = [time_step() for _ in range(3)]
+    base_us = sorted(base)[1]
+    rows, total = [], 0.0
+    for label, module, name, pick, count in families:
+        with doubled(module, name, pick):
+            t = sorted(time_step() for _ in range(3))[1]
+        cost = t - base_us
+        total += cost
+        rows.append({"kernels": label, "launches_per_step": count, "us_per_step": round(cost, 1),
+                     "us_per_launch": round(cost / count, 3)})
+        _log(f"[bench] budget: {label}: {cost:.1f} us per step ({cost / count:.2f} us x {count})")
+    _log(f"[bench] budget: step {base_us:.1f} us; sum of the families {total:.1f} us")
+    return {"step_us": round(base_us, 1), "sum_of_families_us": round(total, 1), "families": rows,
+            "method": "each family's launches doubled inside the captured step; cost = step time difference"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -517,6 +590,8 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="skip the FP8 and prefill GEMM lines")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the 36-layer decode step (both arithmetics) and its lines, for a kernel trace")
+    ap.add_argument("--decode-budget", action="store_true",
+                    help="per-kernel budget of the 36-layer W4A16 decode step, measured inside the untraced step")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 36-layer prompt pass (10 graph replays), for a kernel trace")
     ap.add_argument("--prefill-tokens", type=int, choices=(128, 256, 512), default=512,
@@ -547,6 +622,10 @@ def main() -> int:
         _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); {args.prefill_tokens}-token prompt pass only")
         prefill_pass_bench(torch, args.decode_layers, dev, n=args.prefill_tokens)
         return 0
+    if args.decode_budget:
+        _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode-step budget")
+        print(json.dumps(decode_budget(torch, args.decode_layers, max(1, args.decode_steps), dev)), flush=True)
+        return 0
     if args.decode_only:
         _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode step only")
         for w8 in (False, True):
@@ -565,16 +644,53 @@ def main() -> int:
     _log(f"[bench] {resident / 2**20:.0f} MiB of packed MLP weights resident")
 
     if args.pmc_pass == "gemm":
+        # the four M=512 prefill GEMMs plain, then in the fused forms the prompt pass runs (QKV with
+        # the q/k-norm + RoPE + KV write, gate||up with SiLU*mul, O and down with the add-RMSNorm),
+        # then the e4m3 M=64 linears (K=4096, N=4096 and 12288; split-K GEMM + reduction)
+        from moss_tts._runtime import fp8
+
         del copies
         torch.cuda.empty_cache()
         x = torch.randn((512, INTER), generator=gen, device=dev).bfloat16()
-        for k, n in ((HIDDEN, 6144), (HIDDEN, HIDDEN), (HIDDEN, 2 * INTER), (INTER, HIDDEN)):
+        ws = {}
+        for name, k, n in (("qkv", HIDDEN, 6144), ("o", HIDDEN, HIDDEN), ("gate_up", HIDDEN, 2 * INTER),
+                           ("down", INTER, HIDDEN)):
             pw = _quantized(torch, w4g32, n, k, gen, dev)
-            xk = x[:, :k].contiguous()
+            ws[name] = (pw, x[:, :k].contiguous())
             torch.cuda.synchronize()
-            w4g32.gemm(xk, pw)
+            w4g32.gemm(ws[name][1], pw)
             torch.cuda.synchronize()
             _log(f"[bench] pmc pass: GEMM M=512 K={k} N={n} ({2 * 512 * k * n} flop)")
+        hd = 128
+        qn = (1 + 0.01 * torch.randn(hd, generator=gen, device=dev)).bfloat16()
+        kn = (1 + 0.01 * torch.randn(hd, generator=gen, device=dev)).bfloat16()
+        ang = torch.arange(1024, device=dev, dtype=torch.float32)[:, None] * torch.rand(hd, device=dev)
+        cos, sin = ang.cos().bfloat16().contiguous(), ang.sin().bfloat16().contiguous()
+        kc = torch.zeros((1, 8, 1024, hd), device=dev, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        pos = torch.arange(512, device=dev, dtype=torch.int64)
+        res = torch.randn((512, HIDDEN), generator=gen, device=dev).bfloat16()
+        torch.cuda.synchronize()
+        w4g32.gemm_qk_rope(ws["qkv"][1], ws["qkv"][0], qn, kn, cos, sin, kc, vc, pos, 1e-6)
+        torch.cuda.synchronize()
+        w4g32.gemm_silu(ws["gate_up"][1], ws["gate_up"][0])
+        torch.cuda.synchronize()
+        w4g32.gemm_add_rmsnorm(ws["o"][1], ws["o"][0], res, norm_w, 1e-6)
+        torch.cuda.synchronize()
+        w4g32.gemm_add_rmsnorm(ws["down"][1], ws["down"][0], res, norm_w, 1e-6)
+        torch.cuda.synchronize()
+        _log("[bench] pmc pass: fused prefill forms M=512 (QKV + RoPE, gate||up + SiLU*mul, O / down + add-RMSNorm)")
+        del ws
+        torch.cuda.empty_cache()
+        for n in (HIDDEN, 3 * HIDDEN):
+            w = torch.randn((n, HIDDEN), generator=gen, device=dev).mul_(0.02)
+            s8 = w.abs().amax(dim=1) / 448.0
+            w8 = (w / s8[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+            x64 = torch.randn((64, HIDDEN), generator=gen, device=dev).bfloat16()
+            torch.cuda.synchronize()
+            fp8.linear(x64, w8, s8.contiguous())
+            torch.cuda.synchronize()
+            _log(f"[bench] pmc pass: e4m3 linear M=64 K={HIDDEN} N={n} ({n * HIDDEN + 4 * n + 2 * 64 * HIDDEN + 2 * 64 * n} B)")
         return 0
     if args.pmc_pass == "gemv":
         src = torch.empty(512 * 2**20 // 4, dtype=torch.int32, device=dev).fill_(1)
