@@ -371,12 +371,13 @@ def prefill_bench(torch, dev):
 
 
 def prefill_pass_bench(torch, n_layers: int, dev, replays: int = 10, n: int = 512):
-    """The n-token prompt pass alone (a bucket of 128, 256 or 512 tokens): the bucket graph run once
-    by ``prefill`` and then replayed ``replays`` times (13 executions in all, with the two eager
+    """The n-token prompt pass alone (a bucket of 128, 160, 256 or 512 tokens, the whole 151936-row
+    bf16 text head included, as the reference's prefill returns those logits): the bucket graph run
+    once by ``prefill`` and then replayed ``replays`` times (13 executions in all, with the two eager
     warm-ups before capture, for a kernel trace)."""
     from moss_tts._runtime.decode import DecodeStepG32
 
-    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
+    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242, text_head=True)
     eng.capture_prefill((n,))
     g = torch.Generator().manual_seed(5)
     ids = torch.cat([torch.randint(0, 151643, (n, 1), generator=g), torch.randint(0, 1024, (n, 32), generator=g)], 1)
@@ -482,7 +483,8 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False)
                    "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flop": proj + attn,
                    "parts": "embedding, per layer: norms, INT4 GEMMs, q/k-norm + RoPE + KV write, causal attention, "
                             "SiLU*mul (the last layer's attention, O and MLP for the last token only, whose logits "
-                            "the pass returns); final norm + heads on the last token"}
+                            "the pass returns); final norm + audio heads and the whole 151936-row bf16 text head "
+                            "on the last token"}
         _log(f"[bench] prefill of {n} tokens through {n_layers} layers: {pms:.3f} ms, {tf:.0f} TFLOP/s")
         eng.prefill_graphs.clear()
     nbytes = eng.step_bytes(2047)
@@ -594,7 +596,7 @@ def main() -> int:
                     help="per-kernel budget of the 36-layer W4A16 decode step, measured inside the untraced step")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 36-layer prompt pass (10 graph replays), for a kernel trace")
-    ap.add_argument("--prefill-tokens", type=int, choices=(128, 256, 512), default=512,
+    ap.add_argument("--prefill-tokens", type=int, choices=(128, 160, 256, 512), default=512,
                     help="prompt length (a bucket size) for --prefill-only")
     ap.add_argument("--pmc-pass", choices=("gemv", "gemm"), default=None,
                     help="eager launches only, for rocprofv3 --pmc: 'gemv' = a 512 MiB copy of known size, "
