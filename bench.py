@@ -230,9 +230,10 @@ def fp8_bench(torch, dev):
 
 
 def small_m_bench(torch, dev):
-    """INT4-G32 linear at K = N = 4096 for M = 2..64 tokens (the weight-streaming kernel) beside the
-    M = 1 GEMV of the same shape; weights rotated over >= 600 MB of distinct copies.  GB/s counts
-    the weight stream plus activations in and outputs out."""
+    """INT4-G32 linear at K = N = 4096 for M = 2..64 tokens (2 to 4: the multi-token GEMV; up to 32:
+    the weight-streaming kernel; 64: the register tile) beside the M = 1 GEMV of the same shape;
+    weights rotated over >= 600 MB of distinct copies.  GB/s counts the weight stream plus
+    activations in and outputs out."""
     from moss_tts._runtime import w4g32
 
     out = {}
@@ -241,7 +242,7 @@ def small_m_bench(torch, dev):
     wbytes = n * k // 2 + n * (k // 32) * 2 + n * (k // 64)
     copies = [_quantized(torch, w4g32, n, k, gen, dev) for _ in range(max(2, int(600e6 // wbytes)))]
     gemv_us = None
-    for m in (1, 2, 7, 15, 16, 32, 64):
+    for m in (1, 2, 3, 4, 7, 15, 16, 32, 64):
         x = torch.randn((m, k), generator=gen, device=dev).bfloat16()
         if m == 1:
             fns = [lambda pw=pw: w4g32.gemv(x, pw) for pw in copies]

@@ -79,9 +79,13 @@ int moss_w4g32_quantize_symmetric(const void *w, void *qw, void *sc, void *zp, i
 #define MOSS_DEQUANT_EXACT 0
 #define MOSS_DEQUANT_UNROUNDED 1
 
-/* y bf16 [N] = x bf16 [K] . dequant(W)^T, M must be 1, K % 64 == 0, K <= 16384.
- * rows_per_wave in {0 (auto), 1, 2, 4}.  Replaces the W4A8 projection
- * linear() of src/moss_tts/_runtime/dp4a_scaled.py:81-95 (and int4_dp4a, int4_dp4a.py:56-74). */
+/* y bf16 [M, N] = x bf16 [M, K] . dequant(W)^T, K % 64 == 0, K <= 16384.
+ * M = 1: the decode GEMV; rows_per_wave in {0 (auto), 1, 2, 4}.
+ * M = 2 .. 4 (MOSS_DEQUANT_EXACT only; K <= 4096 or K in {8192, 12288, 16384}): one pass over the
+ * weights for all M tokens, every row of y bit-identical to the M = 1 GEMV of that token's x
+ * (rows_per_wave is ignored).
+ * Replaces the W4A8 projection linear() of src/moss_tts/_runtime/dp4a_scaled.py:81-95 (and
+ * int4_dp4a, int4_dp4a.py:56-74). */
 int moss_w4g32_gemv(const void *x, const void *qw, const void *sc, const void *zp, void *y, int M, int K, int N,
                     int rows_per_wave, int dequant_mode, void *stream);
 
@@ -176,7 +180,9 @@ int moss_w4a8_norm_gateup_silu(const void *x, const void *res, const void *norm_
 /* ------------------------------------------------------------- prefill GEMM */
 /* Y bf16 [M, N] = X bf16 [M, K] . dequant(W)^T with W row-packed INT4-G32 (K % 64 == 0);
  * weights are dequantized bit-exactly (bf16_rne((q-z)*s)), in the registers that feed
- * v_mfma_f32_32x32x16_bf16 (M > 64) or into LDS, fp32 accumulate.  When the output tiles alone
+ * v_mfma_f32_32x32x16_bf16 (M > 64) or into LDS, fp32 accumulate.  2 to 4 tokens (4 only for
+ * K <= 4096) take the multi-token GEMV of moss_w4g32_gemv instead (no matrix cores; each row of Y
+ * equal to the single-token GEMV's).  When the output tiles alone
  * cannot fill the GPU the K dimension is split over workgroups: that needs a caller-owned fp32 workspace
  * of moss_gemm_workspace_bytes(M, K, N) bytes (16-byte aligned; y 8-byte aligned); with a
  * NULL or smaller workspace the GEMM runs unsplit.  Partial sums are added in a fixed order.

@@ -276,6 +276,11 @@ int addnorm_from_parts(const float* parts, int S, const void* res, const void* w
 // overlap xs or res).
 int add_rmsnorm_inplace(void* xs, const void* res, const void* w, void* y, int rows, int n, float eps,
                         hipStream_t st);
+// w4g32_gemv.hip: 2 .. 4 tokens through the exact GEMV (x bf16 [M, K], y bf16 [M, N], x 16-byte
+// aligned), each row of y bit-identical to the single-token GEMV of that token.
+bool w4g32_gemv_tokens_shape(int M, int K);
+int w4g32_gemv_tokens_launch(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
+                             int N, hipStream_t st);
 }  // namespace moss
 
 // true when the byte ranges [a, a + an) and [b, b + bn) share an address

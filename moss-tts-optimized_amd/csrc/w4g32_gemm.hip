@@ -1136,6 +1136,15 @@ template <int FMT>
 int launch_gemm(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K, int N,
                 const float* row_scale, void* ws, long long ws_bytes, hipStream_t st, int* split_out = nullptr) {
     if (split_out) *split_out = 1;
+    // INT4, 2 to 4 tokens: the exact GEMV holding every token's x in registers reads the weights
+    // once, on the VALU, each row of y equal to the single-token GEMV of its token.  Faster than the
+    // weight-streaming kernel (measured on MI355X, 2 / 3 / 4 tokens: K = 4096, N = 12288: 9.8 /
+    // 11.6 / 13.7 against 14.6 / 15.1 / 15.6 us; N = 24576: 16.5 / 20.6 / 24.0 against 27.4 / 28.2
+    // / 29.3 us; K = 12288, N = 4096: 9.9 / 13.1 against 13.0 / 13.3 us) except 4 tokens at
+    // K > 4096 (15.2 against 13.7 us), which stays on the streaming kernel.
+    if (FMT == kInt4G32 && w4g32_gemv_tokens_shape(M, K) && (M <= 3 || K <= 4096) && MOSS_ALIGNED(x, 16) &&
+        MOSS_ALIGNED(qw, 16))
+        return w4g32_gemv_tokens_launch(x, qw, sc, zp, y, M, K, N, st);
     if (stream_shape(FMT, M, K, N, x, qw, sc, zp, y)) {
         launch_stream<FMT>(x, qw, sc, zp, row_scale, y, M, K, N, st);
         return moss_launch_status();

@@ -323,6 +323,164 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
 }
 
 // ---------------------------------------------------------------------------------------
+// A few tokens (M = 2 .. kMaxTokens, exact mode): one weight row per wave, dequantized once and
+// multiplied with the x slice of every token (T slices held in VGPRs), so the weights are read
+// once for all T rows of y, on the VALU (no matrix-core instruction below 16 tokens).  Each
+// token's dot is row_partial_exact's chain over the same words in the same order, followed by
+// the same wave_sum: every row of y equals the single-token GEMV of that token bit for bit.
+constexpr int kMaxTokens = 4;
+
+template <int KG, int T>
+__device__ __forceinline__ void row_partial_exact_tokens(const XSlice<KG> (&xs)[T], const RowLoad<KG>& r, Magic m,
+                                                         float (&acc)[T]) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = 0.f;
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        const uint32_t s_lo = r.s[j] & 0xffffu;
+        const uint32_t s_hi = s_lo << 16;
+        const float bias = -(128.0f + (float)r.z[j]) * bf16_bits((uint16_t)s_lo);
+        const uint32_t words[4] = {r.w[j].x, r.w[j].y, r.w[j].z, r.w[j].w};
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            const uint32_t w = words[wd];
+            uint32_t wq[4];
+            dequant_word_exact(((w >> 0) & m.mask) | m.bias, ((w >> 4) & m.mask) | m.bias,
+                               ((w >> 8) & m.mask) | m.bias, ((w >> 12) & m.mask) | m.bias, s_lo, s_hi, bias, wq);
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t] = dot2_bf16(wq[i], xs[t].v[j][4 * wd + i], acc[t]);
+        }
+    }
+}
+
+// x bf16 [T, 32 G], y bf16 [T, n_out]; R weight rows per wave, grid ceil(n_out / (4 R))
+// workgroups of 4 waves.
+template <int KG, int T, int R, bool FULL>
+__global__ __launch_bounds__(256) void w4g32_gemv_tokens_exact(const uint16_t* __restrict__ x,
+                                                               const uint4* __restrict__ qw,
+                                                               const uint16_t* __restrict__ sc,
+                                                               const uint8_t* __restrict__ zp,
+                                                               uint16_t* __restrict__ y, int G, int n_out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
+    const int row0 = wave * R;
+    if (row0 >= n_out) return;  // wave-uniform
+    XSlice<KG> xs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) load_x<KG, false, FULL>(xs[t], x + (size_t)t * 32 * G, lane, G);
+    RowLoad<KG> rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) load_row_nt<KG, FULL>(rows[r], qw, sc, zp, min(row0 + r, n_out - 1), lane, G);
+    const Magic m = make_magic();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc[T];
+        row_partial_exact_tokens<KG, T>(xs, rows[r], m, acc);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = wave_sum(acc[t]);
+            if (lane == 0 && row0 + r < n_out) y[(size_t)t * n_out + row0 + r] = f32_to_bf16(v);
+        }
+    }
+}
+
+// Large K (K = 4096 W, as gemv_ksplit): workgroup = R weight rows, wave s = K slice s; the
+// slices' sums meet in LDS and are added in slice order, as gemv_ksplit adds them.
+template <int W, int T, int R>
+__global__ __launch_bounds__(64 * W) void w4g32_gemv_ksplit_tokens_exact(const uint16_t* __restrict__ x,
+                                                                        const uint4* __restrict__ qw,
+                                                                        const uint16_t* __restrict__ sc,
+                                                                        const uint8_t* __restrict__ zp,
+                                                                        uint16_t* __restrict__ y, int G, int n_out) {
+    __shared__ float part[W][R][T];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int slice = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int row0 = blockIdx.x * R;  // < n_out (grid)
+    const int g0 = 128 * slice;
+    XSlice<2> xs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) load_x<2, false, true>(xs[t], x + (size_t)t * 32 * G + 32 * g0, lane, 128);
+    RowLoad<2> rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) load_row_slice<true>(rows[r], qw, sc, zp, min(row0 + r, n_out - 1), lane, G, g0);
+    const Magic m = make_magic();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc[T];
+        row_partial_exact_tokens<2, T>(xs, rows[r], m, acc);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = wave_sum(acc[t]);
+            if (lane == 0) part[slice][r][t] = v;
+        }
+    }
+    __syncthreads();
+    if (slice == 0 && lane < R * T) {
+        const int r = lane / T, t = lane % T;
+        if (row0 + r < n_out) {
+            float a = 0.f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) a += part[w][r][t];
+            y[(size_t)t * n_out + row0 + r] = f32_to_bf16(a);
+        }
+    }
+}
+
+template <int T>
+int launch_tokens_t(const void* x, const void* qw, const void* sc, const void* zp, void* y, int G, int n_out,
+                    hipStream_t st) {
+    const auto* xp = (const uint16_t*)x;
+    const auto* qp = (const uint4*)qw;
+    const auto* sp = (const uint16_t*)sc;
+    const auto* zpp = (const uint8_t*)zp;
+    auto* yp = (uint16_t*)y;
+    // K = 4096 W for W = 2, 3, 4: the K-split form (as the single-token GEMV splits those K)
+    if (G % 128 == 0 && G >= 256 && G <= 512) {
+        // 4 rows per workgroup (measured on MI355X at K = 8192 and 12288, N = 4096, 2 to 4 tokens:
+        // 1 row 11.3-28.0 us, 2 rows 8.1-17.3, 4 rows 7.5-15.2)
+        const int W = G / 128;
+        const dim3 grid((n_out + 3) / 4);
+#define MOSS_TK(WV)                                                                                                 \
+    if (W == WV) {                                                                                                  \
+        hipLaunchKernelGGL((w4g32_gemv_ksplit_tokens_exact<WV, T, 4>), grid, dim3(64 * WV), 0, st, xp, qp, sp, zpp, \
+                           yp, G, n_out);                                                                           \
+        return moss_launch_status();                                                                                \
+    }
+        MOSS_TK(2) MOSS_TK(3) MOSS_TK(4)
+#undef MOSS_TK
+        return (int)hipErrorInvalidValue;
+    }
+    const int KG = (G + kWave - 1) / kWave;
+    if (KG > 2) return (int)hipErrorInvalidValue;  // T x KG x 16 VGPRs of x: K <= 4096
+    const bool full = (G == kWave * KG) && (KG % 2 == 0);
+    // 4 rows per wave unless 2 fill the CUs in fewer row-rounds (a round: every CU holding one
+    // workgroup of 4 waves).  Measured on MI355X, K = 4096, 2 to 4 tokens: N = 4096 / 12288 / 24576
+    // fastest at 4 rows, N = 6144 at 2 (384 workgroups of 4 rows leave half a round).
+    const int wg4 = (n_out + 15) / 16, wg2 = (n_out + 7) / 8;
+    const int R = ((wg2 + 255) / 256) * 2 < ((wg4 + 255) / 256) * 4 ? 2 : 4;
+    const dim3 block(256);
+#define MOSS_TR(RV)                                                                                                 \
+    if (R == RV) {                                                                                                  \
+        const dim3 grid((n_out + 4 * RV - 1) / (4 * RV));                                                           \
+        if (KG == 1)                                                                                                \
+            hipLaunchKernelGGL((w4g32_gemv_tokens_exact<1, T, RV, false>), grid, block, 0, st, xp, qp, sp, zpp, yp, \
+                               G, n_out);                                                                           \
+        else if (full)                                                                                              \
+            hipLaunchKernelGGL((w4g32_gemv_tokens_exact<2, T, RV, true>), grid, block, 0, st, xp, qp, sp, zpp, yp,  \
+                               G, n_out);                                                                           \
+        else                                                                                                        \
+            hipLaunchKernelGGL((w4g32_gemv_tokens_exact<2, T, RV, false>), grid, block, 0, st, xp, qp, sp, zpp, yp, \
+                               G, n_out);                                                                           \
+        return moss_launch_status();                                                                                \
+    }
+    MOSS_TR(2) MOSS_TR(4)
+#undef MOSS_TR
+    return (int)hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------------
 // Entry kernels: one name per (role, dequant mode), so profiles tell them apart.
 // The plain GEMV at up to 2 rows per wave fits 6 waves per SIMD (80 VGPRs), so a K = 4096,
 // N = 12288 launch (1536 workgroups) runs in one round on 256 CUs instead of 1.2.
@@ -501,6 +659,28 @@ int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, v
 }
 
 }  // namespace
+
+// M = 2 .. kMaxTokens tokens through the exact GEMV (one weight stream for all of them); K as the
+// single-token GEMV takes it up to 4096 and K = 8192, 12288, 16384.  hipErrorInvalidValue for
+// other shapes (the caller then uses another kernel).
+int w4g32_gemv_tokens_launch(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
+                             int N, hipStream_t st) {
+    if (K % 64 || N <= 0) return (int)hipErrorInvalidValue;
+    const int G = K / 32;
+    switch (M) {
+        case 2: return launch_tokens_t<2>(x, qw, sc, zp, y, G, N, st);
+        case 3: return launch_tokens_t<3>(x, qw, sc, zp, y, G, N, st);
+        case 4: return launch_tokens_t<4>(x, qw, sc, zp, y, G, N, st);
+        default: return (int)hipErrorInvalidValue;
+    }
+}
+
+bool w4g32_gemv_tokens_shape(int M, int K) {
+    if (M < 2 || M > kMaxTokens || K % 64) return false;
+    const int G = K / 32;
+    return G <= 128 || (G % 128 == 0 && G <= 512);
+}
+
 }  // namespace moss
 
 using namespace moss;
@@ -511,8 +691,12 @@ static constexpr int kMaxGemvK = 8 * 64 * 32;
 MOSS_API int moss_w4g32_gemv(const void* x, const void* qw, const void* sc, const void* zp, void* y, int M, int K,
                              int N, int rows_per_wave, int dequant_mode, void* stream) {
     MOSS_CHECK_ARG(x && qw && sc && zp && y);
-    MOSS_CHECK_ARG(M == 1 && K > 0 && N > 0 && K % 64 == 0 && K <= kMaxGemvK);
+    MOSS_CHECK_ARG(M >= 1 && K > 0 && N > 0 && K % 64 == 0 && K <= kMaxGemvK);
     MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
+    if (M > 1) {
+        MOSS_CHECK_ARG(dequant_mode == MOSS_DEQUANT_EXACT && w4g32_gemv_tokens_shape(M, K));
+        return w4g32_gemv_tokens_launch(x, qw, sc, zp, y, M, K, N, (hipStream_t)stream);
+    }
     return launch_gemv<false, 0>(x, qw, sc, zp, y, K, N, rows_per_wave, dequant_mode, NormArgs{}, (hipStream_t)stream);
 }
 

@@ -226,14 +226,29 @@ def _mode_arg(dequant: int) -> int:
     return dequant
 
 
+#: tokens the GEMV takes in one pass over the weights
+MAX_GEMV_TOKENS = 4
+
+
 def gemv(x: torch.Tensor, w: PackedW4G32, *, rows_per_wave: int = 0, dequant: int = EXACT) -> torch.Tensor:
-    """Batch-1 decode projection: bf16 ``[..., K]`` (one row) -> bf16 ``[..., N]``."""
-    _check_row(x, w)
+    """Decode projection: bf16 ``[..., K]`` -> bf16 ``[..., N]``.  One row, or up to
+    ``MAX_GEMV_TOKENS`` rows (exact mode; ``K <= 4096`` or ``K`` in 8192 / 12288 / 16384) read the
+    weights once, each output row bit-identical to the one-row GEMV of its input row."""
+    _cuda_contig("x", x, torch.bfloat16, w.device)
+    m = x.numel() // w.K if w.K else 0
+    _require(x.shape[-1] == w.K and m * w.K == x.numel() and 1 <= m <= MAX_GEMV_TOKENS,
+             f"1 to {MAX_GEMV_TOKENS} contiguous bf16 rows of {w.K} values required, got shape {tuple(x.shape)}")
+    _require(w.K <= _MAX_GEMV_K, f"decode GEMV supports K <= {_MAX_GEMV_K}")
+    _require(_aligned(x, 16), "x must be 16-byte aligned")
     rows = _rows_arg(rows_per_wave)
     mode = _mode_arg(dequant)
+    if m > 1:
+        g = w.K // 32
+        _require(mode == EXACT, "several rows take the exact dequant only")
+        _require(g <= 128 or (g % 128 == 0 and g <= 512), "several rows need K <= 4096 or K in 8192, 12288, 16384")
     y = torch.empty((*x.shape[:-1], w.N), dtype=torch.bfloat16, device=x.device)
     native.call("moss_w4g32_gemv", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales), native.ptr(w.zeros),
-                native.ptr(y), 1, w.K, w.N, rows, mode, native.stream_of(x))
+                native.ptr(y), m, w.K, w.N, rows, mode, native.stream_of(x))
     return y
 
 

@@ -87,7 +87,9 @@ def test_argument_errors_are_rejected_before_launch(lib):
     p = ctypes.c_void_p(4096)
     odd = ctypes.c_void_p(4097)
     assert lib.moss_w4g32_gemv(null, p, p, p, p, 1, 4096, 4096, 0, 0, null) == 1
-    assert lib.moss_w4g32_gemv(p, p, p, p, p, 2, 4096, 4096, 0, 0, null) == 1          # M must be 1
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 5, 4096, 4096, 0, 0, null) == 1          # M <= 4
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 2, 4096, 4096, 0, 1, null) == 1          # M > 1: exact only
+    assert lib.moss_w4g32_gemv(p, p, p, p, p, 2, 6144, 4096, 0, 0, null) == 1          # M > 1: K shape
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4000, 4096, 0, 0, null) == 1          # K % 64
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 3, 0, null) == 1          # rows_per_wave
     assert lib.moss_w4g32_gemv(p, p, p, p, p, 1, 4096, 4096, 0, 7, null) == 1          # dequant mode

@@ -253,6 +253,35 @@ def test_gemv_rejects_bad_inputs(dev):
         w4g32.gemv(torch.randn((1, 128), device=dev).bfloat16(), pw, rows_per_wave=3)
     with pytest.raises(ValueError):
         w4g32.gemv(torch.randn((1, 128), device=dev).bfloat16(), pw, dequant=2)
+    with pytest.raises(ValueError):
+        w4g32.gemv(torch.randn((5, 128), device=dev).bfloat16(), pw)        # at most 4 rows
+    with pytest.raises(ValueError):
+        w4g32.gemv(torch.randn((2, 128), device=dev).bfloat16(), pw, dequant=w4g32.UNROUNDED)
+    pw6 = w4g32.quantize_minmax(torch.randn((8, 6144), device=dev))
+    with pytest.raises(ValueError):
+        w4g32.gemv(torch.randn((2, 6144), device=dev).bfloat16(), pw6)      # several rows: K shape
+
+
+@pytest.mark.parametrize("k,n", [(64, 8), (2112, 129), (3072, 777), (4096, 4096), (4096, 6144), (8192, 2048),
+                                 (12288, 4100), (16384, 1024)])
+def test_gemv_tokens_equal_single_token_gemv(dev, k, n):
+    """2 to 4 tokens in one pass over the weights: every output row equals the one-token GEMV of
+    its input row bit for bit (same per-lane dot2 chain, same cross-lane sum), the GEMM takes that
+    path for 2 and 3 tokens (4 where K <= 4096), and the result is within the oracle's bar."""
+    from moss_tts._runtime import w4g32
+
+    q, z, s = _case(n, k, 900 + k + n)
+    pw = _packed(q, z, s, dev)
+    dq = o.dequantize(q, z, s)
+    for m in (2, 3, 4):
+        print(f"gemv tokens M={m} K={k} N={n}", flush=True)
+        x = torch.randn((m, k), generator=torch.Generator().manual_seed(m + k)).bfloat16().to(dev)
+        y = w4g32.gemv(x, pw)
+        single = torch.cat([w4g32.gemv(x[r:r + 1].contiguous(), pw) for r in range(m)])
+        assert torch.equal(y, single), f"M={m} K={k} N={n}: rows differ from the one-token GEMV"
+        if m <= 3 or k <= 4096:
+            assert torch.equal(w4g32.gemm(x, pw), single), f"M={m} K={k} N={n}: the GEMM took another path"
+        _assert_close(y, o.linear(x.cpu(), dq), f"gemv tokens M={m} K={k} N={n}")
 
 
 # ------------------------------------------------------------------- prefill GEMM
@@ -269,6 +298,7 @@ def test_gemv_rejects_bad_inputs(dev):
                                    # the small-M weight-streaming kernel (M <= 32, K % 4096 == 0): one
                                    # and two token tiles, ragged tiles, a ragged last row tile, K = 12288
                                    (1, 4096, 2048), (2, 4096, 4096), (7, 4096, 4096), (15, 4096, 4096),
+                                   (4, 12288, 4096),
                                    (17, 4096, 2052), (32, 12288, 4096), (25, 4096, 12296),
                                    # just past it: the tiles again
                                    (33, 4096, 6144), (64, 4096, 4096), (50, 12288, 4100)])
