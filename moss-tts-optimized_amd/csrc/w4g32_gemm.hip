@@ -812,7 +812,8 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ par
 }
 
 // ---------------------------------------------------------------------------------------------
-// Small M (up to 32 tokens INT4, 16 e4m3): weight streaming.  A workgroup owns 16 weight rows over
+// Small M (up to 32 tokens INT4, 16 e4m3; 2 to 4 INT4 tokens mostly take the multi-token GEMV,
+// see launch_gemm): weight streaming.  A workgroup owns 16 weight rows over
 // the whole of K, so every weight byte is read once per call and no partial sums leave the
 // workgroup; ceil(N / 16) workgroups of 8 waves, wave w taking the w-th eighth of K, 4 groups of
 // 32 inputs (a quad) per step.  One v_mfma_f32_16x16x32_bf16 per group and token tile: lane

@@ -323,11 +323,11 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
 }
 
 // ---------------------------------------------------------------------------------------
-// A few tokens (M = 2 .. kMaxTokens, exact mode): one weight row per wave, dequantized once and
-// multiplied with the x slice of every token (T slices held in VGPRs), so the weights are read
-// once for all T rows of y, on the VALU (no matrix-core instruction below 16 tokens).  Each
-// token's dot is row_partial_exact's chain over the same words in the same order, followed by
-// the same wave_sum: every row of y equals the single-token GEMV of that token bit for bit.
+// A few tokens (M = 2 .. kMaxTokens, exact mode): R weight rows per wave, each dequantized once
+// and multiplied with the x slice of every token (T slices held in VGPRs), so the weights are
+// read once for all T rows of y, on the VALU (no matrix-core instruction).  Each token's dot is
+// row_partial_exact's chain over the same words in the same order, followed by the same
+// wave_sum: every row of y equals the single-token GEMV of that token bit for bit.
 constexpr int kMaxTokens = 4;
 
 template <int KG, int T>
