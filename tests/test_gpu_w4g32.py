@@ -263,7 +263,9 @@ def test_gemv_rejects_bad_inputs(dev):
 
 
 @pytest.mark.parametrize("k,n", [(64, 8), (2112, 129), (3072, 777), (4096, 4096), (4096, 6144), (8192, 2048),
-                                 (12288, 4100), (16384, 1024)])
+                                 (12288, 4100), (16384, 1024),
+                                 # ragged last workgroup: 4 rows per wave (N = 4094) / per K-split group (4099)
+                                 (4096, 4094), (12288, 4099)])
 def test_gemv_tokens_equal_single_token_gemv(dev, k, n):
     """2 to 4 tokens in one pass over the weights: every output row equals the one-token GEMV of
     its input row bit for bit (same per-lane dot2 chain, same cross-lane sum), the GEMM takes that
