@@ -506,18 +506,19 @@ def decode_step_bench(torch, n_layers: int, steps: int, dev, w4a8: bool = False)
     return out
 
 
-def decode_budget(torch, n_layers: int, steps: int, dev) -> dict:
-    """Per-kernel budget of the W4A16 decode step measured inside the step itself, untraced: for each
-    kernel family, a graph of the step in which every launch of that family runs twice (the
-    launches are idempotent: same inputs, same outputs) is timed against the plain step graph; the
-    difference is what that family's launches cost in the step, dispatch gaps included.  The
-    families' costs sum to about the step time, unlike traced kernel durations."""
+def decode_budget(torch, n_layers: int, steps: int, dev, w4a8: bool = False) -> dict:
+    """Per-kernel budget of the decode step (W4A16, or the W4A8 arithmetic) measured inside the step
+    itself, untraced: for each kernel family, a graph of the step in which every launch of that
+    family runs twice (the launches are idempotent: same inputs, same outputs) is timed against the
+    plain step graph; the difference is what that family's launches cost in the step, dispatch gaps
+    included.  The families' costs sum to about the step time, unlike traced kernel durations."""
     import contextlib
 
     from moss_tts._runtime import attention, sampling, w4g32
+    from moss_tts._runtime import w4a8 as w8
     from moss_tts._runtime.decode import DecodeStepG32
 
-    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242)
+    eng = DecodeStepG32.random(n_layers, max_length=2048, device=dev, seed=4242, w4a8=w4a8)
     ids = torch.tensor([[151643] + [i * 31 % 1025 for i in range(32)]], dtype=torch.int64)
 
     def time_step() -> float:
@@ -533,13 +534,35 @@ def decode_budget(torch, n_layers: int, steps: int, dev) -> dict:
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps * 1e3
 
+    # The extra launch reads copies of the weights (and of the KV caches) made once, outside the
+    # capture, during the eager warm-up: reading the same bytes the step's own launch reads right
+    # after it would find part of them in the Infinity Cache and understate the family's cost.
+    copies = {}
+
+    def cold(obj):
+        # keyed by storage: modules hand out a new PackedW4G32 view of the same tensors per access
+        if isinstance(obj, w4g32.PackedW4G32):
+            key = ("w", obj.qw.data_ptr(), obj.qw.numel())
+        elif isinstance(obj, torch.Tensor):
+            key = ("t", obj.data_ptr(), obj.numel())
+        else:
+            return obj
+        if key not in copies:
+            assert not torch.cuda.is_current_stream_capturing(), "copies are made during the eager warm-up"
+            if isinstance(obj, w4g32.PackedW4G32):
+                copies[key] = w4g32.PackedW4G32(obj.qw.clone(), obj.scales.clone(), obj.zeros.clone())
+            else:
+                copies[key] = obj.clone()
+        return copies[key]
+
     @contextlib.contextmanager
-    def doubled(module, name, pick):
+    def doubled(module, name, pick, cold_args=()):
         orig = getattr(module, name)
 
         def twice(*a, **kw):
             if pick(*a, **kw):
-                orig(*a, **kw)
+                extra = [cold(v) if i in cold_args else v for i, v in enumerate(a)]
+                orig(*extra, **kw)
             return orig(*a, **kw)
 
         setattr(module, name, twice)
@@ -551,32 +574,54 @@ def decode_budget(torch, n_layers: int, steps: int, dev) -> dict:
     def width(a, kw):
         return a[3].N if len(a) > 3 else kw["w"].N
 
-    families = [
-        ("embedding sum", attention, "embedding_sum", lambda *a, **kw: True, 1),
-        ("add-RMSNorm + q||k||v GEMV", w4g32, "norm_gemv", lambda *a, **kw: width(a, kw) == 6144, n_layers),
-        ("q/k-norm + RoPE + KV write + attention split + merge", attention, "decode_attention_qkv",
-         lambda *a, **kw: True, n_layers),
-        ("O GEMV (K=4096)", w4g32, "gemv", lambda *a, **kw: a[1].K == 4096, n_layers),
-        ("add-RMSNorm + gate||up GEMV + SiLU*mul", w4g32, "norm_gateup_silu", lambda *a, **kw: True, n_layers),
-        ("down GEMV (K=12288)", w4g32, "gemv", lambda *a, **kw: a[1].K == 12288, n_layers),
-        ("final add-RMSNorm + heads GEMV", w4g32, "norm_gemv", lambda *a, **kw: width(a, kw) > 6144, 1),
-        ("sampling (text and audio rows)", sampling, "sample_topk_pair", lambda *a, **kw: True, 1),
-        ("next-id composition", sampling, "compose_next_ids", lambda *a, **kw: True, 1),
+    if w4a8:
+        def w8_k(a, kw):
+            return (a[1] if len(a) > 1 else kw["w"]).K
+
+        layer_families = [
+            ("add-RMSNorm + int8 quantizer + q||k||v GEMV", w8, "norm_linear", lambda *a, **kw: True, n_layers, (3,)),
+            ("q/k-norm + RoPE + KV write + attention split + merge with int8 output", attention,
+             "decode_attention_qkv", lambda *a, **kw: True, n_layers, (5, 6)),
+            ("O GEMV (K=4096, int8 input from the merge)", w8, "linear",
+             lambda *a, **kw: w8_k(a, kw) == 4096 and not kw.get("paired"), n_layers, (1,)),
+            ("add-RMSNorm + int8 quantizer", w8, "norm_quant", lambda *a, **kw: True, n_layers, ()),
+            ("gate||up GEMV + SiLU*mul", w8, "linear", lambda *a, **kw: bool(kw.get("paired")), n_layers, (1,)),
+            ("int8 quantizer + down GEMV (K=12288)", w8, "linear", lambda *a, **kw: w8_k(a, kw) == 12288,
+             n_layers, (1,)),
+        ]
+    else:
+        layer_families = [
+            ("add-RMSNorm + q||k||v GEMV", w4g32, "norm_gemv", lambda *a, **kw: width(a, kw) == 6144, n_layers,
+             (3,)),
+            ("q/k-norm + RoPE + KV write + attention split + merge", attention, "decode_attention_qkv",
+             lambda *a, **kw: True, n_layers, (5, 6)),
+            ("O GEMV (K=4096)", w4g32, "gemv", lambda *a, **kw: a[1].K == 4096, n_layers, (1,)),
+            ("add-RMSNorm + gate||up GEMV + SiLU*mul", w4g32, "norm_gateup_silu", lambda *a, **kw: True,
+             n_layers, (3,)),
+            ("down GEMV (K=12288)", w4g32, "gemv", lambda *a, **kw: a[1].K == 12288, n_layers, (1,)),
+        ]
+    families = [("embedding sum", attention, "embedding_sum", lambda *a, **kw: True, 1, ())] + layer_families + [
+        ("final add-RMSNorm + heads GEMV", w4g32, "norm_gemv", lambda *a, **kw: width(a, kw) > 6144, 1, (3,)),
+        ("sampling (text and audio rows)", sampling, "sample_topk_pair", lambda *a, **kw: True, 1, ()),
+        ("next-id composition", sampling, "compose_next_ids", lambda *a, **kw: True, 1, ()),
     ]
-    base = [time_step() for _ in range(3)]
-    base_us = sorted(base)[1]
+    base = [time_step() for _ in range(5)]
+    base_us = sorted(base)[2]
     rows, total = [], 0.0
-    for label, module, name, pick, count in families:
-        with doubled(module, name, pick):
-            t = sorted(time_step() for _ in range(3))[1]
+    for label, module, name, pick, count, cold_args in families:
+        with doubled(module, name, pick, cold_args):
+            t = sorted(time_step() for _ in range(5))[2]
+        copies.clear()
         cost = t - base_us
         total += cost
         rows.append({"kernels": label, "launches_per_step": count, "us_per_step": round(cost, 1),
                      "us_per_launch": round(cost / count, 3)})
         _log(f"[bench] budget: {label}: {cost:.1f} us per step ({cost / count:.2f} us x {count})")
     _log(f"[bench] budget: step {base_us:.1f} us; sum of the families {total:.1f} us")
-    return {"step_us": round(base_us, 1), "sum_of_families_us": round(total, 1), "families": rows,
-            "method": "each family's launches doubled inside the captured step; cost = step time difference"}
+    return {"arithmetic": "w4a8" if w4a8 else "w4a16", "step_us": round(base_us, 1),
+            "sum_of_families_us": round(total, 1), "families": rows,
+            "method": "each family's launches doubled inside the captured step, the extra launch reading its "
+                      "own copy of the weights and KV caches; cost = step time difference"}
 
 
 def main() -> int:
@@ -594,7 +639,8 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the 36-layer decode step (both arithmetics) and its lines, for a kernel trace")
     ap.add_argument("--decode-budget", action="store_true",
-                    help="per-kernel budget of the 36-layer W4A16 decode step, measured inside the untraced step")
+                    help="per-kernel budget of the 36-layer decode step (W4A16, then W4A8), measured inside the "
+                         "untraced step")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 36-layer prompt pass (10 graph replays), for a kernel trace")
     ap.add_argument("--prefill-tokens", type=int, choices=(128, 160, 256, 512), default=512,
@@ -627,7 +673,9 @@ def main() -> int:
         return 0
     if args.decode_budget:
         _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode-step budget")
-        print(json.dumps(decode_budget(torch, args.decode_layers, max(1, args.decode_steps), dev)), flush=True)
+        for w4a8 in (False, True):
+            print(json.dumps(decode_budget(torch, args.decode_layers, max(1, args.decode_steps), dev, w4a8=w4a8)),
+                  flush=True)
         return 0
     if args.decode_only:
         _log(f"[bench] device {torch.cuda.get_device_name(0)} ({arch}); decode step only")
