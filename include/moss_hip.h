@@ -148,10 +148,19 @@ int moss_rmsnorm_quant_g32(const void *x, const void *res, const void *w, void *
 
 /* y bf16 [N] = bf16(sum_g f32(isum[n,g]) * (s[n,g] * sx[g])), isum[n,g] = sum_{k in g}
  * (q[n,k] - z[n,g]) * qx[k] exact in int32, on rowpack weights; K % 64 == 0, K <= 16384,
- * rows_per_wave in {0 (auto), 1, 2, 4}.  Replaces linear (paired=False),
+ * rows_per_wave in {0 (auto), 1, 2, 4}.  The fp32 sum runs over slices of 64 groups: each
+ * slice's terms in a fixed tree, the slice sums in order; every W4A8 projection here uses that
+ * order, so fused and unfused forms agree bit for bit.  Replaces linear (paired=False),
  * src/moss_tts/_runtime/dp4a_scaled.py:22-57,80-95 (and int4_dp4a.py:33-74). */
 int moss_w4a8_gemv(const void *qx, const void *sx, const void *qsum, const void *qw, const void *sc, const void *zp,
                    void *y, int K, int N, int rows_per_wave, void *stream);
+
+/* The same from bf16 x [K] (16-byte aligned): the int8 group quantizer runs inside the
+ * projection's kernel, bit-identical to moss_int8_quantize_g32 followed by moss_w4a8_gemv.
+ * Replaces linear with prequantized=None, src/moss_tts/_runtime/dp4a_scaled.py:80-95 (its
+ * _int8_activation_grouped launch, :86-89, and the _gemv launch, :94). */
+int moss_w4a8_quant_gemv(const void *x, const void *qw, const void *sc, const void *zp, void *y, int K, int N,
+                         int rows_per_wave, void *stream);
 
 /* Paired gate||up (W has 2*N_half rows, gate first): gate and up rounded to bf16, y bf16
  * [N_half] = bf16(bf16(silu(gate)) * up).  With out_qx/out_sx/out_qsum (all set or all NULL;

@@ -9,6 +9,11 @@
 // in fp32, rounded to bf16; the paired form rounds gate and up to bf16 and applies the
 // SiLU*mul epilogue (dp4a_scaled.py:64-68).
 //
+// Combine order, the same in every kernel here so that all forms of a projection agree bit for
+// bit: the groups of a row fall into slices of 64 (slice j = groups 64 j .. 64 j + 63); each
+// group's term f32(isum) * (s_w * s_x) is rounded to fp32 on its own, a slice is summed by
+// wave_sum's fixed tree, and the slice sums are added in slice order.
+//
 // Byte order of the quantized activations ("dot4 order"): within each block of 8 values,
 // bytes 8b..8b+7 hold x[8b + {0, 4, 1, 5, 2, 6, 3, 7}].  That is the order in which
 // (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) expand a row-packed code word into bytes, so
@@ -23,6 +28,58 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+constexpr int kMaxSlices = 8;  // K <= 16384: at most 8 slices of 64 groups
+
+// The integer dot of one group: sum (q - z) * qx over its 32 codes, exact in int32.
+__device__ __forceinline__ int group_isum(const uint4& w, const uint4& xa, const uint4& xb, uint32_t zbyte,
+                                          uint32_t zsh, int xq, uint32_t mask) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    int isum = -(int)((zbyte >> zsh) & 15u) * xq;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        isum = dot4(words[c] & mask, xw[2 * c], isum);
+        isum = dot4((words[c] >> 4) & mask, xw[2 * c + 1], isum);
+    }
+    return isum;
+}
+
+// One slice's sum: the lane's group term rounded on its own (kept opaque, so the compiler cannot
+// fuse it into the first add of the tree), then wave_sum's fixed tree.  A lane past the last
+// group (live false) adds +0, as a zero weight does.
+__device__ __forceinline__ float slice_sum(int isum, uint32_t s_bits, float xs, bool live = true) {
+    float t = (float)isum * (bf16_bits((uint16_t)s_bits) * xs);
+    t = live ? t : 0.f;
+    asm volatile("" : "+v"(t));
+    return wave_sum(t);
+}
+
+// Quantize one group of 32 bf16 values held as four 16-byte words, exactly as
+// int8_quantize_g32 does: codes in dot4 order, the group scale and code sum.
+__device__ __forceinline__ void quantize_group32(const uint4 (&h)[4], uint4& qa, uint4& qb, float& scale, int& sum) {
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t w[4] = {h[c].x, h[c].y, h[c].z, h[c].w};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            v[8 * c + 2 * p] = bf16_lo(w[p]);
+            v[8 * c + 2 * p + 1] = bf16_hi(w[p]);
+        }
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+    scale = g32_scale(m);
+    const float inv = 1.0f / scale;
+    uint32_t q[8];
+    sum = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sum += quantize8_dot4(v + 8 * c, inv, q[2 * c], q[2 * c + 1]);
+    qa = make_uint4(q[0], q[1], q[2], q[3]);
+    qb = make_uint4(q[4], q[5], q[6], q[7]);
 }
 
 // One 32-lane half-wave per group of 32 (one value per lane): the group's max |x| and code
@@ -62,25 +119,30 @@ struct W8Norm {
     float eps;
 };
 
-// Row-per-wave GEMV: lane l owns groups l + 64 j; KG = ceil(G / 64).  QOUT (paired only):
+// Row-per-wave GEMV (the forms with a fused normalization or output quantizer): lane l owns
+// groups l + 64 j; KG = ceil(G / 64).  QOUT (paired only):
 // 32 / R waves x R rows per workgroup cover one 32-row output group, which the workgroup
 // also quantizes (the down projection's activations), as the reference's fused gate/up does
 // (src/moss_tts/_runtime/dp4a_scaled.py:70-78).  ACT 0 reads quantized activations; ACT 1 and
-// 2 form them in the workgroup (W8Norm; K = 2048 KG).
-template <int KG, int R, bool PAIRED, bool QOUT, int ACT = 0>
-__global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
+// 2 form them in the workgroup (W8Norm; K = 2048 KG) with its first 256 threads, then all WPB
+// waves of the workgroup take their rows (8 waves halve the workgroups that repeat the norm).
+template <int KG, int R, bool PAIRED, bool QOUT, int ACT = 0, int WPB = 4>
+__global__ __launch_bounds__(QOUT ? kWave * 32 / R : kWave * WPB) void w4a8_gemv_kernel(
     const uint32_t* __restrict__ qx, const float* __restrict__ sx, const int* __restrict__ qsum,
     const uint4* __restrict__ qw, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     uint16_t* __restrict__ y, uint8_t* __restrict__ oq, float* __restrict__ osx, int* __restrict__ osum, int G,
     int n_out, W8Norm nm) {
     static_assert(!QOUT || (PAIRED && (R == 2 || R == 4)), "output quantization covers 32 paired rows");
     static_assert(ACT == 0 || !QOUT, "the fused normalization runs with 256-thread workgroups");
+    static_assert(QOUT || ACT > 0, "the plain projections run on w4a8_ksplit_kernel");
+    static_assert(WPB == 4 || (WPB == 8 && ACT > 0), "8-wave workgroups for the fused normalization only");
+    // the threads that form the normalized activations (wave-uniform)
+    const bool norm_thread = WPB == 4 || threadIdx.x < 256;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
     const int row0 = wave * R;
-    // wave-uniform; QOUT grids hold whole groups only, and with ACT > 0 every wave takes part in
-    // the workgroup's normalization first
-    if (ACT == 0 && !QOUT && row0 >= n_out) return;
+    // QOUT grids hold whole groups only, and with ACT > 0 every wave takes part in the
+    // workgroup's normalization first: no wave leaves early
     constexpr int NR = PAIRED ? 2 * R : R;
     // activations first (completions are counted in order): 32 int8 per group, its scale and sum
     uint4 xa[KG], xb[KG];
@@ -103,7 +165,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
                 xq[j] = 0;
             }
         }
-    } else {
+    } else if (norm_thread) {
 #pragma unroll
         for (int c = 0; c < KG; ++c) {
             const int ci = threadIdx.x + 256 * c;
@@ -145,6 +207,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
         float ss = 0.f;
 #pragma unroll
         for (int c = 0; c < KG; ++c) {
+            if (!norm_thread) break;  // wave-uniform
             const int ci = threadIdx.x + 256 * c;
             uint32_t sw[4] = {nx[c].x, nx[c].y, nx[c].z, nx[c].w};
             if constexpr (ACT == 2) {
@@ -163,7 +226,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
             }
         }
         ss = wave_sum(ss);
-        if (lane == 0) red[threadIdx.x / kWave] = ss;
+        if (lane == 0 && norm_thread) red[threadIdx.x / kWave] = ss;
         __syncthreads();
         float total = 0.f;
 #pragma unroll
@@ -171,6 +234,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
         const float inv = rsqrtf(total / (float)(32 * G) + nm.eps);
 #pragma unroll
         for (int c = 0; c < KG; ++c) {
+            if (!norm_thread) break;  // wave-uniform
             const int ci = threadIdx.x + 256 * c;
             const uint32_t wv[4] = {nw[c].x, nw[c].y, nw[c].z, nw[c].w};
             float yv[8];
@@ -212,20 +276,13 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
     float out[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        float part = 0.f;
+        float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < KG; ++j) {
-            const uint32_t words[4] = {w[r][j].x, w[r][j].y, w[r][j].z, w[r][j].w};
-            const uint32_t xw[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
-            int isum = -(int)((z[r][j] >> zsh[r][j]) & 15u) * xq[j];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                isum = dot4(words[c] & mask, xw[2 * c], isum);
-                isum = dot4((words[c] >> 4) & mask, xw[2 * c + 1], isum);
-            }
-            part = fmaf((float)isum, bf16_bits((uint16_t)s[r][j]) * xs[j], part);
+        for (int j = 0; j < KG; ++j) {  // lane l's group j lies in slice j
+            const float t = slice_sum(group_isum(w[r][j], xa[j], xb[j], z[r][j], zsh[r][j], xq[j], mask), s[r][j], xs[j]);
+            acc = j == 0 ? t : acc + t;
         }
-        out[r] = wave_sum(part);
+        out[r] = acc;
     }
     uint16_t val[R];
 #pragma unroll
@@ -259,24 +316,115 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : 256) void w4a8_gemv_kernel(
     }
 }
 
-template <bool PAIRED, bool QOUT>
-int launch_w4a8(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc, const void* zp,
-                void* y, void* oq, void* osx, void* osum, int K, int n_out, int rows, hipStream_t st) {
-    const int G = K / 32, KG = (G + kWave - 1) / kWave;
-    if (rows == 0) rows = QOUT ? 2 : 1;
-    if (QOUT && rows == 1) return (int)hipErrorInvalidValue;
-    const int waves = (n_out + rows - 1) / rows;
-    const int wpb = QOUT ? 32 / rows : 4;
-    const dim3 grid((waves + wpb - 1) / wpb), block(kWave * wpb);
-#define MOSS_W4A8(KGV, RV)                                                                                        \
-    if (KG == KGV && rows == RV) {                                                                                \
-        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, QOUT && RV != 1>), grid, block, 0, st,              \
-                           (const uint32_t*)qx, (const float*)sx, (const int*)qsum, (const uint4*)qw,             \
-                           (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, (uint8_t*)oq, (float*)osx,      \
-                           (int*)osum, G, n_out, W8Norm{});                                                       \
+// K-split GEMV: a workgroup of S = ceil(G / 64) waves owns R output rows (PAIRED: R gate and
+// the R matching up rows); wave w takes slice w of every row, lane l the group 64 w + l, so a
+// row's slices are read by S waves at once and the slice sums meet in LDS.  Against one wave per
+// row holding all KG groups per lane this keeps S times as many waves in flight on the same
+// bytes (K=12288, N=4096: 6.5 against 7.5 us).  QIN: the activations arrive as bf16 and each
+// lane quantizes its own group in registers while the weight loads are in flight, bit-identical
+// to int8_quantize_g32 and without its launch.
+template <int R, bool PAIRED, bool QIN>
+__global__ __launch_bounds__(kMaxSlices * kWave) void w4a8_ksplit_kernel(
+    const uint32_t* __restrict__ qx, const float* __restrict__ sx, const int* __restrict__ qsum,
+    const uint16_t* __restrict__ xb16, const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
+    const uint8_t* __restrict__ zp, uint16_t* __restrict__ y, int G, int n_out) {
+    constexpr int NR = PAIRED ? 2 * R : R;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int slice = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int g = kWave * slice + lane;
+    // The last slice may be partial: its dead lanes load group G - 1 (in bounds, no branch around
+    // the loads) and add +0 in slice_sum.
+    const bool live = g < G;
+    const int gc = min(g, G - 1);
+    const int row0 = blockIdx.x * R;
+    // activations first (completions are counted in order)
+    uint4 xa, xb, h[4];
+    float xs;
+    int xq;
+    if constexpr (QIN) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) h[c] = reinterpret_cast<const uint4*>(xb16 + 32 * gc)[c];
+    } else {
+        const uint4* p = reinterpret_cast<const uint4*>(qx + 8 * gc);
+        xa = p[0];
+        xb = p[1];
+        xs = sx[gc];
+        xq = qsum[gc];
+    }
+    uint4 w[NR];
+    uint32_t s[NR], z[NR], zsh[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int local = PAIRED ? (r % R) : r;
+        const size_t n = (size_t)(min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0));
+        const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(qw + n * G + gc));
+        w[r] = make_uint4(v.x, v.y, v.z, v.w);
+        s[r] = sc[n * G + gc];
+        int zb;
+        zero_loc(gc, G, zb, zsh[r]);
+        z[r] = zp[n * (G >> 1) + zb];
+    }
+    if constexpr (QIN) {
+        // every weight load is issued before the quantization waits for the activations
+        __builtin_amdgcn_sched_barrier(0);
+        quantize_group32(h, xa, xb, xs, xq);
+    }
+    uint32_t mask = 0x0F0F0F0Fu;
+    asm volatile("" : "+v"(mask));
+    __shared__ float part[kMaxSlices][NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const float t = slice_sum(group_isum(w[r], xa, xb, z[r], zsh[r], xq, mask), s[r], xs, live);
+        if (lane == 0) part[slice][r] = t;
+    }
+    __syncthreads();
+    const int t = threadIdx.x, S = blockDim.x / kWave;
+    if (t < R && row0 + t < n_out) {
+        float a = part[0][t], b = PAIRED ? part[0][R + t] : 0.f;
+        for (int i = 1; i < S; ++i) {
+            a += part[i][t];
+            if (PAIRED) b += part[i][R + t];
+        }
+        y[row0 + t] = PAIRED ? silu_mul_rounded_bits(a, b) : f32_to_bf16(a);
+    }
+}
+
+template <bool PAIRED, bool QIN>
+int launch_w4a8_ksplit(const void* qx, const void* sx, const void* qsum, const void* xb16, const void* qw,
+                       const void* sc, const void* zp, void* y, int K, int n_out, int rows, hipStream_t st) {
+    const int G = K / 32, S = (G + kWave - 1) / kWave;
+    if (S > kMaxSlices) return (int)hipErrorInvalidValue;
+    // measured: 4 rows for the 6-slice K=12288 down projection, 2 for K=4096 (O, q||k||v, gate||up)
+    const int R = rows ? rows : (!PAIRED && S >= 4 ? 4 : 2);
+    const dim3 grid((n_out + R - 1) / R), block(kWave * S);
+#define MOSS_W4A8K(RV)                                                                                            \
+    if (R == RV) {                                                                                                \
+        hipLaunchKernelGGL((w4a8_ksplit_kernel<RV, PAIRED, QIN>), grid, block, 0, st, (const uint32_t*)qx,         \
+                           (const float*)sx, (const int*)qsum, (const uint16_t*)xb16, (const uint4*)qw,           \
+                           (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, G, n_out);                      \
         return moss_launch_status();                                                                              \
     }
-#define MOSS_W4A8_R(KGV) MOSS_W4A8(KGV, 1) MOSS_W4A8(KGV, 2) MOSS_W4A8(KGV, 4)
+    MOSS_W4A8K(1) MOSS_W4A8K(2) MOSS_W4A8K(4)
+#undef MOSS_W4A8K
+    return (int)hipErrorInvalidValue;
+}
+
+// The paired gate||up with its output quantized (32 output rows per workgroup).
+int launch_w4a8_qout(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc, const void* zp,
+                     void* y, void* oq, void* osx, void* osum, int K, int n_out, int rows, hipStream_t st) {
+    const int G = K / 32, KG = (G + kWave - 1) / kWave;
+    if (rows == 0) rows = 2;
+    const int wpb = 32 / rows;
+    const dim3 grid((n_out + 31) / 32), block(kWave * wpb);
+#define MOSS_W4A8(KGV, RV)                                                                                        \
+    if (KG == KGV && rows == RV) {                                                                                \
+        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, true, true>), grid, block, 0, st, (const uint32_t*)qx,       \
+                           (const float*)sx, (const int*)qsum, (const uint4*)qw, (const uint16_t*)sc,             \
+                           (const uint8_t*)zp, (uint16_t*)y, (uint8_t*)oq, (float*)osx, (int*)osum, G, n_out,     \
+                           W8Norm{});                                                                             \
+        return moss_launch_status();                                                                              \
+    }
+#define MOSS_W4A8_R(KGV) MOSS_W4A8(KGV, 2) MOSS_W4A8(KGV, 4)
     MOSS_W4A8_R(1) MOSS_W4A8_R(2) MOSS_W4A8_R(3) MOSS_W4A8_R(4) MOSS_W4A8_R(5) MOSS_W4A8_R(6) MOSS_W4A8_R(7)
     MOSS_W4A8_R(8)
 #undef MOSS_W4A8_R
@@ -284,28 +432,32 @@ int launch_w4a8(const void* qx, const void* sx, const void* qsum, const void* qw
     return (int)hipErrorInvalidValue;
 }
 
-// K = 2048 KG, KG in {1, 2, 4} (K = 2048, 4096, 8192).
+// K = 2048 KG, KG in {1, 2, 4} (K = 2048, 4096, 8192).  8-wave workgroups once there are at
+// least 2048 waves (the q||k||v projection at 2 rows per wave), else 4.
 template <bool PAIRED>
 int launch_w4a8_norm(const W8Norm& nm, const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
                      int rows, hipStream_t st) {
     const int G = K / 32, KG = K / 2048;
     if (rows == 0) rows = 1;
     const int waves = (n_out + rows - 1) / rows;
-    const dim3 grid((waves + 3) / 4), block(256);
-#define MOSS_W4A8N(KGV, RV, ACTV)                                                                                 \
-    if (KG == KGV && rows == RV) {                                                                                \
-        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, false, ACTV>), grid, block, 0, st, nullptr,         \
+    const int wpb = waves >= 2048 ? 8 : 4;
+    const dim3 grid((waves + wpb - 1) / wpb), block(kWave * wpb);
+#define MOSS_W4A8N(KGV, RV, ACTV, WV)                                                                             \
+    if (KG == KGV && rows == RV && wpb == WV) {                                                                   \
+        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, false, ACTV, WV>), grid, block, 0, st, nullptr,     \
                            nullptr, nullptr, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,           \
                            (uint16_t*)y, nullptr, nullptr, nullptr, G, n_out, nm);                                \
         return moss_launch_status();                                                                              \
     }
-#define MOSS_W4A8N_R(KGV, ACTV) MOSS_W4A8N(KGV, 1, ACTV) MOSS_W4A8N(KGV, 2, ACTV) MOSS_W4A8N(KGV, 4, ACTV)
+#define MOSS_W4A8N_W(KGV, RV, ACTV) MOSS_W4A8N(KGV, RV, ACTV, 4) MOSS_W4A8N(KGV, RV, ACTV, 8)
+#define MOSS_W4A8N_R(KGV, ACTV) MOSS_W4A8N_W(KGV, 1, ACTV) MOSS_W4A8N_W(KGV, 2, ACTV) MOSS_W4A8N_W(KGV, 4, ACTV)
     if (nm.res) {
         MOSS_W4A8N_R(1, 2) MOSS_W4A8N_R(2, 2) MOSS_W4A8N_R(4, 2)
     } else {
         MOSS_W4A8N_R(1, 1) MOSS_W4A8N_R(2, 1) MOSS_W4A8N_R(4, 1)
     }
 #undef MOSS_W4A8N_R
+#undef MOSS_W4A8N_W
 #undef MOSS_W4A8N
     return (int)hipErrorInvalidValue;
 }
@@ -336,8 +488,17 @@ MOSS_API int moss_w4a8_gemv(const void* qx, const void* sx, const void* qsum, co
                             const void* zp, void* y, int K, int N, int rows_per_wave, void* stream) {
     if (int rc = check_w4a8(qx, sx, qsum, qw, sc, zp, y, K, rows_per_wave)) return rc;
     MOSS_CHECK_ARG(N > 0);
-    return launch_w4a8<false, false>(qx, sx, qsum, qw, sc, zp, y, nullptr, nullptr, nullptr, K, N, rows_per_wave,
-                                     (hipStream_t)stream);
+    return launch_w4a8_ksplit<false, false>(qx, sx, qsum, nullptr, qw, sc, zp, y, K, N, rows_per_wave,
+                                            (hipStream_t)stream);
+}
+
+MOSS_API int moss_w4a8_quant_gemv(const void* x, const void* qw, const void* sc, const void* zp, void* y, int K, int N,
+                                  int rows_per_wave, void* stream) {
+    MOSS_CHECK_ARG(x && qw && sc && zp && y && K > 0 && K % 64 == 0 && K <= 16384 && N > 0);
+    MOSS_CHECK_ARG(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4);
+    MOSS_CHECK_ARG(MOSS_ALIGNED(x, 16) && MOSS_ALIGNED(qw, 16));
+    return launch_w4a8_ksplit<false, true>(nullptr, nullptr, nullptr, x, qw, sc, zp, y, K, N, rows_per_wave,
+                                           (hipStream_t)stream);
 }
 
 MOSS_API int moss_w4a8_gateup_silu(const void* qx, const void* sx, const void* qsum, const void* qw, const void* sc,
@@ -348,12 +509,12 @@ MOSS_API int moss_w4a8_gateup_silu(const void* qx, const void* sx, const void* q
     const bool quant = out_qx != nullptr;
     MOSS_CHECK_ARG(quant == (out_sx != nullptr) && quant == (out_qsum != nullptr));
     if (!quant)
-        return launch_w4a8<true, false>(qx, sx, qsum, qw, sc, zp, y, nullptr, nullptr, nullptr, K, N_half,
-                                        rows_per_wave, (hipStream_t)stream);
+        return launch_w4a8_ksplit<true, false>(qx, sx, qsum, nullptr, qw, sc, zp, y, K, N_half, rows_per_wave,
+                                               (hipStream_t)stream);
     MOSS_CHECK_ARG(N_half % 32 == 0 && rows_per_wave != 1);
     MOSS_CHECK_ARG(MOSS_ALIGNED(out_sx, 4) && MOSS_ALIGNED(out_qsum, 4));
-    return launch_w4a8<true, true>(qx, sx, qsum, qw, sc, zp, y, out_qx, out_sx, out_qsum, K, N_half,
-                                   rows_per_wave, (hipStream_t)stream);
+    return launch_w4a8_qout(qx, sx, qsum, qw, sc, zp, y, out_qx, out_sx, out_qsum, K, N_half, rows_per_wave,
+                            (hipStream_t)stream);
 }
 
 static int w4a8_norm_entry(bool paired, const void* x, const void* res, const void* norm_w, void* sum_out, float eps,

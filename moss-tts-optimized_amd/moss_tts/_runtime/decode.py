@@ -11,7 +11,7 @@ bf16 for an installed model, as the reference keeps them, or INT4-G32 for the sy
 arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
 ``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer + q||k||v (one
 kernel) -> attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer ->
-gate||up with SiLU*mul -> int8 quantizer -> down
+gate||up with SiLU*mul -> int8 quantizer + down (one kernel)
 (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
 The heads matrix holds the 32 audio heads (``audio_stride`` rows each, the first 1024 sampled)
 followed by the 2 text-head rows (gen slot, delay slot; ``llm.py:190-191``); the step ends with the
@@ -227,21 +227,23 @@ class DecodeStepG32:
         mlp = None
         for i, layer in enumerate(self.layers):
             state = (residual.clone(), None if mlp is None else mlp.clone()) if trace is not None else None
-            # add-RMSNorm + quantizer + q||k||v in one kernel, two rows per wave (fewer workgroups
-            # repeat the normalization); measured faster than the separate norm_quant here
+            # add-RMSNorm + quantizer + q||k||v in one kernel, one row per wave in 8-wave workgroups
+            # (768 workgroups repeat the normalization); measured faster than two rows per wave and
+            # than the separate norm_quant in front of the K-split projection
             if i == 0:
-                qkv = w4a8.norm_linear(x, layer.input_norm, eps, layer.qkv.packed, rows_per_wave=2)
+                qkv = w4a8.norm_linear(x, layer.input_norm, eps, layer.qkv.packed, rows_per_wave=1)
             else:
                 residual, qkv = w4a8.norm_linear(mlp, layer.input_norm, eps, layer.qkv.packed, residual=residual,
-                                                 rows_per_wave=2)
+                                                 rows_per_wave=1)
             attn, act = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
                                                        self.keys[i], self.values[i], self.position, eps, ws=self.ws,
                                                        quantize=True)
             o = w4a8.linear(None, layer.o.packed, prequantized=act)
             # gate/up: the separate add-RMSNorm + quantizer is faster than the fused form here
             # (3072 workgroups would each repeat the normalization); the SiLU*mul output is
-            # quantized by the standalone quantizer, faster than the gate/up's fused output
-            # quantizer (its 32-row workgroups hold fewer rows in flight)
+            # quantized inside the down projection's kernel (each lane its own group of 32), faster
+            # than the gate/up's fused output quantizer (its 32-row workgroups hold fewer rows in
+            # flight) and than a separate quantizer launch
             residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
             hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)

@@ -63,6 +63,7 @@ SIGNATURES: dict[str, list] = {
     "moss_int8_quantize_g32": [_P, _P, _P, _P, _I, _P],
     "moss_rmsnorm_quant_g32": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
     "moss_w4a8_gemv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "moss_w4a8_quant_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4a8_gateup_silu": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4a8_norm_gemv": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _P],
     "moss_w4a8_norm_gateup_silu": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _P],

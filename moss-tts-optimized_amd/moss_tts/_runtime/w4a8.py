@@ -139,6 +139,9 @@ def linear(x: torch.Tensor | None, w: PackedW4G32, *, paired: bool = False, fuse
     """W4A8 decode projection of one row: ``y[n] = bf16(sum_g f32(isum[n,g]) * (s[n,g] * sx[g]))``
     with ``isum`` the exact integer dot of the group's codes (minus zero point) and int8 ``x``.
 
+    A bf16 ``x`` without ``prequantized`` is quantized inside the projection's kernel (the
+    paired form quantizes it first), bit-identical to ``quantize`` then the prequantized call.
+
     ``paired``: ``w`` holds gate rows then up rows; returns ``bf16(bf16(silu(gate)) * up)``.
     ``fused`` (paired only, N/2 % 32 == 0): also returns that output quantized,
     ``(y, activation)`` (``src/moss_tts/_runtime/dp4a_scaled.py:70-78``)."""
@@ -147,10 +150,14 @@ def linear(x: torch.Tensor | None, w: PackedW4G32, *, paired: bool = False, fuse
     _require(k % 64 == 0 and k <= _MAX_K, f"W4A8 GEMV supports K % 64 == 0 and K <= {_MAX_K}")
     _require(rows_per_wave in (0, 1, 2, 4), "rows_per_wave must be 0 (auto), 1, 2 or 4")
     _require(not fused or paired, "fused output quantization requires the paired gate/up form")
+    # the plain projection of a bf16 row quantizes inside its own kernel (one launch)
+    quant_inside = prequantized is None and not paired
     if prequantized is None:
         _require(x is not None, "x or prequantized is required")
         _require(x.numel() == k, f"one contiguous bf16 row of {k} values required, got shape {tuple(x.shape)}")
-        a = quantize(x)
+        _cuda_contig("x", x, torch.bfloat16, w.device)
+        _require(_aligned(x, 16), "x must be 16-byte aligned")
+        a = None if quant_inside else quantize(x)
     else:
         a = prequantized
         _check_activation(a, k, w.device)
@@ -165,6 +172,10 @@ def linear(x: torch.Tensor | None, w: PackedW4G32, *, paired: bool = False, fuse
         _cuda_contig("out", out, torch.bfloat16, w.device)
         _require(out.numel() == n_out, f"out must hold {n_out} values")
     stream = native.stream_of(out)
+    if quant_inside:
+        native.call("moss_w4a8_quant_gemv", native.ptr(x), native.ptr(w.qw), native.ptr(w.scales),
+                    native.ptr(w.zeros), native.ptr(out), k, n_out, rows_per_wave, stream)
+        return out
     if not paired:
         native.call("moss_w4a8_gemv", native.ptr(a.qx), native.ptr(a.scales), native.ptr(a.sums), native.ptr(w.qw),
                     native.ptr(w.scales), native.ptr(w.zeros), native.ptr(out), k, n_out, rows_per_wave, stream)

@@ -110,6 +110,10 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_rmsnorm_quant_g32(p, null, p, null, null, p, p, p, 1, 4112, ctypes.c_float(1e-6), null) == 1
     assert lib.moss_w4a8_gemv(p, p, p, p, p, p, p, 4128, 64, 0, null) == 1                # K % 64
     assert lib.moss_w4a8_gemv(p, p, p, odd, p, p, p, 4096, 64, 0, null) == 1              # weight alignment
+    assert lib.moss_w4a8_quant_gemv(p, p, p, p, p, 4128, 64, 0, null) == 1                 # K % 64
+    assert lib.moss_w4a8_quant_gemv(p, p, p, p, p, 16448, 64, 0, null) == 1                # K <= 16384
+    assert lib.moss_w4a8_quant_gemv(odd, p, p, p, p, 4096, 64, 0, null) == 1                # x alignment
+    assert lib.moss_w4a8_quant_gemv(p, p, p, p, p, 4096, 64, 3, null) == 1                  # rows_per_wave
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, null, p, 4096, 64, 0, null) == 1   # partial outputs
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, p, p, 4096, 48, 0, null) == 1      # N_half % 32
     assert lib.moss_w4a8_gateup_silu(p, p, p, p, p, p, p, p, p, p, 4096, 64, 1, null) == 1      # fused rows 2|4

@@ -125,8 +125,11 @@ def _oracle_rows(act, q, z, s):
 
 
 @pytest.mark.parametrize("k,n,rows", [(64, 37, 0), (4096, 6144, 0), (4096, 4096, 1), (4096, 4096, 2),
-                                      (12288, 4096, 0), (12288, 4096, 4), (2048, 100, 4)])
+                                      (12288, 4096, 0), (12288, 4096, 4), (2048, 100, 4), (2112, 99, 0),
+                                      (6208, 45, 2), (16384, 130, 0)])
 def test_gemv_vs_oracle(dev, k, n, rows):
+    """One workgroup per R rows, its ceil(K / 2048) waves splitting K (the last slice partial for
+    K = 2112 and 6208, the widest K = 16384 with 8 waves)."""
     from moss_tts._runtime import w4a8
 
     print(f"w4a8 gemv K={k} N={n} rows={rows}", flush=True)
@@ -140,8 +143,11 @@ def test_gemv_vs_oracle(dev, k, n, rows):
     y64, mag = _oracle_rows(act, q, z, s)
     _assert_rne_or_adjacent(y, torch.from_numpy(y64.astype(np.float32)), torch.from_numpy(mag), k,
                             f"w4a8 gemv K={k} N={n}")
-    # quantize-inside form gives the same bits
+    # quantize-inside form (one kernel) gives the same bits
     assert torch.equal(_bits(w4a8.linear(x.to(dev), pw, rows_per_wave=rows)), _bits(y))
+    # and so does every row count per workgroup: the combine order does not depend on it
+    for r in (1, 2, 4):
+        assert torch.equal(_bits(w4a8.linear(None, pw, prequantized=act, rows_per_wave=r)), _bits(y)), r
 
 
 @pytest.mark.parametrize("k,n_half,fused", [(4096, 12288, True), (4096, 12288, False), (2048, 64, True),
@@ -203,6 +209,8 @@ def test_w4a8_mlp_chain_matches_oracle_chain(dev):
     summed, y, act = w4a8.norm_quant(x, r, w, 1e-6)
     mid, mid_act = w4a8.linear(None, gu, paired=True, fused=True, prequantized=act)
     out = w4a8.linear(None, down, prequantized=mid_act)
+    # the down projection quantizing its bf16 input inside its own kernel: the same bits
+    assert torch.equal(_bits(w4a8.linear(mid, down)), _bits(out))
     torch.cuda.synchronize()
     _check_activation(act, y.cpu(), "norm")
     _check_activation(mid_act, mid.cpu(), "gate/up output")
