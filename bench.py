@@ -586,7 +586,7 @@ def decode_budget(torch, n_layers: int, steps: int, dev, w4a8: bool = False) -> 
              lambda *a, **kw: w8_k(a, kw) == 4096 and not kw.get("paired"), n_layers, (1,)),
             ("add-RMSNorm + int8 quantizer", w8, "norm_quant", lambda *a, **kw: True, n_layers, ()),
             ("gate||up GEMV + SiLU*mul", w8, "linear", lambda *a, **kw: bool(kw.get("paired")), n_layers, (1,)),
-            ("int8 quantizer + down GEMV (K=12288)", w8, "linear", lambda *a, **kw: w8_k(a, kw) == 12288,
+            ("down GEMV (K=12288) quantizing its bf16 input inside", w8, "linear", lambda *a, **kw: w8_k(a, kw) == 12288,
              n_layers, (1,)),
         ]
     else:
