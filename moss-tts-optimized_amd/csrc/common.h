@@ -119,18 +119,26 @@ __device__ __forceinline__ float g32_scale(float absmax) { return fmaxf(absmax /
 // Quantize 8 consecutive values into two words in dot4 order: bytes 0..7 hold
 // q[0], q[4], q[1], q[5], q[2], q[6], q[3], q[7] -- the order in which (w & 0x0F0F0F0F)
 // and ((w >> 4) & 0x0F0F0F0F) expand a row-packed INT4 code word.  Returns the code sum.
+// q = rint(v * inv) for inv = RN(1 / scale) of the group's scale (so |v * inv| <= 127 (1 + 3 *
+// 2^-24) and |q| <= 127): the product is rounded on its own (kept opaque, so it is not fused
+// into the add), then adding 1.5 * 2^23 rounds it to the nearest integer, ties to even, and
+// leaves q in the low byte of the result; two byte permutes pack four codes, and the code sum is
+// a dot4 of the packed codes with ones.
+__device__ __forceinline__ uint32_t pack4_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | (__builtin_amdgcn_perm(d, c, 0x0c0c0400u) << 16);
+}
+
 __device__ __forceinline__ int quantize8_dot4(const float* v, float inv, uint32_t& lo, uint32_t& hi) {
-    int q[8], sum = 0;
+    uint32_t t[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        q[i] = (int)rintf(v[i] * inv);
-        sum += q[i];
+        float prod = v[i] * inv;
+        asm volatile("" : "+v"(prod));
+        t[i] = __float_as_uint(prod + 12582912.0f);
     }
-    lo = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[4] & 0xff) << 8 | (uint32_t)(q[1] & 0xff) << 16 |
-         (uint32_t)(q[5] & 0xff) << 24;
-    hi = (uint32_t)(q[2] & 0xff) | (uint32_t)(q[6] & 0xff) << 8 | (uint32_t)(q[3] & 0xff) << 16 |
-         (uint32_t)(q[7] & 0xff) << 24;
-    return sum;
+    lo = pack4_low_bytes(t[0], t[4], t[1], t[5]);
+    hi = pack4_low_bytes(t[2], t[6], t[3], t[7]);
+    return __builtin_amdgcn_sdot4((int)hi, 0x01010101, __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false), false);
 }
 
 // Byte offset, within its 8-value block, of value t in dot4 order.
