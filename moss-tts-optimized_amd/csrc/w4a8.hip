@@ -133,7 +133,7 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : kWave * WPB) void w4a8_gemv
     uint16_t* __restrict__ y, uint8_t* __restrict__ oq, float* __restrict__ osx, int* __restrict__ osum, int G,
     int n_out, W8Norm nm) {
     static_assert(!QOUT || (PAIRED && (R == 2 || R == 4)), "output quantization covers 32 paired rows");
-    static_assert(ACT == 0 || !QOUT, "the fused normalization runs with 256-thread workgroups");
+    static_assert(ACT == 0 || !QOUT, "a fused normalization and a fused output quantizer are separate forms");
     static_assert(QOUT || ACT > 0, "the plain projections run on w4a8_ksplit_kernel");
     static_assert(WPB == 4 || (WPB == 8 && ACT > 0), "8-wave workgroups for the fused normalization only");
     // the threads that form the normalized activations (wave-uniform)
