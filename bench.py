@@ -579,13 +579,14 @@ def decode_budget(torch, n_layers: int, steps: int, dev, w4a8: bool = False) -> 
             return (a[1] if len(a) > 1 else kw["w"]).K
 
         layer_families = [
-            ("add-RMSNorm + int8 quantizer + q||k||v GEMV", w8, "norm_linear", lambda *a, **kw: True, n_layers, (3,)),
+            ("add-RMSNorm + int8 quantizer + q||k||v GEMV", w8, "norm_linear", lambda *a, **kw: not kw.get("paired"),
+             n_layers, (3,)),
             ("q/k-norm + RoPE + KV write + attention split + merge with int8 output", attention,
              "decode_attention_qkv", lambda *a, **kw: True, n_layers, (5, 6)),
             ("O GEMV (K=4096, int8 input from the merge)", w8, "linear",
              lambda *a, **kw: w8_k(a, kw) == 4096 and not kw.get("paired"), n_layers, (1,)),
-            ("add-RMSNorm + int8 quantizer", w8, "norm_quant", lambda *a, **kw: True, n_layers, ()),
-            ("gate||up GEMV + SiLU*mul", w8, "linear", lambda *a, **kw: bool(kw.get("paired")), n_layers, (1,)),
+            ("add-RMSNorm + int8 quantizer + gate||up GEMV + SiLU*mul", w8, "norm_linear",
+             lambda *a, **kw: bool(kw.get("paired")), n_layers, (3,)),
             ("down GEMV (K=12288) quantizing its bf16 input inside", w8, "linear", lambda *a, **kw: w8_k(a, kw) == 12288,
              n_layers, (1,)),
         ]
@@ -803,13 +804,12 @@ def main() -> int:
     unr_s = _time_graph(torch, g_unr, max(1, args.steps // cycle)) / cycle
 
     # the same MLP step in the W4A8 arithmetic, as the decode step runs it: RMSNorm + int8
-    # quantizer, gate||up with SiLU*mul, the quantizer and down
+    # quantizer + gate||up with SiLU*mul in one kernel, then the quantizer + down in one kernel
     def steps_w4a8(count: int):
         def run():
             for i in range(count):
                 gu, dn = copies[i % len(copies)]
-                _, _, act = w4a8.norm_quant(h, None, norm_w, 1e-6, normalized=False)
-                mid = w4a8.linear(None, gu, paired=True, prequantized=act)
+                mid = w4a8.norm_linear(h, norm_w, 1e-6, gu, paired=True, rows_per_wave=2)
                 w4a8.linear(mid, dn)
         return run
 

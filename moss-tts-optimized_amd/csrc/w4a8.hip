@@ -106,11 +106,12 @@ __global__ __launch_bounds__(256) void int8_quantize_g32(const uint16_t* __restr
 
 // The fused normalization in front of a W4A8 projection (ACT 1: RMSNorm, ACT 2: add-RMSNorm;
 // src/moss_tts/_runtime/dp4a_norm_projection.py:48-96, dp4a_fusions.py:24-61): every
-// 256-thread workgroup recomputes y = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * w) of the one
-// K-wide row (s = x, or bf16(x + res), which workgroup 0 also stores) and its int8 groups of 32
-// into LDS while its weight rows are in flight.  Thread t owns the 8-value chunks t + 256 c and
-// the 4 chunks of a group sit in one DPP quad, with the summation order and rounding points of
-// rmsnorm_rows<RESIDUAL, true>, so the activations are bit-identical to moss_rmsnorm_quant_g32's.
+// workgroup recomputes y = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * w) of the one K-wide row
+// (s = x, or bf16(x + res), which workgroup 0 also stores) and its int8 groups of 32 into LDS
+// with its first 256 threads, while its weight rows are in flight.  Thread t owns the 8-value
+// chunks t + 256 c (c < KG = K / 2048) and the 4 chunks of a group sit in one DPP quad, with the
+// summation order and rounding points of rmsnorm_rows<RESIDUAL, true>, so the activations are
+// bit-identical to moss_rmsnorm_quant_g32's.
 struct W8Norm {
     const uint16_t* __restrict__ x;
     const uint16_t* __restrict__ res;
@@ -119,67 +120,196 @@ struct W8Norm {
     float eps;
 };
 
-// Row-per-wave GEMV (the forms with a fused normalization or output quantizer): lane l owns
-// groups l + 64 j; KG = ceil(G / 64).  QOUT (paired only):
-// 32 / R waves x R rows per workgroup cover one 32-row output group, which the workgroup
-// also quantizes (the down projection's activations), as the reference's fused gate/up does
-// (src/moss_tts/_runtime/dp4a_scaled.py:70-78).  ACT 0 reads quantized activations; ACT 1 and
-// 2 form them in the workgroup (W8Norm; K = 2048 KG) with its first 256 threads, then all WPB
-// waves of the workgroup take their rows (8 waves halve the workgroups that repeat the norm).
-template <int KG, int R, bool PAIRED, bool QOUT, int ACT = 0, int WPB = 4>
-__global__ __launch_bounds__(QOUT ? kWave * 32 / R : kWave * WPB) void w4a8_gemv_kernel(
+template <int KG>
+struct W8NormLoad {
+    uint4 x[KG], r[KG], w[KG];
+};
+
+// Issued before the weight loads (completions are counted in order); threads >= 256 load nothing.
+template <int KG, int ACT>
+__device__ __forceinline__ void w8norm_load(W8NormLoad<KG>& nl, const W8Norm& nm) {
+    const int t = threadIdx.x;
+    if (t >= 256) return;  // wave-uniform
+#pragma unroll
+    for (int c = 0; c < KG; ++c) {
+        const int ci = t + 256 * c;
+        nl.w[c] = reinterpret_cast<const uint4*>(nm.w)[ci];
+        nl.x[c] = reinterpret_cast<const uint4*>(nm.x)[ci];
+        if constexpr (ACT == 2) nl.r[c] = reinterpret_cast<const uint4*>(nm.res)[ci];
+    }
+}
+
+// The normalized row quantized into LDS: lq[2 g .. 2 g + 1] (16 bytes) the codes of group g in
+// dot4 order, lsx[g] its scale, lsum[g] its code sum.  Every thread of the workgroup calls it
+// (two barriers).
+template <int KG, int ACT>
+__device__ __forceinline__ void w8norm_into_lds(const W8NormLoad<KG>& nl, const W8Norm& nm, uint2* lq, float* lsx,
+                                                int* lsum, float* red, int G) {
+    const int t = threadIdx.x, lane = t & (kWave - 1);
+    const bool active = t < 256;  // wave-uniform
+    float v[KG][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < KG; ++c) {
+        if (!active) break;
+        const int ci = t + 256 * c;
+        uint32_t sw[4] = {nl.x[c].x, nl.x[c].y, nl.x[c].z, nl.x[c].w};
+        if constexpr (ACT == 2) {
+            const uint32_t bw[4] = {nl.r[c].x, nl.r[c].y, nl.r[c].z, nl.r[c].w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                sw[p] = pack_bf16x2(bf16_lo(sw[p]) + bf16_lo(bw[p]), bf16_hi(sw[p]) + bf16_hi(bw[p]));
+            if (blockIdx.x == 0) reinterpret_cast<uint4*>(nm.sum_out)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            v[c][2 * p] = bf16_lo(sw[p]);
+            v[c][2 * p + 1] = bf16_hi(sw[p]);
+            ss = fmaf(v[c][2 * p], v[c][2 * p], ss);
+            ss = fmaf(v[c][2 * p + 1], v[c][2 * p + 1], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0 && active) red[t / kWave] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) total += red[i];
+    const float inv = rsqrtf(total / (float)(32 * G) + nm.eps);
+#pragma unroll
+    for (int c = 0; c < KG; ++c) {
+        if (!active) break;
+        const int ci = t + 256 * c;
+        const uint32_t wv[4] = {nl.w[c].x, nl.w[c].y, nl.w[c].z, nl.w[c].w};
+        float yv[8];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
+            const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
+            const uint32_t o = pack_bf16x2(a, b);
+            yv[2 * p] = bf16_lo(o);
+            yv[2 * p + 1] = bf16_hi(o);
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(yv[i]));
+        const float scale = g32_scale(quad_max(m));
+        uint32_t lo, hi;
+        const int part = quantize8_dot4(yv, 1.0f / scale, lo, hi);
+        const float gsum = quad_sum((float)part);  // |sum| <= 32 * 127: exact in fp32
+        lq[ci] = make_uint2(lo, hi);
+        if ((ci & 3) == 0) {
+            lsx[ci / 4] = scale;
+            lsum[ci / 4] = (int)gsum;
+        }
+    }
+    __syncthreads();
+}
+
+// The fused (add+)RMSNorm + quantizer + projection with K split: 8 waves per workgroup, KG
+// slices of 64 groups (K = 2048 KG) times 8 / KG row groups of R rows (PAIRED: R gate and the R
+// matching up rows); wave (slice, row group) takes the slice's groups of its rows, one per lane,
+// and reads only its own group of the quantized row from LDS.  The slice sums meet in LDS and are
+// added in slice order.  Against one wave per row holding the whole K (the same 8 rows per
+// workgroup) the q||k||v projection goes from 6.0-6.3 to 5.3 us and the W4A8 decode step from
+// 1.61 to 1.57 ms.
+template <int KG, int R, bool PAIRED, int ACT>
+__global__ __launch_bounds__(512) void w4a8_ksplit_norm_kernel(const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
+                                                               const uint8_t* __restrict__ zp, uint16_t* __restrict__ y,
+                                                               int G, int n_out, W8Norm nm) {
+    static_assert(KG == 1 || KG == 2 || KG == 4, "K = 2048, 4096 or 8192");
+    constexpr int S = KG, RG = 8 / KG, NR = PAIRED ? 2 * R : R;
+    const int t = threadIdx.x, lane = t & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int slice = w % S, rg = w / S;
+    const int g = kWave * slice + lane;  // G = 64 KG: every lane's group exists
+    const int rbase = blockIdx.x * RG * R, row0 = rbase + rg * R;
+    W8NormLoad<KG> nl;
+    w8norm_load<KG, ACT>(nl, nm);
+    uint4 wv[NR];
+    uint32_t s[NR], z[NR], zsh[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int local = PAIRED ? (r % R) : r;
+        const size_t n = (size_t)(min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0));
+        const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(qw + n * G + g));
+        wv[r] = make_uint4(v.x, v.y, v.z, v.w);
+        s[r] = sc[n * G + g];
+        int zb;
+        zero_loc(g, G, zb, zsh[r]);
+        z[r] = zp[n * (G >> 1) + zb];
+    }
+    __shared__ uint2 lq[256 * KG];
+    __shared__ float lsx[64 * KG];
+    __shared__ int lsum[64 * KG];
+    __shared__ float red[4];
+    __shared__ float part[S][RG * NR];
+    w8norm_into_lds<KG, ACT>(nl, nm, lq, lsx, lsum, red, G);
+    const uint4* p4 = reinterpret_cast<const uint4*>(lq) + 2 * g;
+    const uint4 xa = p4[0], xb = p4[1];
+    const float xs = lsx[g];
+    const int xq = lsum[g];
+    uint32_t mask = 0x0F0F0F0Fu;
+    asm volatile("" : "+v"(mask));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const float v = slice_sum(group_isum(wv[r], xa, xb, z[r], zsh[r], xq, mask), s[r], xs);
+        if (lane == 0) part[slice][rg * NR + r] = v;
+    }
+    __syncthreads();
+    if (t < RG * R && rbase + t < n_out) {
+        const int pr = (t / R) * NR + t % R;  // row group t / R, local row t % R
+        float a = part[0][pr], b = PAIRED ? part[0][pr + R] : 0.f;
+#pragma unroll
+        for (int i = 1; i < S; ++i) {
+            a += part[i][pr];
+            if constexpr (PAIRED) b += part[i][pr + R];
+        }
+        y[rbase + t] = PAIRED ? silu_mul_rounded_bits(a, b) : f32_to_bf16(a);
+    }
+}
+
+// The paired gate||up GEMV with its output quantized for the next projection, row per wave:
+// lane l owns groups l + 64 j (KG = ceil(G / 64)); 32 / R waves x R rows per workgroup cover
+// one 32-row output group, which the workgroup also quantizes, as the reference's fused gate/up
+// does (src/moss_tts/_runtime/dp4a_scaled.py:70-78).
+template <int KG, int R>
+__global__ __launch_bounds__(kWave * 32 / R) void w4a8_gemv_kernel(
     const uint32_t* __restrict__ qx, const float* __restrict__ sx, const int* __restrict__ qsum,
     const uint4* __restrict__ qw, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     uint16_t* __restrict__ y, uint8_t* __restrict__ oq, float* __restrict__ osx, int* __restrict__ osum, int G,
-    int n_out, W8Norm nm) {
-    static_assert(!QOUT || (PAIRED && (R == 2 || R == 4)), "output quantization covers 32 paired rows");
-    static_assert(ACT == 0 || !QOUT, "a fused normalization and a fused output quantizer are separate forms");
-    static_assert(QOUT || ACT > 0, "the plain projections run on w4a8_ksplit_kernel");
-    static_assert(WPB == 4 || (WPB == 8 && ACT > 0), "8-wave workgroups for the fused normalization only");
-    // the threads that form the normalized activations (wave-uniform)
-    const bool norm_thread = WPB == 4 || threadIdx.x < 256;
+    int n_out) {
+    static_assert(R == 2 || R == 4, "output quantization covers 32 paired rows");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave));
     const int row0 = wave * R;
-    // QOUT grids hold whole groups only, and with ACT > 0 every wave takes part in the
-    // workgroup's normalization first: no wave leaves early
-    constexpr int NR = PAIRED ? 2 * R : R;
+    // the grid holds whole 32-row groups (N_half % 32 == 0): no wave leaves early
+    constexpr int NR = 2 * R;
     // activations first (completions are counted in order): 32 int8 per group, its scale and sum
     uint4 xa[KG], xb[KG];
     float xs[KG];
     int xq[KG];
-    uint4 nx[KG], nr[KG], nw[KG];  // ACT > 0: the chunks t + 256 c of x, res and the norm weight
-    if constexpr (ACT == 0) {
 #pragma unroll
-        for (int j = 0; j < KG; ++j) {
-            const int g = lane + kWave * j;
-            if (g < G) {
-                const uint4* p = reinterpret_cast<const uint4*>(qx + 8 * g);
-                xa[j] = p[0];
-                xb[j] = p[1];
-                xs[j] = sx[g];
-                xq[j] = qsum[g];
-            } else {
-                xa[j] = xb[j] = make_uint4(0u, 0u, 0u, 0u);
-                xs[j] = 0.f;
-                xq[j] = 0;
-            }
-        }
-    } else if (norm_thread) {
-#pragma unroll
-        for (int c = 0; c < KG; ++c) {
-            const int ci = threadIdx.x + 256 * c;
-            nw[c] = reinterpret_cast<const uint4*>(nm.w)[ci];
-            nx[c] = reinterpret_cast<const uint4*>(nm.x)[ci];
-            if constexpr (ACT == 2) nr[c] = reinterpret_cast<const uint4*>(nm.res)[ci];
+    for (int j = 0; j < KG; ++j) {
+        const int g = lane + kWave * j;
+        if (g < G) {
+            const uint4* p = reinterpret_cast<const uint4*>(qx + 8 * g);
+            xa[j] = p[0];
+            xb[j] = p[1];
+            xs[j] = sx[g];
+            xq[j] = qsum[g];
+        } else {
+            xa[j] = xb[j] = make_uint4(0u, 0u, 0u, 0u);
+            xs[j] = 0.f;
+            xq[j] = 0;
         }
     }
     uint4 w[NR][KG];
     uint32_t s[NR][KG], z[NR][KG], zsh[NR][KG];  // z: the raw byte holding the zero point at bit zsh
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const int local = PAIRED ? (r % R) : r;
-        const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
+        const int local = r % R;
+        const int n = min(row0 + local, n_out - 1) + (r >= R ? n_out : 0);
 #pragma unroll
         for (int j = 0; j < KG; ++j) {
             const int g = lane + kWave * j;
@@ -198,79 +328,6 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : kWave * WPB) void w4a8_gemv
             }
         }
     }
-    if constexpr (ACT > 0) {
-        __shared__ uint2 lq[256 * KG];
-        __shared__ float lsx[64 * KG];
-        __shared__ int lsum[64 * KG];
-        __shared__ float red[4];
-        float v[KG][8];
-        float ss = 0.f;
-#pragma unroll
-        for (int c = 0; c < KG; ++c) {
-            if (!norm_thread) break;  // wave-uniform
-            const int ci = threadIdx.x + 256 * c;
-            uint32_t sw[4] = {nx[c].x, nx[c].y, nx[c].z, nx[c].w};
-            if constexpr (ACT == 2) {
-                const uint32_t bw[4] = {nr[c].x, nr[c].y, nr[c].z, nr[c].w};
-#pragma unroll
-                for (int p = 0; p < 4; ++p)
-                    sw[p] = pack_bf16x2(bf16_lo(sw[p]) + bf16_lo(bw[p]), bf16_hi(sw[p]) + bf16_hi(bw[p]));
-                if (blockIdx.x == 0) reinterpret_cast<uint4*>(nm.sum_out)[ci] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
-            }
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                v[c][2 * p] = bf16_lo(sw[p]);
-                v[c][2 * p + 1] = bf16_hi(sw[p]);
-                ss = fmaf(v[c][2 * p], v[c][2 * p], ss);
-                ss = fmaf(v[c][2 * p + 1], v[c][2 * p + 1], ss);
-            }
-        }
-        ss = wave_sum(ss);
-        if (lane == 0 && norm_thread) red[threadIdx.x / kWave] = ss;
-        __syncthreads();
-        float total = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) total += red[i];
-        const float inv = rsqrtf(total / (float)(32 * G) + nm.eps);
-#pragma unroll
-        for (int c = 0; c < KG; ++c) {
-            if (!norm_thread) break;  // wave-uniform
-            const int ci = threadIdx.x + 256 * c;
-            const uint32_t wv[4] = {nw[c].x, nw[c].y, nw[c].z, nw[c].w};
-            float yv[8];
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
-                const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
-                const uint32_t o = pack_bf16x2(a, b);
-                yv[2 * p] = bf16_lo(o);
-                yv[2 * p + 1] = bf16_hi(o);
-            }
-            float m = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(yv[i]));
-            const float scale = g32_scale(quad_max(m));
-            uint32_t lo, hi;
-            const int part = quantize8_dot4(yv, 1.0f / scale, lo, hi);
-            const float gsum = quad_sum((float)part);  // |sum| <= 32 * 127: exact in fp32
-            lq[ci] = make_uint2(lo, hi);
-            if ((ci & 3) == 0) {
-                lsx[ci / 4] = scale;
-                lsum[ci / 4] = (int)gsum;
-            }
-        }
-        __syncthreads();
-        if (row0 >= n_out) return;  // after the workgroup's barriers
-#pragma unroll
-        for (int j = 0; j < KG; ++j) {
-            const int g = lane + kWave * j;
-            const uint4* p = reinterpret_cast<const uint4*>(lq) + 2 * g;
-            xa[j] = p[0];
-            xb[j] = p[1];
-            xs[j] = lsx[g];
-            xq[j] = lsum[g];
-        }
-    }
     uint32_t mask = 0x0F0F0F0Fu;
     asm volatile("" : "+v"(mask));
     float out[NR];
@@ -286,32 +343,30 @@ __global__ __launch_bounds__(QOUT ? kWave * 32 / R : kWave * WPB) void w4a8_gemv
     }
     uint16_t val[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) val[r] = PAIRED ? silu_mul_rounded_bits(out[r], out[R + r]) : f32_to_bf16(out[r]);
+    for (int r = 0; r < R; ++r) val[r] = silu_mul_rounded_bits(out[r], out[R + r]);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
             if (row0 + r < n_out) y[row0 + r] = val[r];
     }
-    if constexpr (QOUT) {
-        // rows 32 b .. 32 b + 31 of this workgroup form output group b
-        __shared__ float grp[32];
-        const int wl = threadIdx.x / kWave;
-        if (lane == 0) {
+    // rows 32 b .. 32 b + 31 of this workgroup form output group b
+    __shared__ float grp[32];
+    const int wl = threadIdx.x / kWave;
+    if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) grp[R * wl + r] = bf16_bits(val[r]);
-        }
-        __syncthreads();
-        if (wl == 0) {
-            const int b = blockIdx.x;
-            const float v = lane < 32 ? grp[lane] : 0.f;
-            const float scale = g32_scale(wave_max(fabsf(v)));
-            const float q = rintf(v * (1.0f / scale));
-            const float total = wave_sum(q);  // |sum| <= 32 * 127: exact in fp32
-            if (lane < 32) oq[32 * b + 8 * (lane >> 3) + dot4_slot(lane & 7)] = (uint8_t)(int)q;
-            if (lane == 0) {
-                osx[b] = scale;
-                osum[b] = (int)total;
-            }
+        for (int r = 0; r < R; ++r) grp[R * wl + r] = bf16_bits(val[r]);
+    }
+    __syncthreads();
+    if (wl == 0) {
+        const int b = blockIdx.x;
+        const float v = lane < 32 ? grp[lane] : 0.f;
+        const float scale = g32_scale(wave_max(fabsf(v)));
+        const float q = rintf(v * (1.0f / scale));
+        const float total = wave_sum(q);  // |sum| <= 32 * 127: exact in fp32
+        if (lane < 32) oq[32 * b + 8 * (lane >> 3) + dot4_slot(lane & 7)] = (uint8_t)(int)q;
+        if (lane == 0) {
+            osx[b] = scale;
+            osum[b] = (int)total;
         }
     }
 }
@@ -418,10 +473,9 @@ int launch_w4a8_qout(const void* qx, const void* sx, const void* qsum, const voi
     const dim3 grid((n_out + 31) / 32), block(kWave * wpb);
 #define MOSS_W4A8(KGV, RV)                                                                                        \
     if (KG == KGV && rows == RV) {                                                                                \
-        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, true, true>), grid, block, 0, st, (const uint32_t*)qx,       \
-                           (const float*)sx, (const int*)qsum, (const uint4*)qw, (const uint16_t*)sc,             \
-                           (const uint8_t*)zp, (uint16_t*)y, (uint8_t*)oq, (float*)osx, (int*)osum, G, n_out,     \
-                           W8Norm{});                                                                             \
+        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV>), grid, block, 0, st, (const uint32_t*)qx, (const float*)sx, \
+                           (const int*)qsum, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,           \
+                           (uint16_t*)y, (uint8_t*)oq, (float*)osx, (int*)osum, G, n_out);                        \
         return moss_launch_status();                                                                              \
     }
 #define MOSS_W4A8_R(KGV) MOSS_W4A8(KGV, 2) MOSS_W4A8(KGV, 4)
@@ -432,32 +486,28 @@ int launch_w4a8_qout(const void* qx, const void* sx, const void* qsum, const voi
     return (int)hipErrorInvalidValue;
 }
 
-// K = 2048 KG, KG in {1, 2, 4} (K = 2048, 4096, 8192).  8-wave workgroups once there are at
-// least 2048 waves (the q||k||v projection at 2 rows per wave), else 4.
+// K = 2048 KG, KG in {1, 2, 4} (K = 2048, 4096, 8192); rows per wave 1, 2 or 4 (0: 2, measured
+// best for the q||k||v projection).
 template <bool PAIRED>
 int launch_w4a8_norm(const W8Norm& nm, const void* qw, const void* sc, const void* zp, void* y, int K, int n_out,
                      int rows, hipStream_t st) {
     const int G = K / 32, KG = K / 2048;
-    if (rows == 0) rows = 1;
-    const int waves = (n_out + rows - 1) / rows;
-    const int wpb = waves >= 2048 ? 8 : 4;
-    const dim3 grid((waves + wpb - 1) / wpb), block(kWave * wpb);
-#define MOSS_W4A8N(KGV, RV, ACTV, WV)                                                                             \
-    if (KG == KGV && rows == RV && wpb == WV) {                                                                   \
-        hipLaunchKernelGGL((w4a8_gemv_kernel<KGV, RV, PAIRED, false, ACTV, WV>), grid, block, 0, st, nullptr,     \
-                           nullptr, nullptr, (const uint4*)qw, (const uint16_t*)sc, (const uint8_t*)zp,           \
-                           (uint16_t*)y, nullptr, nullptr, nullptr, G, n_out, nm);                                \
+    if (rows == 0) rows = 2;
+    const int per_block = (8 / KG) * rows;
+    const dim3 grid((n_out + per_block - 1) / per_block), block(512);
+#define MOSS_W4A8N(KGV, RV, ACTV)                                                                                 \
+    if (KG == KGV && rows == RV) {                                                                                \
+        hipLaunchKernelGGL((w4a8_ksplit_norm_kernel<KGV, RV, PAIRED, ACTV>), grid, block, 0, st, (const uint4*)qw, \
+                           (const uint16_t*)sc, (const uint8_t*)zp, (uint16_t*)y, G, n_out, nm);                  \
         return moss_launch_status();                                                                              \
     }
-#define MOSS_W4A8N_W(KGV, RV, ACTV) MOSS_W4A8N(KGV, RV, ACTV, 4) MOSS_W4A8N(KGV, RV, ACTV, 8)
-#define MOSS_W4A8N_R(KGV, ACTV) MOSS_W4A8N_W(KGV, 1, ACTV) MOSS_W4A8N_W(KGV, 2, ACTV) MOSS_W4A8N_W(KGV, 4, ACTV)
+#define MOSS_W4A8N_R(KGV, ACTV) MOSS_W4A8N(KGV, 1, ACTV) MOSS_W4A8N(KGV, 2, ACTV) MOSS_W4A8N(KGV, 4, ACTV)
     if (nm.res) {
         MOSS_W4A8N_R(1, 2) MOSS_W4A8N_R(2, 2) MOSS_W4A8N_R(4, 2)
     } else {
         MOSS_W4A8N_R(1, 1) MOSS_W4A8N_R(2, 1) MOSS_W4A8N_R(4, 1)
     }
 #undef MOSS_W4A8N_R
-#undef MOSS_W4A8N_W
 #undef MOSS_W4A8N
     return (int)hipErrorInvalidValue;
 }

@@ -10,8 +10,8 @@ bf16 for an installed model, as the reference keeps them, or INT4-G32 for the sy
 36-layer benchmark step.  With ``w4a8`` the four layer projections run the reference's serving
 arithmetic instead (int8 activations per group of 32, integer dot products, fp32 group combine;
 ``src/moss_tts/_runtime/dp4a_scaled.py:22-95``): add-RMSNorm + int8 quantizer + q||k||v (one
-kernel) -> attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer ->
-gate||up with SiLU*mul -> int8 quantizer + down (one kernel)
+kernel) -> attention with the int8 quantizer in its merge -> O -> add-RMSNorm + quantizer +
+gate||up with SiLU*mul (one kernel) -> int8 quantizer + down (one kernel)
 (``src/moss_tts/_runtime/llm.py:29-56,71-92``).
 The heads matrix holds the 32 audio heads (``audio_stride`` rows each, the first 1024 sampled)
 followed by the 2 text-head rows (gen slot, delay slot; ``llm.py:190-191``); the step ends with the
@@ -227,25 +227,27 @@ class DecodeStepG32:
         mlp = None
         for i, layer in enumerate(self.layers):
             state = (residual.clone(), None if mlp is None else mlp.clone()) if trace is not None else None
-            # add-RMSNorm + quantizer + q||k||v in one kernel, one row per wave in 8-wave workgroups
-            # (768 workgroups repeat the normalization); measured faster than two rows per wave and
-            # than the separate norm_quant in front of the K-split projection
+            # add-RMSNorm + quantizer + q||k||v in one kernel (8 waves per workgroup: 2 K slices x
+            # 4 row groups of 2 rows, so 768 workgroups repeat the normalization); measured faster
+            # than one row per wave over the whole K and than the separate norm_quant in front of
+            # the K-split projection
             if i == 0:
-                qkv = w4a8.norm_linear(x, layer.input_norm, eps, layer.qkv.packed, rows_per_wave=1)
+                qkv = w4a8.norm_linear(x, layer.input_norm, eps, layer.qkv.packed, rows_per_wave=2)
             else:
                 residual, qkv = w4a8.norm_linear(mlp, layer.input_norm, eps, layer.qkv.packed, residual=residual,
-                                                 rows_per_wave=1)
+                                                 rows_per_wave=2)
             attn, act = attention.decode_attention_qkv(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
                                                        self.keys[i], self.values[i], self.position, eps, ws=self.ws,
                                                        quantize=True)
             o = w4a8.linear(None, layer.o.packed, prequantized=act)
-            # gate/up: the separate add-RMSNorm + quantizer is faster than the fused form here
-            # (3072 workgroups would each repeat the normalization); the SiLU*mul output is
-            # quantized inside the down projection's kernel (each lane its own group of 32), faster
-            # than the gate/up's fused output quantizer (its 32-row workgroups hold fewer rows in
-            # flight) and than a separate quantizer launch
-            residual, _, act = w4a8.norm_quant(o.view(1, HIDDEN), residual, layer.post_norm, eps, normalized=False)
-            hidden = w4a8.linear(None, layer.gate_up.packed, paired=True, prequantized=act)
+            # add-RMSNorm + quantizer + gate/up + SiLU*mul in one kernel (the same K-split fused
+            # form as q||k||v: 1536 workgroups repeat the normalization), measured faster than the
+            # separate norm_quant in front of the K-split gate/up; the SiLU*mul output is quantized
+            # inside the down projection's kernel (each lane its own group of 32), faster than the
+            # gate/up's fused output quantizer (its 32-row workgroups hold fewer rows in flight) and
+            # than a separate quantizer launch
+            residual, hidden = w4a8.norm_linear(o.view(1, HIDDEN), layer.post_norm, eps, layer.gate_up.packed,
+                                                residual=residual, paired=True, rows_per_wave=2)
             mlp = w4a8.linear(hidden, layer.down.packed).view(1, HIDDEN)
             if trace is not None:
                 trace.append(dict(residual_in=state[0], mlp_in=state[1], qkv=qkv.clone(), attn=attn.clone(),
