@@ -211,8 +211,8 @@ __device__ __forceinline__ void w8norm_into_lds(const W8NormLoad<KG>& nl, const 
 // matching up rows); wave (slice, row group) takes the slice's groups of its rows, one per lane,
 // and reads only its own group of the quantized row from LDS.  The slice sums meet in LDS and are
 // added in slice order.  Against one wave per row holding the whole K (the same 8 rows per
-// workgroup) the q||k||v projection goes from 6.0-6.3 to 5.3 us and the W4A8 decode step from
-// 1.61 to 1.57 ms.
+// workgroup) the q||k||v projection goes from 6.0-6.3 to 5.3 us; the paired gate||up form takes
+// 12 us against 13.6 us for the standalone norm + quantizer and the K-split gate||up.
 template <int KG, int R, bool PAIRED, int ACT>
 __global__ __launch_bounds__(512) void w4a8_ksplit_norm_kernel(const uint4* __restrict__ qw, const uint16_t* __restrict__ sc,
                                                                const uint8_t* __restrict__ zp, uint16_t* __restrict__ y,
