@@ -202,6 +202,70 @@ __device__ __forceinline__ void dequant_word_exact(uint32_t d0, uint32_t d1, uin
         : "v"(d0), "v"(d1), "v"(d2), "v"(d3), "v"(s_lo), "v"(s_hi), "v"(bias));
 }
 
+// Constants of dequant_word_mixed.  v_and_or_b32 is a VOP3 form, which on gfx9 takes no literal
+// operand and one scalar operand: the masks are pinned in SGPRs, the bias patterns in VGPRs.
+struct MixedUnpack {
+    uint32_t mask_lo, mask_hi, bf16_bias, f16_bias;
+};
+
+__device__ __forceinline__ MixedUnpack make_mixed_unpack() {
+    MixedUnpack c{0x000F000Fu, 0x00F000F0u, 0x43004300u, 0x54005400u};
+    asm volatile("" : "+s"(c.mask_lo), "+s"(c.mask_hi), "+v"(c.bf16_bias), "+v"(c.f16_bias));
+    return c;
+}
+
+// dequant_word_exact's four bf16 pairs of a row-packed word w, bit for bit, with two shifts fewer.
+// The codes at nibble positions 0 and 4 become the bf16 pair (128 + q) as before; the codes at
+// positions 1 and 5 are masked in place into an fp16 pair, where bits 4..7 of the mantissa of
+// 0x5400 (64.0) weigh 1/16 each, so (w & 0x00F000F0) | 0x54005400 is (64 + q, 64 + q') without a
+// shift.  w >> 8 gives positions 2/6 and 3/7 the same way.  The fp16 pairs go through
+// v_fma_mix_f32 with the fp32 scale s and bias_f16 = -(64 + z) s: (64 + q) s has at most 15
+// significant bits, so (q - z) s is again exact in fp32 before v_cvt_pk_bf16_f32 rounds it.
+// s_lo / s_hi / bias_bf16 are dequant_word_exact's operands and s their fp32 value.  Each output
+// register first takes the low product of its pair; the v_dot2 results are read by the v_cvt_pk
+// at least 5 instructions later (see dequant_pair_exact).
+__device__ __forceinline__ void dequant_word_mixed(uint32_t w, const MixedUnpack& c, uint32_t s_lo, uint32_t s_hi,
+                                                   float s, float bias_bf16, float bias_f16, uint32_t (&o)[4]) {
+    const uint32_t d0 = (w & c.mask_lo) | c.bf16_bias;
+    const uint32_t d1 = (w & c.mask_hi) | c.f16_bias;
+    const uint32_t w8 = w >> 8;
+    const uint32_t d2 = (w8 & c.mask_lo) | c.bf16_bias;
+    const uint32_t d3 = (w8 & c.mask_hi) | c.f16_bias;
+    float t0, t1, t2, t3;
+    asm("v_dot2_f32_bf16 %0, %8, %12, %15\n\t"
+        "v_dot2_f32_bf16 %4, %8, %13, %15\n\t"
+        "v_dot2_f32_bf16 %2, %10, %12, %15\n\t"
+        "v_dot2_f32_bf16 %6, %10, %13, %15\n\t"
+        "v_fma_mix_f32 %1, %9, %14, %16 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %5, %9, %14, %16 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %3, %11, %14, %16 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %7, %11, %14, %16 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_cvt_pk_bf16_f32 %0, %0, %4\n\t"
+        "v_cvt_pk_bf16_f32 %1, %1, %5\n\t"
+        "v_cvt_pk_bf16_f32 %2, %2, %6\n\t"
+        "v_cvt_pk_bf16_f32 %3, %3, %7"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(d0), "v"(d1), "v"(d2), "v"(d3), "v"(s_lo), "v"(s_hi), "v"(s), "v"(bias_bf16), "v"(bias_f16));
+}
+
+// The group operands of dequant_word_mixed from the scale bits and zero point.  Both biases are
+// exact: (128 + z) s and (64 + z) s have at most 16 significant bits, and the fma adds 64 s
+// exactly.
+struct GroupDequant {
+    uint32_t s_lo, s_hi;
+    float s, bias_bf16, bias_f16;
+};
+
+__device__ __forceinline__ GroupDequant group_dequant(uint32_t s_bits, uint32_t z) {
+    GroupDequant g;
+    g.s_lo = s_bits & 0xffffu;
+    g.s_hi = g.s_lo << 16;
+    g.s = __uint_as_float(g.s_lo << 16);
+    g.bias_bf16 = -(128.0f + (float)z) * g.s;
+    g.bias_f16 = __builtin_fmaf(64.0f, g.s, g.bias_bf16);
+    return g;
+}
+
 // One 128-dim head through RMSNorm + rotate-half RoPE, one wave per head: lane l holds dims
 // l and l + 64 (each other's RoPE partners).  Rounding points of the reference
 // (src/moss_tts/_runtime/kernels.py:142-170): xn = bf16(bf16(x * r) * w); out_l =

@@ -134,30 +134,27 @@ __device__ __forceinline__ float row_partial_unrounded(const XSlice<KG>& xs, con
 }
 
 // Exact form: every weight is the bit-exact bf16 dequant bf16_rne((q - z) * s) before it
-// meets x (dequant_word_exact, four pairs at a time), then a dot2 with the matching x pair
+// meets x (dequant_word_mixed, four pairs at a time), then a dot2 with the matching x pair
 // accumulates in fp32.
-__device__ __forceinline__ float word_dot_exact(uint32_t w, const uint32_t* xv, float acc, Magic m, uint32_t s_lo,
-                                                uint32_t s_hi, float bias) {
+__device__ __forceinline__ float word_dot_exact(uint32_t w, const uint32_t* xv, float acc, const MixedUnpack& c,
+                                                const GroupDequant& gd) {
     uint32_t wq[4];
-    dequant_word_exact(((w >> 0) & m.mask) | m.bias, ((w >> 4) & m.mask) | m.bias, ((w >> 8) & m.mask) | m.bias,
-                       ((w >> 12) & m.mask) | m.bias, s_lo, s_hi, bias, wq);
+    dequant_word_mixed(w, c, gd.s_lo, gd.s_hi, gd.s, gd.bias_bf16, gd.bias_f16, wq);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc = dot2_bf16(wq[i], xv[i], acc);
     return acc;
 }
 
 template <int KG>
-__device__ __forceinline__ float row_partial_exact(const XSlice<KG>& xs, const RowLoad<KG>& r, Magic m) {
+__device__ __forceinline__ float row_partial_exact(const XSlice<KG>& xs, const RowLoad<KG>& r, const MixedUnpack& c) {
     float acc = 0.f;  // one dot2 chain over the whole row: the weights already carry their scale
 #pragma unroll
     for (int j = 0; j < KG; ++j) {
-        const uint32_t s_lo = r.s[j] & 0xffffu;
-        const uint32_t s_hi = s_lo << 16;
-        const float bias = -(128.0f + (float)r.z[j]) * bf16_bits((uint16_t)s_lo);  // exact: 16 bits
-        acc = word_dot_exact(r.w[j].x, &xs.v[j][0], acc, m, s_lo, s_hi, bias);
-        acc = word_dot_exact(r.w[j].y, &xs.v[j][4], acc, m, s_lo, s_hi, bias);
-        acc = word_dot_exact(r.w[j].z, &xs.v[j][8], acc, m, s_lo, s_hi, bias);
-        acc = word_dot_exact(r.w[j].w, &xs.v[j][12], acc, m, s_lo, s_hi, bias);
+        const GroupDequant gd = group_dequant(r.s[j], r.z[j]);
+        acc = word_dot_exact(r.w[j].x, &xs.v[j][0], acc, c, gd);
+        acc = word_dot_exact(r.w[j].y, &xs.v[j][4], acc, c, gd);
+        acc = word_dot_exact(r.w[j].z, &xs.v[j][8], acc, c, gd);
+        acc = word_dot_exact(r.w[j].w, &xs.v[j][12], acc, c, gd);
     }
     return acc;
 }
@@ -237,11 +234,16 @@ __device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const 
         load_x<KG, !EXACT, FULL>(xs, xn, lane, G);
     }
 
-    const Magic m = make_magic();
     float out[NR];
+    if constexpr (EXACT) {
+        const MixedUnpack c = make_mixed_unpack();
 #pragma unroll
-    for (int r = 0; r < NR; ++r)
-        out[r] = wave_sum(EXACT ? row_partial_exact(xs, rows[r], m) : row_partial_unrounded(xs, rows[r], m));
+        for (int r = 0; r < NR; ++r) out[r] = wave_sum(row_partial_exact(xs, rows[r], c));
+    } else {
+        const Magic m = make_magic();
+#pragma unroll
+        for (int r = 0; r < NR; ++r) out[r] = wave_sum(row_partial_unrounded(xs, rows[r], m));
+    }
 
     if (lane == 0) {
 #pragma unroll
@@ -301,11 +303,19 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
         const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
         load_row_slice<true>(rows[r], qw, sc, zp, n, lane, G, g0);
     }
-    const Magic m = make_magic();
+    float v[NR];
+    if constexpr (EXACT) {
+        const MixedUnpack c = make_mixed_unpack();
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        const float v = wave_sum(EXACT ? row_partial_exact(xs, rows[r], m) : row_partial_unrounded(xs, rows[r], m));
-        if (lane == 0) part[slice][r] = v;
+        for (int r = 0; r < NR; ++r) v[r] = wave_sum(row_partial_exact(xs, rows[r], c));
+    } else {
+        const Magic m = make_magic();
+#pragma unroll
+        for (int r = 0; r < NR; ++r) v[r] = wave_sum(row_partial_unrounded(xs, rows[r], m));
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) part[slice][r] = v[r];
     }
     __syncthreads();
     if (slice == 0 && lane < R) {
@@ -331,22 +341,18 @@ __device__ __forceinline__ void gemv_ksplit(const uint16_t* __restrict__ x, cons
 constexpr int kMaxTokens = 4;
 
 template <int KG, int T>
-__device__ __forceinline__ void row_partial_exact_tokens(const XSlice<KG> (&xs)[T], const RowLoad<KG>& r, Magic m,
-                                                         float (&acc)[T]) {
+__device__ __forceinline__ void row_partial_exact_tokens(const XSlice<KG> (&xs)[T], const RowLoad<KG>& r,
+                                                         const MixedUnpack& c, float (&acc)[T]) {
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = 0.f;
 #pragma unroll
     for (int j = 0; j < KG; ++j) {
-        const uint32_t s_lo = r.s[j] & 0xffffu;
-        const uint32_t s_hi = s_lo << 16;
-        const float bias = -(128.0f + (float)r.z[j]) * bf16_bits((uint16_t)s_lo);
+        const GroupDequant gd = group_dequant(r.s[j], r.z[j]);
         const uint32_t words[4] = {r.w[j].x, r.w[j].y, r.w[j].z, r.w[j].w};
 #pragma unroll
         for (int wd = 0; wd < 4; ++wd) {
-            const uint32_t w = words[wd];
             uint32_t wq[4];
-            dequant_word_exact(((w >> 0) & m.mask) | m.bias, ((w >> 4) & m.mask) | m.bias,
-                               ((w >> 8) & m.mask) | m.bias, ((w >> 12) & m.mask) | m.bias, s_lo, s_hi, bias, wq);
+            dequant_word_mixed(words[wd], c, gd.s_lo, gd.s_hi, gd.s, gd.bias_bf16, gd.bias_f16, wq);
 #pragma unroll
             for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -373,11 +379,11 @@ __global__ __launch_bounds__(256) void w4g32_gemv_tokens_exact(const uint16_t* _
     RowLoad<KG> rows[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) load_row_nt<KG, FULL>(rows[r], qw, sc, zp, min(row0 + r, n_out - 1), lane, G);
-    const Magic m = make_magic();
+    const MixedUnpack c = make_mixed_unpack();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float acc[T];
-        row_partial_exact_tokens<KG, T>(xs, rows[r], m, acc);
+        row_partial_exact_tokens<KG, T>(xs, rows[r], c, acc);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float v = wave_sum(acc[t]);
@@ -405,11 +411,11 @@ __global__ __launch_bounds__(64 * W) void w4g32_gemv_ksplit_tokens_exact(const u
     RowLoad<2> rows[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) load_row_slice<true>(rows[r], qw, sc, zp, min(row0 + r, n_out - 1), lane, G, g0);
-    const Magic m = make_magic();
+    const MixedUnpack c = make_mixed_unpack();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float acc[T];
-        row_partial_exact_tokens<2, T>(xs, rows[r], m, acc);
+        row_partial_exact_tokens<2, T>(xs, rows[r], c, acc);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float v = wave_sum(acc[t]);
