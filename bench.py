@@ -160,10 +160,17 @@ def cpu_baseline(torch, budget_s: float, gateup, down, h, norm_w):
             "cpu_model": _cpu_model(), "threads_4": four}
 
 
+# Launches per captured graph in the per-launch timings: the gap between two replays of a graph is
+# spread over this many launches, so it stays a small part of each launch's time.
+MIN_GRAPH_LAUNCHES = 64
+
+
 def _per_launch(torch, fns, replays: int = 20) -> float:
-    """Seconds per launch of ``fns`` (one launch each) captured into one HIP graph."""
-    graph = _capture(torch, lambda: [f() for f in fns])
-    return _time_graph(torch, graph, replays) / len(fns)
+    """Seconds per launch of ``fns`` (one launch each), the list repeated into one HIP graph of at
+    least MIN_GRAPH_LAUNCHES launches."""
+    reps = max(1, -(-MIN_GRAPH_LAUNCHES // len(fns)))
+    graph = _capture(torch, lambda: [f() for _ in range(reps) for f in fns])
+    return _time_graph(torch, graph, replays) / (len(fns) * reps)
 
 
 def streaming_read_bench(torch, dev, nbytes: int):
@@ -187,6 +194,28 @@ def streaming_read_bench(torch, dev, nbytes: int):
     res = {"us_per_call": out[best], "kernel": f"torch.{best}", "bytes": read_bytes,
            "frac_of_peak": round(read_bytes / (out[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "all_us": out}
     _log(f"[bench] vendor streaming read of {read_bytes} B: {out} us per launch (best {best})")
+    return res
+
+
+def own_streaming_read_bench(torch, dev, nbytes: int):
+    """The library's own streaming read (``moss_stream_read``: 16-byte loads, 1 KiB contiguous per
+    wave instruction, nothing but the reads and an XOR) of ``nbytes``, per launch in a HIP graph
+    over >= 512 MiB of distinct copies: the ceiling of one launch that only reads the GEMV's bytes."""
+    from moss_tts._runtime import native
+
+    n_copies = max(2, -(-(512 << 20) // nbytes))
+    copies = [torch.empty(nbytes // 4, device=dev, dtype=torch.int32).random_() for _ in range(n_copies)]
+    sink = torch.empty(int(native.lib().moss_stream_read_words(nbytes)), device=dev, dtype=torch.int32)
+
+    def launch(b):
+        native.call("moss_stream_read", native.ptr(b), nbytes, native.ptr(sink), native.stream_of(b))
+
+    sec = min(_per_launch(torch, [lambda b=b: launch(b) for b in copies], replays=20) for _ in range(3))
+    del copies
+    torch.cuda.empty_cache()
+    res = {"us_per_call": round(sec * 1e6, 3), "kernel": "moss_stream_read", "bytes": nbytes,
+           "frac_of_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4)}
+    _log(f"[bench] own streaming read of {nbytes} B: {res['us_per_call']} us per launch")
     return res
 
 
@@ -770,7 +799,8 @@ def main() -> int:
                 w4g32.gemv(a, dn, dequant=dequant)
         return run
 
-    cycle = len(copies)
+    # one graph holds whole rotations over the copies and at least MIN_GRAPH_LAUNCHES launches
+    cycle = len(copies) * max(1, -(-MIN_GRAPH_LAUNCHES // (2 * len(copies))))
     g_cycle = _capture(torch, steps(cycle))
     rem = args.steps % cycle
     g_rem = _capture(torch, steps(rem)) if rem else None
@@ -822,8 +852,9 @@ def main() -> int:
     xs = pointwise.rmsnorm(h, norm_w, 1e-6)
 
     def per_launch(fn, launches):
-        graph = _capture(torch, fn)
-        return _time_graph(torch, graph, 50) / launches
+        reps = max(1, -(-MIN_GRAPH_LAUNCHES // launches))
+        graph = _capture(torch, lambda: [fn() for _ in range(reps)])
+        return _time_graph(torch, graph, 50) / (launches * reps)
 
     gu_s = per_launch(lambda: [w4g32.norm_gateup_silu(h, norm_w, 1e-6, gu) for gu, _ in copies], len(copies))
     gu_gbs = NORM_GATEUP_BYTES / gu_s / 1e9
@@ -859,6 +890,8 @@ def main() -> int:
     torch.cuda.empty_cache()
     read = streaming_read_bench(torch, dev, ns_bytes)
     read["gemv_time_over_read_time"] = round(ns_s * 1e6 / read["us_per_call"], 4)
+    own_read = own_streaming_read_bench(torch, dev, ns_bytes)
+    own_read["gemv_time_over_read_time"] = round(ns_s * 1e6 / own_read["us_per_call"], 4)
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
     small_m = small_m_bench(torch, dev) if not args.no_extras else None
     heads_bf16 = bf16_heads_bench(torch, dev) if not args.no_extras else None
@@ -900,7 +933,7 @@ def main() -> int:
             "resident_weight_mib": round(resident / 2**20, 1),
             "weights": "N(0,0.02) fp32, min-max quantized per 32-input group on the GPU (seeded)",
             "activations": "bf16 N(0,1) through RMSNorm with weight 1+N(0,0.01)",
-            "timing": "one HIP graph of weight-copy-rotating steps, HIP events on its stream",
+            "timing": f"HIP graphs of {cycle} steps rotating over the weight copies, HIP events on their stream",
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -918,7 +951,8 @@ def main() -> int:
         "extra": {
             "gemv_k4096_n12288": {"us_per_call": round(ns_s * 1e6, 3), "GB/s": round(ns_gbs, 1),
                                   "frac_of_peak": round(ns_gbs / HBM_PEAK_GBS, 4), "bytes": ns_bytes,
-                                  "dequant": "exact", "vendor_streaming_read_same_bytes": read},
+                                  "dequant": "exact", "vendor_streaming_read_same_bytes": read,
+                                  "streaming_read_same_bytes": own_read},
             "gemv_k4096_n12288_unrounded": {"us_per_call": round(ns_unr_s * 1e6, 3),
                                             "GB/s": round(ns_bytes / ns_unr_s / 1e9, 1),
                                             "frac_of_peak": round(ns_bytes / ns_unr_s / 1e9 / HBM_PEAK_GBS, 4)},

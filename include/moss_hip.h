@@ -402,6 +402,16 @@ int moss_advance_step(const void *next_ids, void *ids, void *position, void *aud
                       void *history, void *status, int step, int width, long long audio_start_id,
                       long long gen_slot_id, long long delay_slot_id, void *stream);
 
+/* ------------------------------------------------------- measurement */
+/* No counterpart in the reference: a streaming read for bench.py, which times it on the bytes of a
+ * decode GEMV to measure the ceiling of one launch that only reads those bytes.  Reads `bytes` (a
+ * multiple of 16) from the 16-byte aligned src with 16-byte loads, one 256-thread workgroup per
+ * 16 KiB (thread t of workgroup b reads chunks 1024 b + 256 u + t, u < 4), and writes the XOR of
+ * the 32-bit words each wave read to xor_out[4 b + t / 64] (uint32, moss_stream_read_words(bytes)
+ * entries). */
+long long moss_stream_read_words(long long bytes);
+int moss_stream_read(const void *src, long long bytes, void *xor_out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

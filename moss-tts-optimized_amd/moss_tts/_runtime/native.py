@@ -72,10 +72,13 @@ SIGNATURES: dict[str, list] = {
     "moss_compose_next_ids": [_P, _P, _P, _P, _P, ctypes.c_longlong, ctypes.c_longlong, _I, ctypes.c_longlong, _P, _P],
     "moss_advance_step": [_P, _P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong,
                           _P],
+    "moss_stream_read_words": [ctypes.c_longlong],
+    "moss_stream_read": [_P, ctypes.c_longlong, _P, _P],
 }
 _RESTYPES = {"moss_error_string": ctypes.c_char_p, "moss_gemm_workspace_bytes": ctypes.c_longlong,
              "moss_gemm_silu_workspace_bytes": ctypes.c_longlong,
-             "moss_gemm_qk_rope_workspace_bytes": ctypes.c_longlong}
+             "moss_gemm_qk_rope_workspace_bytes": ctypes.c_longlong,
+             "moss_stream_read_words": ctypes.c_longlong}
 
 
 class NativeLibraryMissing(RuntimeError):

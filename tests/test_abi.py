@@ -100,6 +100,10 @@ def test_argument_errors_are_rejected_before_launch(lib):
     assert lib.moss_fp8_linear(p, p, null, p, 2, 4112, 64, 0, null, 0, null) == 1      # GEMM K % 64
     assert lib.moss_fp8_gateup_silu(p, p, null, p, 2, 4096, 64, 0, null) == 1           # M must be 1
     assert lib.moss_fp8_to_bf16(p, p, 6, null) == 1                                     # count % 4
+    assert lib.moss_stream_read(p, 24, p, null) == 1                                     # bytes % 16
+    assert lib.moss_stream_read(odd, 32, p, null) == 1                                   # src alignment
+    assert lib.moss_stream_read(null, 32, p, null) == 1
+    assert lib.moss_stream_read_words(16385) == 8 and lib.moss_stream_read_words(0) == 0
     assert lib.moss_bf16_gemv(p, p, p, 4608, 64, 0, null) == 1                           # K / 512 = 9
     assert lib.moss_bf16_gemv(p, p, p, 4000, 64, 0, null) == 1                           # K % 512
     assert lib.moss_bf16_gemv(p, odd, p, 4096, 64, 0, null) == 1                         # weight alignment
