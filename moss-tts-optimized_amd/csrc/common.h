@@ -162,48 +162,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// Exact bf16 dequant of one code pair: d = (128+qa | 128+qb) in bf16, s_lo = (s | 0),
-// s_hi = (0 | s), bias = -(128+z) s (exact in fp32).  Each v_dot2_f32_bf16 then yields the
-// exact fp32 (q - z) s (every addend's bits lie inside the adder's window) and
-// v_cvt_pk_bf16_f32 rounds the pair to nearest even.  The block is one asm statement
-// because a v_dot2 result is not interlocked on gfx950: a non-dot VALU may read it only
-// after 3 wait states (the s_nop 2), which the compiler cannot see inside inline asm.
-__device__ __forceinline__ uint32_t dequant_pair_exact(uint32_t d, uint32_t s_lo, uint32_t s_hi, float bias) {
-    uint32_t w;
-    float t;
-    asm("v_dot2_f32_bf16 %0, %2, %3, %5\n\t"
-        "v_dot2_f32_bf16 %1, %2, %4, %5\n\t"
-        "s_nop 2\n\t"
-        "v_cvt_pk_bf16_f32 %0, %0, %1"
-        : "=&v"(w), "=&v"(t)
-        : "v"(d), "v"(s_lo), "v"(s_hi), "v"(bias));
-    return w;
-}
-
-// The same for the four code pairs of one row-packed word (d_i = pair i in magic form): the eight
-// v_dot2 come first, so each v_cvt_pk reads results written at least 3 instructions earlier and
-// the block needs no s_nop.
-__device__ __forceinline__ void dequant_word_exact(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t s_lo,
-                                                   uint32_t s_hi, float bias, uint32_t (&o)[4]) {
-    float t0, t1, t2, t3;
-    asm("v_dot2_f32_bf16 %0, %8, %12, %14\n\t"
-        "v_dot2_f32_bf16 %4, %8, %13, %14\n\t"
-        "v_dot2_f32_bf16 %1, %9, %12, %14\n\t"
-        "v_dot2_f32_bf16 %5, %9, %13, %14\n\t"
-        "v_dot2_f32_bf16 %2, %10, %12, %14\n\t"
-        "v_dot2_f32_bf16 %6, %10, %13, %14\n\t"
-        "v_dot2_f32_bf16 %3, %11, %12, %14\n\t"
-        "v_dot2_f32_bf16 %7, %11, %13, %14\n\t"
-        "v_cvt_pk_bf16_f32 %0, %0, %4\n\t"
-        "v_cvt_pk_bf16_f32 %1, %1, %5\n\t"
-        "v_cvt_pk_bf16_f32 %2, %2, %6\n\t"
-        "v_cvt_pk_bf16_f32 %3, %3, %7"
-        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
-        : "v"(d0), "v"(d1), "v"(d2), "v"(d3), "v"(s_lo), "v"(s_hi), "v"(bias));
-}
-
 // Constants of dequant_word_mixed.  v_and_or_b32 is a VOP3 form, which on gfx9 takes no literal
 // operand and one scalar operand: the masks are pinned in SGPRs, the bias patterns in VGPRs.
+// (The two shifts this form saves per word against masking every pair at bits 0..3 measured 2-3%
+// on the K = 4096 decode GEMVs.)
 struct MixedUnpack {
     uint32_t mask_lo, mask_hi, bf16_bias, f16_bias;
 };
@@ -214,16 +176,19 @@ __device__ __forceinline__ MixedUnpack make_mixed_unpack() {
     return c;
 }
 
-// dequant_word_exact's four bf16 pairs of a row-packed word w, bit for bit, with two shifts fewer.
-// The codes at nibble positions 0 and 4 become the bf16 pair (128 + q) as before; the codes at
-// positions 1 and 5 are masked in place into an fp16 pair, where bits 4..7 of the mantissa of
-// 0x5400 (64.0) weigh 1/16 each, so (w & 0x00F000F0) | 0x54005400 is (64 + q, 64 + q') without a
-// shift.  w >> 8 gives positions 2/6 and 3/7 the same way.  The fp16 pairs go through
-// v_fma_mix_f32 with the fp32 scale s and bias_f16 = -(64 + z) s: (64 + q) s has at most 15
-// significant bits, so (q - z) s is again exact in fp32 before v_cvt_pk_bf16_f32 rounds it.
-// s_lo / s_hi / bias_bf16 are dequant_word_exact's operands and s their fp32 value.  Each output
-// register first takes the low product of its pair; the v_dot2 results are read by the v_cvt_pk
-// at least 5 instructions later (see dequant_pair_exact).
+// The bit-exact bf16 dequant bf16_rne((q - z) * s) of the eight codes of a row-packed word w, as
+// four bf16 pairs o[i] = (code 2i, code 2i + 1) (the code of t = 2i at bits [4i, 4i + 4), of
+// t = 2i + 1 at bits [16 + 4i, 20 + 4i)).  Each pair is masked in place into a float pair that is
+// exact: nibble positions 0 and 4 into bf16 (128 + q) ((w & 0x000F000F) | 0x43004300), positions
+// 1 and 5 into fp16 (64 + q) ((w & 0x00F000F0) | 0x54005400: bits 4..7 of the mantissa of 64.0
+// weigh 1/16 each, so no shift is needed), and w >> 8 gives positions 2/6 and 3/7 the same way.
+// The bf16 pairs meet (s | 0) and (0 | s) in v_dot2_f32_bf16 with bias_bf16 = -(128 + z) s, the
+// fp16 halves meet s in v_fma_mix_f32 with bias_f16 = -(64 + z) s: every addend has at most 16
+// significant bits, so each fp32 result is exactly (q - z) s, and v_cvt_pk_bf16_f32 rounds each
+// pair to nearest even.  The block is one asm statement because a v_dot2 result is not
+// interlocked on gfx950: a non-dot VALU may read it only after 3 wait states, which the compiler
+// cannot see inside inline asm; here each v_cvt_pk reads v_dot2 results written at least 5
+// instructions earlier, and each output register first takes the low product of its pair.
 __device__ __forceinline__ void dequant_word_mixed(uint32_t w, const MixedUnpack& c, uint32_t s_lo, uint32_t s_hi,
                                                    float s, float bias_bf16, float bias_f16, uint32_t (&o)[4]) {
     const uint32_t d0 = (w & c.mask_lo) | c.bf16_bias;

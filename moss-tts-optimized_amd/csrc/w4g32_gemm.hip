@@ -170,16 +170,12 @@ __device__ __forceinline__ void store_b(const StepRegs<BM, BN>& r, const StepAdd
             out[2 * c + 1] = fp8x2_to_bf16x2<true>(r.w[c]);
         }
     } else {
-        uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
-        asm volatile("" : "+v"(mask), "+v"(bias_bits));
-        const uint32_t s_lo = r.s & 0xffffu, s_hi = s_lo << 16;
-        const float bias = -(128.0f + (float)((r.z >> r.zsh) & 15u)) * bf16_bits((uint16_t)s_lo);
+        const MixedUnpack mu = make_mixed_unpack();
+        const GroupDequant gd = group_dequant(r.s, (r.z >> r.zsh) & 15u);
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
             uint32_t o[4];
-            dequant_word_exact((r.w[j] & mask) | bias_bits, ((r.w[j] >> 4) & mask) | bias_bits,
-                               ((r.w[j] >> 8) & mask) | bias_bits, ((r.w[j] >> 12) & mask) | bias_bits, s_lo, s_hi,
-                               bias, o);
+            dequant_word_mixed(r.w[j], mu, gd.s_lo, gd.s_hi, gd.s, gd.bias_bf16, gd.bias_f16, o);
 #pragma unroll
             for (int i = 0; i < 4; ++i) out[4 * j + i] = o[i];
         }
@@ -393,8 +389,7 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
     pin();
     store_x(xv[0], Xs[0]);
     __syncthreads();
-    uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
-    asm volatile("" : "+v"(mask), "+v"(bias_bits));
+    const MixedUnpack mu = make_mixed_unpack();
     for (int blk = 0; blk < blocks; ++blk) {
         const int st = blk * kTs;
 #pragma unroll
@@ -415,15 +410,12 @@ __global__ __launch_bounds__(256) void w4g32_gemm_t_kernel(const uint16_t* __res
             {
                 const uint32_t sw = i == 0 ? cur.s.x : i == 1 ? cur.s.y : i == 2 ? cur.s.z : cur.s.w;
                 const uint32_t zw = i < 2 ? cur.z.x : cur.z.y;
-                const uint32_t s_lo = (sw >> (16 * half)) & 0xffffu, s_hi = s_lo << 16;
                 const uint32_t zq = (zw >> (8 * (2 * (i & 1) + half) + cur.zsh)) & 15u;
-                const float bias = -(128.0f + (float)zq) * bf16_bits((uint16_t)s_lo);
+                const GroupDequant gd = group_dequant(sw >> (16 * half), zq);
                 const uint32_t words[4] = {cw[i].x, cw[i].y, cw[i].z, cw[i].w};
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk)
-                    dequant_word_exact((words[kk] & mask) | bias_bits, ((words[kk] >> 4) & mask) | bias_bits,
-                                       ((words[kk] >> 8) & mask) | bias_bits, ((words[kk] >> 12) & mask) | bias_bits,
-                                       s_lo, s_hi, bias, wf[kk]);
+                    dequant_word_mixed(words[kk], mu, gd.s_lo, gd.s_hi, gd.s, gd.bias_bf16, gd.bias_f16, wf[kk]);
             }
             pin();
             // slot i of the code ring is free once dequantized: codes of step s + kTs into it
@@ -585,8 +577,7 @@ __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t*
     MOSS_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     cbar();
-    uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
-    asm volatile("" : "+v"(mask), "+v"(bias_bits));
+    const MixedUnpack mu = make_mixed_unpack();
     // I: step within the block, P: which tb holds the block's scales, LAST: the last block, whose
     // refills are never read (the compiler drops them, so its waits count nothing after the copy)
     auto step = [&](auto ic, auto pc, auto lc, int blk, const uint16_t* rd, uint16_t* wr) {
@@ -598,9 +589,8 @@ __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t*
         cbar();
         const uint32_t sw = i == 0 ? cur.s.x : i == 1 ? cur.s.y : i == 2 ? cur.s.z : cur.s.w;
         const uint32_t zw = i < 2 ? cur.z.x : cur.z.y;
-        const uint32_t s_lo = (sw >> (16 * half)) & 0xffffu, s_hi = s_lo << 16;
         const uint32_t zq = (zw >> (8 * (2 * (i & 1) + half) + cur.zsh)) & 15u;
-        const float bias = -(128.0f + (float)zq) * bf16_bits((uint16_t)s_lo);
+        const GroupDequant gd = group_dequant(sw >> (16 * half), zq);
         const char* xs = reinterpret_cast<const char*>(rd);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -609,8 +599,7 @@ __global__ __launch_bounds__(256, 3) void w4g32_gemm_tdma_kernel(const uint16_t*
             for (int j = 0; j < JT; ++j) b[j] = *reinterpret_cast<const bf16x8_t*>(xs + roff[kk] + 4096 * j);
             const uint32_t wd = kk == 0 ? cw[i].x : kk == 1 ? cw[i].y : kk == 2 ? cw[i].z : cw[i].w;
             uint32_t wf[4];
-            dequant_word_exact((wd & mask) | bias_bits, ((wd >> 4) & mask) | bias_bits, ((wd >> 8) & mask) | bias_bits,
-                               ((wd >> 12) & mask) | bias_bits, s_lo, s_hi, bias, wf);
+            dequant_word_mixed(wd, mu, gd.s_lo, gd.s_hi, gd.s, gd.bias_bf16, gd.bias_f16, wf);
             const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{wf[0], wf[1], wf[2], wf[3]});
 #pragma unroll
             for (int j = 0; j < JT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], acc[j], 0, 0, 0);
@@ -911,8 +900,7 @@ __global__ __launch_bounds__(512) void stream_gemm_kernel(const uint16_t* __rest
         load_w(cw[i], i);  // quads >= 4 >= DQ
         load_x(xv[i], i);
     }
-    uint32_t mask = 0x000F000Fu, bias_bits = 0x43004300u;
-    asm volatile("" : "+v"(mask), "+v"(bias_bits));
+    const MixedUnpack mu = make_mixed_unpack();
     for (int d0 = 0; d0 < quads; d0 += 4) {  // quads % 4 == 0; DQ divides 4
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -940,13 +928,9 @@ __global__ __launch_bounds__(512) void stream_gemm_kernel(const uint16_t* __rest
                     const int gi = 4 * (u & 1) + t;  // within the 8-group scale block u / 2
                     const uint4& s8 = sv[u >> 1];
                     const uint32_t sw = gi < 2 ? s8.x : gi < 4 ? s8.y : gi < 6 ? s8.z : s8.w;
-                    const uint32_t s_lo = (sw >> (16 * (gi & 1))) & 0xffffu, s_hi = s_lo << 16;
                     const uint32_t zq = ((gi < 4 ? zv[u >> 1].x : zv[u >> 1].y) >> (8 * (gi & 3) + zsh[u >> 1])) & 15u;
-                    const float bias = -(128.0f + (float)zq) * bf16_bits((uint16_t)s_lo);
-                    const uint32_t w = wq[t];
-                    dequant_word_exact((w & mask) | bias_bits, ((w >> 4) & mask) | bias_bits,
-                                       ((w >> 8) & mask) | bias_bits, ((w >> 12) & mask) | bias_bits, s_lo, s_hi,
-                                       bias, a);
+                    const GroupDequant gd = group_dequant(sw >> (16 * (gi & 1)), zq);
+                    dequant_word_mixed(wq[t], mu, gd.s_lo, gd.s_hi, gd.s, gd.bias_bf16, gd.bias_f16, a);
                 } else {
                     a[0] = fp8x2_to_bf16x2<false>(wq[2 * t]);
                     a[1] = fp8x2_to_bf16x2<true>(wq[2 * t]);

@@ -5,10 +5,12 @@
 // Mapping (gfx950, wave64): one wave owns R output rows; its 64 lanes split K, lane l
 // owning groups l, l+64, l+128, ... (16 bytes of codes per group, so each global_load_dwordx4
 // of a wave reads 1 KiB contiguous).  The lane's slice of x stays in VGPRs for all R rows.
-// Codes become bf16 lanes with one and-or: (w >> 4i) & 0x000F000F | 0x43004300 is the pair
-// (128 + q_2i, 128 + q_2i+1), exact in bf16, fed to v_dot2_f32_bf16 against the matching
-// x pair.  Per group: sum (q - z) x = acc - (128 + z) * sum_g x, then * s.  Rows are reduced
-// with DPP (no LDS, no atomics, no workspace): every output element is written once.
+// Unrounded mode: codes become bf16 lanes with one and-or: (w >> 4i) & 0x000F000F | 0x43004300
+// is the pair (128 + q_2i, 128 + q_2i+1), exact in bf16, fed to v_dot2_f32_bf16 against the
+// matching x pair; per group sum (q - z) x = acc - (128 + z) * sum_g x, then * s.  Exact mode:
+// every weight is dequantized bit-exactly first (dequant_word_mixed), then meets its x pair in
+// v_dot2_f32_bf16.  Rows are reduced with DPP (no LDS, no atomics, no workspace): every output
+// element is written once.
 //
 // Reference semantics: dequant-then-matmul of src/moss_tts/calibration.py:185-188 with
 // src/moss_tts/_runtime/calibrated_quant.py:41-42; paired epilogue rounding points of

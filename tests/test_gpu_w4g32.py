@@ -188,11 +188,11 @@ def _scale_sweep_weight():
 def test_exact_dequant_every_bf16_scale(dev):
     """The bit-exact dequant bf16_rne((q - z) * s) over all 16 x 16 (q, z) pairs and every positive
     finite bf16 scale, in the three places it is formed: the dequant kernel (plain fp32 product),
-    the decode GEMV's exact mode (one-hot activations select each column; v_dot2 block) and the
-    prefill GEMM's producer (identity activations give the whole matrix; same block).  The dequant
-    kernel must equal the oracle bit for bit everywhere.  The GEMV and GEMM form (128 + q) s in fp32,
-    finite below 2^120.8, so they are held to every scale below 2^120 (the bound the loaders enforce;
-    31,615 scales, subnormals included)."""
+    the decode GEMV's exact mode (one-hot activations select each column; the v_dot2 / v_fma_mix
+    block) and the prefill GEMM's producer (identity activations give the whole matrix; same
+    block).  The dequant kernel must equal the oracle bit for bit everywhere.  The GEMV and GEMM
+    form (128 + q) s in fp32, finite below 2^120.8, so they are held to every scale below 2^120 (the
+    bound the loaders enforce; 31,615 scales, subnormals included)."""
     from moss_tts._runtime import w4g32
 
     print("exact dequant over every positive finite bf16 scale", flush=True)
