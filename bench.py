@@ -211,11 +211,17 @@ def own_streaming_read_bench(torch, dev, nbytes: int):
         native.call("moss_stream_read", native.ptr(b), nbytes, native.ptr(sink), native.stream_of(b))
 
     sec = min(_per_launch(torch, [lambda b=b: launch(b) for b in copies], replays=20) for _ in range(3))
-    del copies
+    # the fixed cost of a launch in a graph: the same kernel on 16 bytes (one workgroup)
+    tiny = copies[0][:4]
+    floor = min(_per_launch(torch, [lambda: native.call("moss_stream_read", native.ptr(tiny), 16, native.ptr(sink),
+                                                        native.stream_of(tiny))], replays=20) for _ in range(3))
+    del copies, tiny
     torch.cuda.empty_cache()
     res = {"us_per_call": round(sec * 1e6, 3), "kernel": "moss_stream_read", "bytes": nbytes,
-           "frac_of_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4)}
-    _log(f"[bench] own streaming read of {nbytes} B: {res['us_per_call']} us per launch")
+           "frac_of_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "launch_floor_us_16_bytes": round(floor * 1e6, 3)}
+    _log(f"[bench] own streaming read of {nbytes} B: {res['us_per_call']} us per launch; of 16 B: "
+         f"{res['launch_floor_us_16_bytes']} us")
     return res
 
 
