@@ -653,12 +653,14 @@ int launch_gemv(const void* x, const void* qw, const void* sc, const void* zp, v
         if (mode == MOSS_DEQUANT_UNROUNDED) return launch_ksplit<PAIRED, false>(x, qw, sc, zp, y, G, n_out, rows, st);
         return (int)hipErrorInvalidValue;
     }
-    // measured on MI355X (K = 4096): 2 rows per wave is best for the exact mode in both roles up
-    // to N = 12288 and 4 for the 32-head output projection (N ~ 32800); the unrounded GEMV is as
-    // fast at 4 and the unrounded gate||up at 2
+    // measured on MI355X (K = 4096): 2 rows per wave is best for the exact mode in both roles and
+    // every N (N = 24576 / 32802: 12.3 / 15.3 us against 13.6 / 17.2 at 4), except the fused
+    // add-RMSNorm form of the 32-head output projection (N ~ 32800: 18.8 us at 4, 20.9 at 2); the
+    // unrounded GEMV is as fast at 4 and the unrounded gate||up at 2
     if (rows == 0)
-        rows = (G <= 128) ? ((PAIRED || mode == MOSS_DEQUANT_EXACT) ? (!PAIRED && n_out >= 24576 ? 4 : 2) : 4)
-                          : (G <= 256 ? 2 : 1);
+        rows = (G <= 128)
+                   ? ((PAIRED || mode == MOSS_DEQUANT_EXACT) ? (!PAIRED && NORM > 0 && n_out >= 24576 ? 4 : 2) : 4)
+                   : (G <= 256 ? 2 : 1);
     if (mode == MOSS_DEQUANT_EXACT)
         return launch_gemv_mode<PAIRED, true, NORM>(x, qw, sc, zp, y, G, n_out, rows, na, st);
     if (mode == MOSS_DEQUANT_UNROUNDED)
