@@ -221,8 +221,9 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
 
 // grid 32 query heads, 128 threads (one per dim).  The splits holding attended rows are
 // weighted by exp(lse - max lse) and summed in split order, with no LDS and no barrier.  The
-// first 64 splits' partials (L <= 4096) are loaded together with the lse values, so a typical
-// merge is one round trip.
+// first CHUNK splits' partials (CHUNK = 32 for L <= 2048, else 64: L <= 4096) are loaded together
+// with the lse values, so a typical merge is one round trip; the split order of the sum does not
+// depend on CHUNK.
 constexpr int kMergeChunk = 64;
 
 // QUANT: the merged bf16 row also leaves as int8 groups of 32 (4 per head; the groups of a
@@ -235,19 +236,20 @@ struct MergeQuant {
     int* __restrict__ qsum;
 };
 
-template <bool QUANT>
+template <bool QUANT, int CHUNK>
 __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict__ part,
                                                          const float* __restrict__ lse,
                                                          const int64_t* __restrict__ pos, uint16_t* __restrict__ out,
                                                          int L, int S, MergeQuant mq) {
+    static_assert(CHUNK <= kMergeChunk, "the first chunk's weights come from one lane each");
     const int hq = blockIdx.x, d = threadIdx.x, lane = d & (kWave - 1);
     // the partials and this lane's first lse value are loaded together with the position
     // (clamped into the workspace, branch-free) and masked once the position is known
     const int64_t p_raw = pos[0];
     const float* src = part + (size_t)hq * S * kHeadDim + d;
-    float v[kMergeChunk];
+    float v[CHUNK];
 #pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u) v[u] = src[(size_t)min(u, S - 1) * kHeadDim];
+    for (int u = 0; u < CHUNK; ++u) v[u] = src[(size_t)min(u, S - 1) * kHeadDim];
     const float lse0 = lse[hq * S + min(lane, S - 1)];
     const int p = (int)min(max(p_raw, (int64_t)0), (int64_t)(L - 1));
     const int active = p / kSplit + 1;
@@ -262,11 +264,15 @@ __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict
     const float wsum = wave_sum(ws);
     float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < kMergeChunk; ++u) {  // split order; split u's weight from lane u
+    for (int u = 0; u < CHUNK; ++u) {  // split order; split u's weight from lane u
         const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), u));
         if (u < active) acc = fmaf(wu, v[u], acc);
     }
-    for (int s = kMergeChunk; s < active; ++s) acc = fmaf(expf(lse[hq * S + s] - mx), src[(size_t)s * kHeadDim], acc);
+    for (int s = CHUNK; s < active; ++s) {  // splits 32 .. 63 (CHUNK 32 only) have their weight in lane s
+        const float ws_ = s < kWave ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), s))
+                                    : expf(lse[hq * S + s] - mx);
+        acc = fmaf(ws_, src[(size_t)s * kHeadDim], acc);
+    }
     const uint16_t o = f32_to_bf16(acc / wsum);
     out[hq * kHeadDim + d] = o;
     if constexpr (QUANT) {
@@ -281,6 +287,17 @@ __global__ __launch_bounds__(128) void decode_attn_merge(const float* __restrict
             mq.qsum[g] = total;
         }
     }
+}
+
+template <bool QUANT>
+void launch_merge(const float* part, const float* lse, const int64_t* pos, uint16_t* out, int L, int S,
+                  const MergeQuant& mq, hipStream_t st) {
+    if (S <= 32)
+        hipLaunchKernelGGL((decode_attn_merge<QUANT, 32>), dim3(kQHeads), dim3(kHeadDim), 0, st, part, lse, pos, out,
+                           L, S, mq);
+    else
+        hipLaunchKernelGGL((decode_attn_merge<QUANT, kMergeChunk>), dim3(kQHeads), dim3(kHeadDim), 0, st, part, lse,
+                           pos, out, L, S, mq);
 }
 
 // ids int64 [T, Q+1] (text token, then one code per codebook); grid (T, H / (256 VEC)): each
@@ -341,8 +358,8 @@ MOSS_API int moss_decode_attention(const void* q, const void* k_cache, const voi
     hipLaunchKernelGGL(decode_attn_split<false>, dim3(kKvHeads, S), dim3(256), 0, st, (const uint16_t*)q,
                        (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
                        (float*)lse, L, S, QkvArgs{});
-    hipLaunchKernelGGL(decode_attn_merge<false>, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
-                       (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S, MergeQuant{});
+    launch_merge<false>((const float*)partial, (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S,
+                        MergeQuant{}, st);
     return moss_launch_status();
 }
 
@@ -364,11 +381,11 @@ int attention_qkv(const void* qkv, const void* q_norm_w, const void* k_norm_w, c
                        (uint16_t*)k_cache, (uint16_t*)v_cache, (const int64_t*)position, (float*)partial,
                        (float*)lse, L, S, qa);
     if (mq)
-        hipLaunchKernelGGL(decode_attn_merge<true>, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
-                           (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S, *mq);
+        launch_merge<true>((const float*)partial, (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S,
+                           *mq, st);
     else
-        hipLaunchKernelGGL(decode_attn_merge<false>, dim3(kQHeads), dim3(kHeadDim), 0, st, (const float*)partial,
-                           (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S, MergeQuant{});
+        launch_merge<false>((const float*)partial, (const float*)lse, (const int64_t*)position, (uint16_t*)out, L, S,
+                            MergeQuant{}, st);
     return moss_launch_status();
 }
 
