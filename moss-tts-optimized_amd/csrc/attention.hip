@@ -24,8 +24,7 @@ constexpr int kMaxSplits = 512;             // L <= 32768
 // row l % 16, dims 8 (l / 16) .. + 7 of each 32-dim chunk) and its V rows one 256-byte row per
 // load (lane l: dims 2l, 2l + 1), all before any arithmetic, straight into registers.  The scores
 // of the 4 query heads are 4 MFMAs (B: the heads' q, columns 4..15 zero); the wave's softmax over
-// its 16 rows and its P.V (fp32, each probability read from the lane that holds it with
-// v_readlane) need no barrier and no LDS; the 4 waves' (max, sum, P.V) meet once in LDS,
+// its 16 rows and its P.V (fp32) need no barrier; the 4 waves' (max, sum, P.V) meet once in LDS,
 // rescaled to the split's max.  Each split writes its normalized partial output and log-sum-exp;
 // splits after the position write nothing.
 //
@@ -54,6 +53,7 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
                                                          float* __restrict__ lse, int L, int S, QkvArgs qa) {
     __shared__ __attribute__((aligned(16))) uint16_t qb[kGroup][kHeadDim];  // the 4 query heads, bf16
     __shared__ __attribute__((aligned(16))) uint16_t newkv[2][kHeadDim];     // owner: the new K and V rows
+    __shared__ __attribute__((aligned(16))) float pw[4][kGroup][kWaveRows];  // per wave: P[head][row]
     __shared__ __attribute__((aligned(16))) float ow[4][kGroup][kHeadDim];   // per wave: unnormalized P.V
     __shared__ float mw[4][kGroup], lw[4][kGroup];
     const int hk = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
@@ -174,12 +174,12 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
+    if (hd < kGroup) *reinterpret_cast<float4*>(&pw[w][hd][4 * (l >> 4)]) = make_float4(e[0], e[1], e[2], e[3]);
     if (l < kGroup) {
         mw[w][l] = m;
         lw[w][l] = sum;
     }
-    // P.V of the wave's rows: lane l, dims 2l, 2l + 1.  P of head h, row 4 r4 + i is e[i] of lane
-    // h + 16 r4, read straight from that lane (no LDS round trip)
+    // P.V of the wave's rows (the wave reads back what it wrote: no barrier): lane l, dims 2l, 2l + 1
     float o[kGroup][2];
 #pragma unroll
     for (int h = 0; h < kGroup; ++h) {
@@ -187,11 +187,12 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
         o[h][1] = 0.f;
 #pragma unroll
         for (int r4 = 0; r4 < kWaveRows / 4; ++r4) {
+            const float4 pe = *reinterpret_cast<const float4*>(&pw[w][h][4 * r4]);
+            const float pv[4] = {pe.x, pe.y, pe.z, pe.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i]), h + 16 * r4));
-                o[h][0] = fmaf(pv, bf16_lo(vv[4 * r4 + i]), o[h][0]);
-                o[h][1] = fmaf(pv, bf16_hi(vv[4 * r4 + i]), o[h][1]);
+                o[h][0] = fmaf(pv[i], bf16_lo(vv[4 * r4 + i]), o[h][0]);
+                o[h][1] = fmaf(pv[i], bf16_hi(vv[4 * r4 + i]), o[h][1]);
             }
         }
         *reinterpret_cast<float2*>(&ow[w][h][2 * l]) = make_float2(o[h][0], o[h][1]);
