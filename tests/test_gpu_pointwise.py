@@ -88,7 +88,7 @@ def test_silu_mul(dev, rows, n):
 
 
 @pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (128, 127),
-                                        (32768, 20000)])
+                                        (2560, 2500), (4096, 4095), (32768, 20000)])
 def test_decode_attention(dev, L, position):
     """Split-softmax GQA decode attention vs the oracle's exact fp32 softmax; bf16 output."""
     from moss_tts._runtime import attention
@@ -141,7 +141,8 @@ def test_decode_attention_rejects_unaligned_length(dev):
         attention.decode_attention(q, kc, kc.clone(), torch.zeros(1, device=dev, dtype=torch.int64))
 
 
-@pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (128, 5)])
+@pytest.mark.parametrize("L,position", [(2048, 2047), (2048, 0), (2048, 1000), (1024, 63), (1024, 64), (128, 5),
+                                        (4096, 3000)])
 def test_fused_qkv_attention_equals_rope_then_attention(dev, L, position):
     """q/k-norm + RoPE + KV write fused into the attention kernel reproduces moss_qk_norm_rope_kv
     followed by moss_decode_attention bit for bit, output and both caches."""
