@@ -67,9 +67,9 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
     const int r0 = t0 + kWaveRows * w;            // this wave's first row
     const bool live = r0 <= p;                    // wave-uniform: the wave holds attended rows
 
-    // Loads, in this order: the q path's (L2 hits; the new K and V rows are loaded by every
-    // workgroup, branch-free, and used by the owner only), then the wave's K and V rows.
-    // Completions are counted in order, so the head norm + RoPE runs while the rows arrive.
+    // Loads, in this order: the q path's (L2 hits; the new K and V rows only by the owner's waves
+    // 0 and 1, which form them), then the wave's K and V rows.  Completions are counted in order,
+    // so the head norm + RoPE runs while the rows arrive.
     constexpr int D = kHeadDim;
     uint16_t qx0 = 0, qx1 = 0, qw0 = 0, qw1 = 0, cs0 = 0, cs1 = 0, sn0 = 0, sn1 = 0;
     uint16_t kx0 = 0, kx1 = 0, kw0 = 0, kw1 = 0, vx0 = 0, vx1 = 0;
@@ -85,9 +85,13 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
         qw0 = qa.qnw[l]; qw1 = qa.qnw[l + 64];
         cs0 = cr[l]; cs1 = cr[l + 64];
         sn0 = sr[l]; sn1 = sr[l + 64];
-        kx0 = kh[l]; kx1 = kh[l + 64];
-        kw0 = qa.knw[l]; kw1 = qa.knw[l + 64];
-        vx0 = vh[l]; vx1 = vh[l + 64];
+        if (owner && w == 0) {
+            kx0 = kh[l]; kx1 = kh[l + 64];
+            kw0 = qa.knw[l]; kw1 = qa.knw[l + 64];
+        }
+        if (owner && w == 1) {
+            vx0 = vh[l]; vx1 = vh[l + 64];
+        }
     } else {
         qpair = reinterpret_cast<const uint32_t*>(q + (size_t)hk * kGroup * kHeadDim)[tid];
     }
