@@ -144,17 +144,28 @@ __device__ __forceinline__ int quantize8_dot4(const float* v, float inv, uint32_
 // Byte offset, within its 8-value block, of value t in dot4 order.
 __device__ __forceinline__ int dot4_slot(int t) { return ((t & 3) << 1) | (t >> 2); }
 
-// Max / sum over each 32-lane half of a wave (a group of 32 values, one per lane).
+// Max / sum over each 32-lane half of a wave (a group of 32 values, one per lane): the 16-lane
+// rows with DPP moves, then one exchange between the two rows of each half.  Both are exact
+// (max, integer sum), so the order of the combination does not matter.
 __device__ __forceinline__ float half_wave_max(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 32));
-    return v;
+    v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror: every lane holds its row's max
+    return fmaxf(v, __shfl_xor(v, 16, 32));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_move_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
 }
 
 __device__ __forceinline__ int half_wave_sum(int v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 32);
-    return v;
+    v += dpp_move_i<0xB1>(v);
+    v += dpp_move_i<0x4E>(v);
+    v += dpp_move_i<0x141>(v);
+    v += dpp_move_i<0x140>(v);
+    return v + __shfl_xor(v, 16, 32);
 }
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
