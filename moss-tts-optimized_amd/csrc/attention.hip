@@ -168,16 +168,14 @@ __global__ __launch_bounds__(256) void decode_attn_split(const uint16_t* __restr
         sv[i] = t <= p ? sc[i] * kScale : -INFINITY;
         m = fmaxf(m, sv[i]);
     }
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
+    m = max_xor32(max_xor16(m));
     float e[4], sum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         e[i] = live ? expf(sv[i] - m) : 0.f;  // a live wave's max is finite (row r0 <= p)
         sum += e[i];
     }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
+    sum = sum_xor32(sum_xor16(sum));
     if (hd < kGroup) *reinterpret_cast<float4*>(&pw[w][hd][4 * (l >> 4)]) = make_float4(e[0], e[1], e[2], e[3]);
     if (l < kGroup) {
         mw[w][l] = m;

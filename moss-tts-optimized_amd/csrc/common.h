@@ -144,6 +144,31 @@ __device__ __forceinline__ int quantize8_dot4(const float* v, float inv, uint32_
 // Byte offset, within its 8-value block, of value t in dot4 order.
 __device__ __forceinline__ int dot4_slot(int t) { return ((t & 3) << 1) | (t >> 2); }
 
+// v combined with its lane l ^ 16 / l ^ 32 partner (gfx950 v_permlane16_swap / v_permlane32_swap
+// of v with itself: the two results hold, in every lane, the lane's own value and its partner's,
+// in an order that depends on the lane; max and + are commutative, so every lane gets the same
+// bits as from an exchange through LDS).
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ int isum_xor16(int v) {
+    const auto p = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)p[0] + (int)p[1];
+}
+
 // Max / sum over each 32-lane half of a wave (a group of 32 values, one per lane): the 16-lane
 // rows with DPP moves, then one exchange between the two rows of each half.  Both are exact
 // (max, integer sum), so the order of the combination does not matter.
@@ -152,7 +177,7 @@ __device__ __forceinline__ float half_wave_max(float v) {
     v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]
     v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
     v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror: every lane holds its row's max
-    return fmaxf(v, __shfl_xor(v, 16, 32));
+    return max_xor16(v);
 }
 
 template <int CTRL>
@@ -165,7 +190,7 @@ __device__ __forceinline__ int half_wave_sum(int v) {
     v += dpp_move_i<0x4E>(v);
     v += dpp_move_i<0x141>(v);
     v += dpp_move_i<0x140>(v);
-    return v + __shfl_xor(v, 16, 32);
+    return isum_xor16(v);
 }
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
