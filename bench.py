@@ -15,7 +15,9 @@ The JSON line also carries:
                 ``traffic`` comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in
                 profiles/ when present
   cpu_baseline  the oracle's torch-CPU dequant-then-matmul of the same MLP step on this host
-  extra         the K=4096 N=12288 GEMV alone (GB/s, us/call, fraction of peak)
+  extra         the K=4096 N=12288 GEMV alone (GB/s, us/call, fraction of peak) beside a streaming
+                read of the same bytes; the exact GEMV and the read over N = 12288 .. 98304; the
+                decode step, the prompt pass, FP8, small-M, bf16-head and pointwise lines
 """
 from __future__ import annotations
 
@@ -223,6 +225,34 @@ def own_streaming_read_bench(torch, dev, nbytes: int):
     _log(f"[bench] own streaming read of {nbytes} B: {res['us_per_call']} us per launch; of 16 B: "
          f"{res['launch_floor_us_16_bytes']} us")
     return res
+
+
+def gemv_size_sweep(torch, dev, sizes=(12288, 24576, 49152, 98304)):
+    """The exact INT4-G32 GEMV at K=4096 over N in ``sizes`` against the library's streaming read of
+    the same bytes, each per launch in a HIP graph over >= 512 MiB of distinct copies: how the
+    fraction of HBM peak that one launch reaches grows as its fixed costs (the dispatch and the
+    first loads' latency) spread over more bytes."""
+    from moss_tts._runtime import pointwise, w4g32
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    x = pointwise.rmsnorm(torch.randn((1, HIDDEN), generator=gen, device=dev).bfloat16(),
+                          torch.ones(HIDDEN, device=dev, dtype=torch.bfloat16), 1e-6)
+    out = {}
+    for n in sizes:
+        nbytes = gemv_bytes(HIDDEN, n)
+        copies = [_quantized(torch, w4g32, n, HIDDEN, gen, dev) for _ in range(max(2, -(-(512 << 20) // nbytes)))]
+        sec = min(_per_launch(torch, [lambda w=w: w4g32.gemv(x, w) for w in copies], replays=20) for _ in range(3))
+        del copies
+        torch.cuda.empty_cache()
+        rd = own_streaming_read_bench(torch, dev, nbytes)
+        out[f"n{n}"] = {"bytes": nbytes, "gemv_us": round(sec * 1e6, 3),
+                        "gemv_frac_of_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+                        "read_us": rd["us_per_call"], "read_frac_of_peak": rd["frac_of_peak"],
+                        "gemv_time_over_read_time": round(sec * 1e6 / rd["us_per_call"], 4)}
+        _log(f"[bench] GEMV K=4096 N={n}: {sec * 1e6:.2f} us ({out[f'n{n}']['gemv_frac_of_peak']:.1%}), "
+             f"read of the same bytes {rd['us_per_call']} us ({rd['frac_of_peak']:.1%})")
+    return out
 
 
 def fp8_bench(torch, dev):
@@ -903,6 +933,7 @@ def main() -> int:
     read["gemv_time_over_read_time"] = round(ns_s * 1e6 / read["us_per_call"], 4)
     own_read = own_streaming_read_bench(torch, dev, ns_bytes)
     own_read["gemv_time_over_read_time"] = round(ns_s * 1e6 / own_read["us_per_call"], 4)
+    size_sweep = gemv_size_sweep(torch, dev) if not args.no_extras else None
     fp8_lines = fp8_bench(torch, dev) if not args.no_extras else None
     small_m = small_m_bench(torch, dev) if not args.no_extras else None
     heads_bf16 = bf16_heads_bench(torch, dev) if not args.no_extras else None
@@ -964,6 +995,7 @@ def main() -> int:
                                   "frac_of_peak": round(ns_gbs / HBM_PEAK_GBS, 4), "bytes": ns_bytes,
                                   "dequant": "exact", "vendor_streaming_read_same_bytes": read,
                                   "streaming_read_same_bytes": own_read},
+            "gemv_k4096_size_sweep": size_sweep,
             "gemv_k4096_n12288_unrounded": {"us_per_call": round(ns_unr_s * 1e6, 3),
                                             "GB/s": round(ns_bytes / ns_unr_s / 1e9, 1),
                                             "frac_of_peak": round(ns_bytes / ns_unr_s / 1e9 / HBM_PEAK_GBS, 4)},
