@@ -79,26 +79,29 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Full 64-lane sum, wave-uniform result.  Fixed order, so results are deterministic.
+// Full 64-lane sum, the same value in every lane.  Fixed order, so results are deterministic:
+// the 16-lane row sums r0..r3, then (r0 + r1) + (r2 + r3).  v_permlane16_swap(x, x) hands every
+// lane the row sums of its own and its neighbouring row (r0 | r1 in rows 0 and 1, r2 | r3 in rows
+// 2 and 3) and v_permlane32_swap(x, x) the two halves' results; being commutative, + and max give
+// the same bits in every lane, without the readlanes and their SGPR hazards.
 __device__ __forceinline__ float wave_sum(float v) {
     v = row16_sum(v);
-    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (a + b) + (c + d);
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// Full 64-lane maximum, the same value in every lane (the row maxima combined as in wave_sum).
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_move<0xB1>(v));
     v = fmaxf(v, dpp_move<0x4E>(v));
     v = fmaxf(v, dpp_move<0x141>(v));
     v = fmaxf(v, dpp_move<0x140>(v));
-    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
 // Max and sum over the 4 lanes of each DPP quad; every lane of the quad receives the result.
