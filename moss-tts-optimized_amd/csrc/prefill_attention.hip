@@ -184,7 +184,7 @@ __global__ __launch_bounds__(64 * HPW * KS, 1) void prefill_attention_kernel(
                 s[e] = v;
                 bmax = fmaxf(bmax, v);
             }
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            bmax = max_xor32(bmax);  // the other 32-lane half's keys of the same query rows
             const float mn = fmaxf(m, bmax);
             const float mr = mn == -INFINITY ? 0.f : mn;  // no key of this wave visible yet: nothing changes
             const float alpha = __builtin_amdgcn_exp2f(m - mr);
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(64 * HPW * KS, 1) void prefill_attention_kernel(
                     bsum += p;
                     pf[u][v] = (__bf16)p;
                 }
-            bsum += __shfl_xor(bsum, 32);
+            bsum = sum_xor32(bsum);
             l = l * alpha + bsum;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
