@@ -44,7 +44,7 @@ template <int NORM, int CH>
 __device__ __forceinline__ void norm_into_lds(const NormLoad<CH>& nl, const NormArgs& na, uint16_t* xn, float* red,
                                               int K) {
     const int t = threadIdx.x;
-    float v[CH][8];
+    uint32_t pk[CH][4];  // the row as packed bf16 pairs between the two phases (8 VGPRs, not 16)
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -62,10 +62,10 @@ __device__ __forceinline__ void norm_into_lds(const NormLoad<CH>& nl, const Norm
         }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            v[c][2 * p] = bf16_lo(sw[p]);
-            v[c][2 * p + 1] = bf16_hi(sw[p]);
-            ss = fmaf(v[c][2 * p], v[c][2 * p], ss);
-            ss = fmaf(v[c][2 * p + 1], v[c][2 * p + 1], ss);
+            pk[c][p] = sw[p];
+            const float lo = bf16_lo(sw[p]), hi = bf16_hi(sw[p]);
+            ss = fmaf(lo, lo, ss);
+            ss = fmaf(hi, hi, ss);
         }
     }
     ss = wave_sum(ss);
@@ -79,8 +79,8 @@ __device__ __forceinline__ void norm_into_lds(const NormLoad<CH>& nl, const Norm
         uint32_t o[4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const float a = round_bf16(v[c][2 * p] * inv) * bf16_lo(wv[p]);
-            const float b = round_bf16(v[c][2 * p + 1] * inv) * bf16_hi(wv[p]);
+            const float a = round_bf16(bf16_lo(pk[c][p]) * inv) * bf16_lo(wv[p]);
+            const float b = round_bf16(bf16_hi(pk[c][p]) * inv) * bf16_hi(wv[p]);
             o[p] = pack_bf16x2(a, b);
         }
         reinterpret_cast<uint4*>(xn)[ci] = make_uint4(o[0], o[1], o[2], o[3]);

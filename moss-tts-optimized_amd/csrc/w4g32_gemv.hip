@@ -161,6 +161,41 @@ __device__ __forceinline__ float row_partial_exact(const XSlice<KG>& xs, const R
     return acc;
 }
 
+// The exact form over the normalized row in LDS (the fused-norm kernels), group by group: the
+// lane's x group j (16 packed pairs) is read once for all rows, then group j + 1, so one group of
+// x is held at a time (16 VGPRs instead of 16 KG: the gate||up kernel fits 5 waves per SIMD
+// instead of 4).  Every row's chain visits its words in row_partial_exact's order, so the sums
+// are bit-identical to it.  NORM > 0 means G = 64 KG: every group of every lane exists.
+template <int KG, int NR>
+__device__ __forceinline__ void rows_exact_from_lds(const uint16_t* xn, const RowLoad<KG> (&rows)[NR], int lane,
+                                                    float (&acc)[NR]) {
+    const MixedUnpack c = make_mixed_unpack();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        uint32_t xv[16];
+        const uint4* p = reinterpret_cast<const uint4*>(xn + 32 * (lane + kWave * j));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = p[q];
+            xv[4 * q] = v.x;
+            xv[4 * q + 1] = v.y;
+            xv[4 * q + 2] = v.z;
+            xv[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const GroupDequant gd = group_dequant(rows[r].s[j], rows[r].z[j]);
+            acc[r] = word_dot_exact(rows[r].w[j].x, &xv[0], acc[r], c, gd);
+            acc[r] = word_dot_exact(rows[r].w[j].y, &xv[4], acc[r], c, gd);
+            acc[r] = word_dot_exact(rows[r].w[j].z, &xv[8], acc[r], c, gd);
+            acc[r] = word_dot_exact(rows[r].w[j].w, &xv[12], acc[r], c, gd);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the next group's LDS reads stay after these products
+    }
+}
+
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Non-temporal loads: every weight byte is read once.
@@ -228,24 +263,31 @@ __device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ x, const 
         const int n = min(row0 + local, n_out - 1) + ((PAIRED && r >= R) ? n_out : 0);
         load_row_nt<KG, FULL>(rows[r], qw, sc, zp, n, lane, G);
     }
+    float out[NR];
     if constexpr (NORM > 0) {
         __shared__ __attribute__((aligned(16))) uint16_t xn[2048 * KG];
         __shared__ float red[4];
         norm_into_lds<NORM, KG>(nl, na, xn, red, 32 * G);
         if (row0 >= n_out) return;  // after the workgroup's barriers
-        load_x<KG, !EXACT, FULL>(xs, xn, lane, G);
-    }
-
-    float out[NR];
-    if constexpr (EXACT) {
+        if constexpr (EXACT) {
+            rows_exact_from_lds<KG, NR>(xn, rows, lane, out);
+        } else {
+            load_x<KG, true, FULL>(xs, xn, lane, G);
+            const Magic m = make_magic();
+#pragma unroll
+            for (int r = 0; r < NR; ++r) out[r] = row_partial_unrounded(xs, rows[r], m);
+        }
+    } else if constexpr (EXACT) {
         const MixedUnpack c = make_mixed_unpack();
 #pragma unroll
-        for (int r = 0; r < NR; ++r) out[r] = wave_sum(row_partial_exact(xs, rows[r], c));
+        for (int r = 0; r < NR; ++r) out[r] = row_partial_exact(xs, rows[r], c);
     } else {
         const Magic m = make_magic();
 #pragma unroll
-        for (int r = 0; r < NR; ++r) out[r] = wave_sum(row_partial_unrounded(xs, rows[r], m));
+        for (int r = 0; r < NR; ++r) out[r] = row_partial_unrounded(xs, rows[r], m);
     }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) out[r] = wave_sum(out[r]);
 
     if (lane == 0) {
 #pragma unroll
